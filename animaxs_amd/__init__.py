@@ -1,0 +1,18 @@
+"""animaxs_amd: MI355X-native (gfx950) attention + quantized-linear hot path of AnimaXS.
+
+The product is ``libanima_hip.so`` (C ABI in ``include/anima_hip.h``, HIP kernels in
+``csrc/``).  This package builds it in-tree (``animaxs_amd.build``) and mirrors the
+reference's Swift operator surface in Python over that ABI (``executors``).
+"""
+
+from ._abi import AnimaError, LIB_PATH, load  # noqa: F401
+from .executors import (  # noqa: F401
+    AttentionExecutor, BlockOps, Context, DiTBlockExecutor, DitRoPE, LinearExecutor, QKPrologue,
+    QuantDecoders, QuantizedLinearWeightBuffers, as_buffer, qwen_rope,
+)
+
+__all__ = [
+    "AnimaError", "LIB_PATH", "load", "AttentionExecutor", "BlockOps", "Context", "DiTBlockExecutor",
+    "DitRoPE", "LinearExecutor", "QKPrologue", "QuantDecoders", "QuantizedLinearWeightBuffers",
+    "as_buffer", "qwen_rope",
+]

@@ -1,0 +1,243 @@
+// extern "C" entry points of libanima_hip (include/anima_hip.h).  Each converts
+// exceptions into an anima_status and the thread-local last-error message; no
+// entry point launches anything before its arguments validate.
+#include <string>
+
+#include "attention.hpp"
+#include "block.hpp"
+#include "context.hpp"
+#include "linear.hpp"
+
+namespace anima {
+
+static thread_local std::string g_last_error;
+
+void set_last_error(const char* msg) { g_last_error = msg ? msg : ""; }
+
+template <class T>
+static T* require(T* p, const char* what) {
+  if (!p) fail(ANIMA_E_INVALID_ARGUMENT, std::string(what) + " handle is null");
+  return p;
+}
+
+}  // namespace anima
+
+using namespace anima;
+
+extern "C" {
+
+const char* anima_last_error(void) { return g_last_error.c_str(); }
+
+int32_t anima_abi_version(void) { return ANIMA_HIP_ABI_VERSION; }
+
+// ---------------------------------------------------------------- context
+anima_status anima_ctx_create(int32_t device, anima_ctx** out) {
+  return guarded([&] {
+    require(out, "context output");
+    *out = nullptr;
+    // The device is bound lazily: nothing touches HIP until the first launch,
+    // so validation works (and is tested) on hosts without a GPU.
+    if (device < 0) fail(ANIMA_E_INVALID_ARGUMENT, "HIP device index must be >= 0");
+    anima_ctx* c = new anima_ctx();
+    c->device = device;
+    c->stream = nullptr;
+    *out = c;
+  });
+}
+
+anima_status anima_ctx_destroy(anima_ctx* ctx) {
+  return guarded([&] { delete ctx; });
+}
+
+anima_status anima_ctx_set_stream(anima_ctx* ctx, void* hip_stream) {
+  return guarded([&] { require(ctx, "context")->stream = static_cast<hipStream_t>(hip_stream); });
+}
+
+anima_status anima_ctx_synchronize(anima_ctx* ctx) {
+  return guarded([&] {
+    require(ctx, "context");
+    DeviceGuard g(ctx);
+    ANIMA_HIP(hipStreamSynchronize(ctx->stream));
+  });
+}
+
+// ---------------------------------------------------------------- attention
+anima_status anima_attention_create(anima_ctx* ctx, const anima_attention_config* cfg, anima_attention** out) {
+  return guarded([&] {
+    require(out, "attention output");
+    *out = nullptr;
+    require(ctx, "context");
+    require(cfg, "attention config");
+    *out = new anima_attention(ctx, *cfg);
+  });
+}
+
+anima_status anima_attention_destroy(anima_attention* attn) {
+  return guarded([&] {
+    delete attn;  // hipFree needs no current-device switch
+  });
+}
+
+anima_status anima_attention_encode(anima_attention* attn, const anima_attention_args* args) {
+  return guarded([&] { require(attn, "attention")->impl.encode(*require(args, "attention args")); });
+}
+
+anima_status anima_attention_execute(anima_attention* attn, const anima_attention_args* args) {
+  return guarded([&] {
+    require(attn, "attention")->impl.encode(*require(args, "attention args"));
+    DeviceGuard g(attn->impl.context());
+    ANIMA_HIP(hipStreamSynchronize(attn->impl.context()->stream));
+  });
+}
+
+anima_status anima_attention_max_score_scratch_bytes(anima_attention* attn, int64_t key_count, int64_t query_count,
+                                                     int64_t* out_bytes) {
+  return guarded([&] {
+    *require(out_bytes, "output") = require(attn, "attention")->impl.maximum_score_scratch_bytes(key_count, query_count);
+  });
+}
+
+anima_status anima_attention_workspace_bytes(anima_attention* attn, int64_t* out_bytes) {
+  return guarded([&] { *require(out_bytes, "output") = require(attn, "attention")->impl.workspace_bytes(); });
+}
+
+// ---------------------------------------------------------------- linear
+anima_status anima_linear_create(anima_ctx* ctx, const anima_linear_config* cfg, anima_linear** out) {
+  return guarded([&] {
+    require(out, "linear output");
+    *out = nullptr;
+    require(ctx, "context");
+    require(cfg, "linear config");
+    *out = new anima_linear(ctx, *cfg);
+  });
+}
+
+anima_status anima_linear_destroy(anima_linear* lin) {
+  return guarded([&] {
+    delete lin;
+  });
+}
+
+anima_status anima_linear_encode(anima_linear* lin, anima_buffer input, int64_t input_offset,
+                                 const anima_qweight* weight, anima_buffer output, int64_t output_offset,
+                                 int64_t input_rows, int32_t family) {
+  return guarded([&] {
+    require(lin, "linear")->impl.encode(input, input_offset, *require(weight, "weight"), output, output_offset,
+                                        input_rows, family);
+  });
+}
+
+anima_status anima_linear_execute(anima_linear* lin, anima_buffer input, int64_t input_offset,
+                                  const anima_qweight* weight, anima_buffer output, int64_t output_offset,
+                                  int64_t input_rows, int32_t family) {
+  return guarded([&] {
+    require(lin, "linear")->impl.encode(input, input_offset, *require(weight, "weight"), output, output_offset,
+                                        input_rows, family);
+    DeviceGuard g(lin->impl.context());
+    ANIMA_HIP(hipStreamSynchronize(lin->impl.context()->stream));
+  });
+}
+
+anima_status anima_matvec_encode(anima_ctx* ctx, const anima_qweight* weight, anima_buffer input_f32,
+                                 int64_t input_offset, anima_buffer output_f32, int64_t output_offset) {
+  return guarded([&] {
+    encode_matvec(require(ctx, "context"), *require(weight, "weight"), input_f32, input_offset, output_f32,
+                  output_offset);
+  });
+}
+
+anima_status anima_dequant_to_half_encode(anima_ctx* ctx, const anima_qweight* weight, anima_buffer output,
+                                          int64_t output_offset, int64_t out_row_stride) {
+  return guarded([&] {
+    encode_dequant(require(ctx, "context"), *require(weight, "weight"), output, output_offset, out_row_stride);
+  });
+}
+
+// ---------------------------------------------------------------- DiT block support kernels
+static void check_elementwise(const anima_buffer& b, int64_t count, int64_t elem, const char* what) {
+  if (count < 0) fail(ANIMA_E_INVALID_SHAPE, std::string(what) + " count must be >= 0");
+  if (checked_product({count, elem}, what) > b.length) fail(ANIMA_E_OUT_OF_BOUNDS, std::string(what) + " buffer range is out of bounds");
+  if (count > 0 && !b.ptr) fail(ANIMA_E_INVALID_ARGUMENT, std::string(what) + " buffer pointer is null");
+}
+
+anima_status anima_layernorm_modulate_to_half_encode(anima_ctx* ctx, anima_buffer residual, anima_buffer modulation,
+                                                     anima_buffer output, int64_t n, int64_t rows, float eps,
+                                                     int64_t modulation_offset) {
+  return guarded([&] {
+    require(ctx, "context");
+    if (n <= 0 || rows <= 0 || modulation_offset < 0) fail(ANIMA_E_INVALID_SHAPE, "invalid layernorm-modulate shape");
+    check_elementwise(residual, checked_product({rows, n}, "layernorm"), 4, "layernorm residual");
+    check_elementwise(output, checked_product({rows, n}, "layernorm"), 2, "layernorm output");
+    check_elementwise(modulation, std::max(n, checked_end(modulation_offset, n, "layernorm")), 4, "layernorm modulation");
+    DeviceGuard g(ctx);
+    launch_layernorm_modulate(static_cast<const float*>(residual.ptr), static_cast<const float*>(modulation.ptr),
+                              static_cast<half_t*>(output.ptr), n, rows, eps, modulation_offset, ctx->stream);
+  });
+}
+
+anima_status anima_gate_add_half_f32_encode(anima_ctx* ctx, anima_buffer residual, anima_buffer branch,
+                                            anima_buffer gate, int64_t n, int64_t count) {
+  return guarded([&] {
+    require(ctx, "context");
+    if (n <= 0) fail(ANIMA_E_INVALID_SHAPE, "gate width must be positive");
+    check_elementwise(residual, count, 4, "gate_add residual");
+    check_elementwise(branch, count, 2, "gate_add branch");
+    check_elementwise(gate, n, 4, "gate_add gate");
+    if (count == 0) return;
+    DeviceGuard g(ctx);
+    launch_gate_add(static_cast<float*>(residual.ptr), static_cast<const half_t*>(branch.ptr),
+                    static_cast<const float*>(gate.ptr), n, count, ctx->stream);
+  });
+}
+
+anima_status anima_gelu_half_inplace_encode(anima_ctx* ctx, anima_buffer values, int64_t count) {
+  return guarded([&] {
+    require(ctx, "context");
+    check_elementwise(values, count, 2, "gelu");
+    if (count == 0) return;
+    DeviceGuard g(ctx);
+    launch_gelu(static_cast<half_t*>(values.ptr), count, ctx->stream);
+  });
+}
+
+anima_status anima_silu_f32_encode(anima_ctx* ctx, anima_buffer input, anima_buffer output, int64_t count) {
+  return guarded([&] {
+    require(ctx, "context");
+    check_elementwise(input, count, 4, "silu input");
+    check_elementwise(output, count, 4, "silu output");
+    if (count == 0) return;
+    DeviceGuard g(ctx);
+    launch_silu(static_cast<const float*>(input.ptr), static_cast<float*>(output.ptr), count, ctx->stream);
+  });
+}
+
+anima_status anima_add_f32_encode(anima_ctx* ctx, anima_buffer destination, anima_buffer source, int64_t count) {
+  return guarded([&] {
+    require(ctx, "context");
+    check_elementwise(destination, count, 4, "add destination");
+    check_elementwise(source, count, 4, "add source");
+    if (count == 0) return;
+    DeviceGuard g(ctx);
+    launch_add(static_cast<float*>(destination.ptr), static_cast<const float*>(source.ptr), count, ctx->stream);
+  });
+}
+
+// ---------------------------------------------------------------- DiT block
+anima_status anima_dit_block_create(anima_ctx* ctx, anima_dit_block** out) {
+  return guarded([&] {
+    require(out, "block output");
+    *out = nullptr;
+    *out = new anima_dit_block(require(ctx, "context"));
+  });
+}
+
+anima_status anima_dit_block_destroy(anima_dit_block* blk) {
+  return guarded([&] { delete blk; });
+}
+
+anima_status anima_dit_block_encode(anima_dit_block* blk, const anima_dit_block_weights* w,
+                                    const anima_dit_block_args* args) {
+  return guarded([&] { require(blk, "block")->impl.encode(*require(w, "block weights"), *require(args, "block args")); });
+}
+
+}  // extern "C"

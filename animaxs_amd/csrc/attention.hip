@@ -1,0 +1,451 @@
+// Attention for gfx950: MFMA flash kernel (head_dim 64/128), generic fp32 kernel
+// (any head_dim <= 512) and the per-head RMSNorm + split-half RoPE prologue.
+//
+// Replaces the reference's AttentionExecutor backends
+// (AnimaXS/Runtime/Metal/AttentionExecutor.swift:122-733) and the Metal kernels
+// attention_softmax_rows, attention_*_f32, streaming_*, dit_flash_attention_h128_*,
+// rms_rope_split_half and rmsnorm_heads_half (AnimaXS/Shaders/AnimaKernels.metal:
+// 660-729, 1051-1185, 2069-2427).  Maths: O = softmax(scale * Q K^T + mask) V per
+// head, kv head = h / (heads / kv_heads) (AttentionExecutor.swift:222).
+#include <cmath>
+#include <vector>
+
+#include "attention.hpp"
+
+namespace anima {
+
+// ===========================================================================
+// Flash kernel.
+//
+// One workgroup = 4 waves = 128 query rows of one (batch, head); each wave owns
+// 32 rows.  Per 64-key tile a wave computes S^T = K Q^T with two 32x32 tiles of
+// v_mfma_f32_32x32x16_f16 (keys on M, queries on N), so every lane holds 32
+// scores of ONE query row (lane%32) and the row max needs a single exchange with
+// lane^32.  P^T stays in registers and is the B operand of O^T += V^T P^T: the
+// C-operand layout of S^T maps register j of lane (n, h) to key
+// 32t + 8(j/4) + 4h + j%4, which is a valid K-slot order for the next MFMA as
+// long as the A operand (V^T, read from a transposed LDS tile) uses the same key
+// permutation.  Online softmax in base 2 with the scale folded into one FMA; the
+// running max is only raised when it grows by more than 2^8 (P stays <= 256,
+// exact maths, far fewer O rescales).  K/V tiles are double-buffered in LDS with
+// XOR swizzles, the next tile's global loads are issued before the current
+// tile's MFMAs.
+// ===========================================================================
+constexpr int FA_BM = 128;
+constexpr int FA_BN = 64;
+constexpr int FA_NT = 256;
+constexpr float FA_RESCALE_THRESHOLD = 8.0f;
+
+__device__ __forceinline__ int vt_swz(int d) { return ((d & 15) + (d >> 4)) & 15; }
+
+template <int D>
+__global__ __launch_bounds__(FA_NT, 2) void flash_attention_kernel(FlashParams p) {
+  constexpr int DCH = D / 8;                       // 16-byte chunks per K row
+  constexpr int QS = D / 16;                       // k-steps of S^T = K Q^T
+  constexpr int OB = D / 32;                       // 32-row blocks of O^T
+  constexpr int KQ = FA_BN / 4;                    // key quads per tile
+  constexpr int KLOADS = (FA_BN * DCH) / FA_NT;    // 16-byte K loads per thread
+  constexpr int VBLOCKS = KQ * DCH;                // 4x8 V blocks per tile
+  static_assert(KLOADS >= 1 && VBLOCKS <= FA_NT, "tile shape");
+
+  __shared__ __attribute__((aligned(16))) half_t Ks[2][FA_BN * D];
+  __shared__ __attribute__((aligned(16))) half_t Vt[2][D * FA_BN];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int c32 = lane & 31, hh = lane >> 5;
+
+  int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int qt = lb % p.q_tiles;
+  lb /= p.q_tiles;
+  const int head = lb % p.H;
+  const int b = lb / p.H;
+  const int kvh = head / p.group;
+  const int q0 = qt * FA_BM;
+  const int qi = q0 + wave * 32 + c32;
+  const int wave_row0 = q0 + wave * 32;
+
+  int kv_len = p.Sk;
+  if (p.key_lengths_dev) {
+    int L = p.key_lengths_dev[b];
+    kv_len = L < 1 ? 1 : (L > p.Sk ? p.Sk : L);
+  } else if (p.use_host_lengths) {
+    kv_len = p.host_lengths[b];
+  }
+  int kend = kv_len;
+  if (p.causal) kend = min(kend, q0 + FA_BM);
+  const int ntiles = (kend + FA_BN - 1) / FA_BN;
+
+  const half_t* kbase = p.k + (int64_t)b * p.k_batch + (int64_t)kvh * p.k_head;
+  const half_t* vbase = p.v + (int64_t)b * p.v_batch + (int64_t)kvh * p.v_head;
+
+  // ---- Q fragment (B operand of S^T): lane holds Q[qi][16s + 8h + 0..7] ----
+  half8v qf[QS];
+  {
+    const int qrow = qi < p.Sq ? qi : p.Sq - 1;
+    const half_t* qp = p.q + (int64_t)b * p.q_batch + (int64_t)head * p.q_head + (int64_t)qrow * p.q_tok;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) qf[s] = *reinterpret_cast<const half8v*>(qp + 16 * s + 8 * hh);
+    if (p.q_norm_w || p.rope) {
+      float x[QS][8];
+#pragma unroll
+      for (int s = 0; s < QS; ++s)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[s][i] = (float)qf[s][i];
+      if (p.q_norm_w) {
+        float ss = 0.f;
+#pragma unroll
+        for (int s = 0; s < QS; ++s)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) ss = fmaf(x[s][i], x[s][i], ss);
+        ss += __shfl_xor(ss, 32);
+        const float inv = rsqrtf(ss / (float)D + p.eps);
+#pragma unroll
+        for (int s = 0; s < QS; ++s) {
+          const half8v w = *reinterpret_cast<const half8v*>(p.q_norm_w + 16 * s + 8 * hh);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] * inv * (float)w[i];
+        }
+      }
+      if (p.rope) {
+        const float* rr = p.rope + (int64_t)qrow * (D / 2) * 4;
+#pragma unroll
+        for (int s = 0; s < QS / 2; ++s)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const floatx4 blk = *reinterpret_cast<const floatx4*>(rr + (16 * s + 8 * hh + i) * 4);
+            const float a = x[s][i], bb = x[s + QS / 2][i];
+            x[s][i] = blk[0] * a + blk[1] * bb;
+            x[s + QS / 2][i] = blk[2] * a + blk[0] * bb;
+          }
+      }
+#pragma unroll
+      for (int s = 0; s < QS; ++s)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qf[s][i] = f32_to_f16(x[s][i]);
+    }
+  }
+
+  // ---- K/V tile staging ----
+  half8v kreg[KLOADS];
+  half8v vreg[4];
+  const half8v zero8 = {};
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int r = 0; r < KLOADS; ++r) {
+      const int c = tid + FA_NT * r;
+      const int key = c / DCH, ch = c % DCH;
+      const int kg = k0 + key;
+      kreg[r] = kg < p.Sk ? *reinterpret_cast<const half8v*>(kbase + (int64_t)kg * p.k_tok + ch * 8) : zero8;
+    }
+    if (tid < VBLOCKS) {
+      const int dch = tid % DCH, kq = tid / DCH;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kg = k0 + 4 * kq + r;
+        vreg[r] = kg < p.Sk ? *reinterpret_cast<const half8v*>(vbase + (int64_t)kg * p.v_tok + dch * 8) : zero8;
+      }
+    }
+  };
+  auto store_tile = [&](int st) {
+#pragma unroll
+    for (int r = 0; r < KLOADS; ++r) {
+      const int c = tid + FA_NT * r;
+      const int key = c / DCH, ch = c % DCH;
+      *reinterpret_cast<half8v*>(&Ks[st][key * D + ((ch ^ (key & (DCH - 1))) * 8)]) = kreg[r];
+    }
+    if (tid < VBLOCKS) {
+      const int dch = tid % DCH, kq = tid / DCH;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = dch * 8 + e;
+        half4v val = {vreg[0][e], vreg[1][e], vreg[2][e], vreg[3][e]};
+        *reinterpret_cast<half4v*>(&Vt[st][d * FA_BN + ((kq ^ vt_swz(d)) * 4)]) = val;
+      }
+    }
+  };
+
+  floatx16 accO[OB];
+#pragma unroll
+  for (int c = 0; c < OB; ++c) accO[c] = floatx16{};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  if (ntiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int st = it & 1;
+    const int k0 = it * FA_BN;
+    if (it + 1 < ntiles) load_tile(k0 + FA_BN);
+
+    const bool skip = p.causal && (k0 > wave_row0 + 31);
+    if (!skip) {
+      floatx16 sacc[2] = {floatx16{}, floatx16{}};
+#pragma unroll
+      for (int s = 0; s < QS; ++s) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int key = 32 * t + c32;
+          const half8v a = *reinterpret_cast<const half8v*>(&Ks[st][key * D + (((2 * s + hh) ^ (key & (DCH - 1))) * 8)]);
+          sacc[t] = mfma32(a, qf[s], sacc[t]);
+        }
+      }
+      const bool need_mask = (k0 + FA_BN > kv_len) || (p.causal && k0 + FA_BN - 1 > wave_row0);
+      if (need_mask) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int kidx = k0 + 32 * t + (j >> 2) * 8 + 4 * hh + (j & 3);
+            if (kidx >= kv_len || (p.causal && kidx > qi)) sacc[t][j] = -INFINITY;
+          }
+      }
+      float mloc = sacc[0][0];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, sacc[t][j]);
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+      const float cand = mloc * p.scale_log2;
+      if (__any(cand > m_run + FA_RESCALE_THRESHOLD)) {
+        const float mnew = fmaxf(m_run, cand);
+        const float alpha = (mnew == -INFINITY) ? 1.f : fast_exp2(m_run - mnew);
+        l_run *= alpha;
+#pragma unroll
+        for (int c = 0; c < OB; ++c) accO[c] *= alpha;
+        m_run = mnew;
+      }
+      const float msub = (m_run == -INFINITY) ? 0.f : m_run;
+      half8v pb[4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float pv = fast_exp2(fmaf(sacc[t][j], p.scale_log2, -msub));
+          l_run += pv;
+          pb[2 * t + (j >> 3)][j & 7] = (half_t)pv;
+        }
+#pragma unroll
+      for (int c = 0; c < OB; ++c) {
+        const int d = 32 * c + c32;
+        const int f = vt_swz(d);
+        const half_t* vrow = &Vt[st][d * FA_BN];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const half4v lo = *reinterpret_cast<const half4v*>(vrow + (((4 * u + hh) ^ f) * 4));
+          const half4v hi = *reinterpret_cast<const half4v*>(vrow + (((4 * u + 2 + hh) ^ f) * 4));
+          const half8v a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          accO[c] = mfma32(a, pb[u], accO[c]);
+        }
+      }
+    }
+    if (it + 1 < ntiles) store_tile(st ^ 1);
+    __syncthreads();
+  }
+
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (qi < p.Sq) {
+    half_t* op = p.o + (int64_t)b * p.o_batch + (int64_t)head * p.o_head + (int64_t)qi * p.o_tok;
+#pragma unroll
+    for (int c = 0; c < OB; ++c)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        half4v val = {(half_t)(accO[c][4 * jj + 0] * inv), (half_t)(accO[c][4 * jj + 1] * inv),
+                      (half_t)(accO[c][4 * jj + 2] * inv), (half_t)(accO[c][4 * jj + 3] * inv)};
+        *reinterpret_cast<half4v*>(op + 32 * c + 8 * jj + 4 * hh) = val;
+      }
+  }
+}
+
+// ===========================================================================
+// Generic kernel: one 64-lane workgroup per (batch, head, query row), fp32
+// scores / online softmax / accumulation, any head_dim <= 512 and any
+// alignment.  The diagnostic fp32 path (encodeFP32, AttentionExecutor.swift:
+// 325-405) re-cut as a single fused kernel.
+// ===========================================================================
+constexpr int GEN_MAX_D = 512;
+
+__global__ __launch_bounds__(64) void generic_attention_kernel(FlashParams p, int D) {
+  __shared__ float qs[GEN_MAX_D];
+  __shared__ float ps[64];
+  const int lane = threadIdx.x;
+  const int qi = blockIdx.x;
+  const int head = blockIdx.y % p.H;
+  const int b = blockIdx.y / p.H;
+  const int kvh = head / p.group;
+
+  int kv_len = p.Sk;
+  if (p.key_lengths_dev) {
+    int L = p.key_lengths_dev[b];
+    kv_len = L < 1 ? 1 : (L > p.Sk ? p.Sk : L);
+  } else if (p.use_host_lengths) {
+    kv_len = p.host_lengths[b];
+  }
+  int kend = kv_len;
+  if (p.causal) kend = min(kend, qi + 1);
+
+  const half_t* qp = p.q + (int64_t)b * p.q_batch + (int64_t)head * p.q_head + (int64_t)qi * p.q_tok;
+  for (int d = lane; d < D; d += 64) qs[d] = (float)qp[d];
+  __syncthreads();
+
+  const half_t* kb = p.k + (int64_t)b * p.k_batch + (int64_t)kvh * p.k_head;
+  const half_t* vb = p.v + (int64_t)b * p.v_batch + (int64_t)kvh * p.v_head;
+  constexpr int EMAX = GEN_MAX_D / 64;
+  float acc[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) acc[e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  for (int k0 = 0; k0 < kend; k0 += 64) {
+    const int j = k0 + lane;
+    float s = -INFINITY;
+    if (j < kend) {
+      const half_t* kr = kb + (int64_t)j * p.k_tok;
+      float dot = 0.f;
+      for (int d = 0; d < D; ++d) dot = fmaf(qs[d], (float)kr[d], dot);
+      s = dot * p.scale_log2;
+    }
+    float mc = s;
+    for (int off = 32; off > 0; off >>= 1) mc = fmaxf(mc, __shfl_xor(mc, off));
+    const float mnew = fmaxf(m_run, mc);
+    const float alpha = (m_run == -INFINITY) ? 0.f : exp2f(m_run - mnew);
+    const float pj = (s == -INFINITY) ? 0.f : exp2f(s - mnew);
+    float psum = pj;
+    for (int off = 32; off > 0; off >>= 1) psum += __shfl_xor(psum, off);
+    l_run = l_run * alpha + psum;
+    m_run = mnew;
+    ps[lane] = pj;
+    __syncthreads();
+    const int cnt = min(64, kend - k0);
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) {
+      const int d = lane + 64 * e;
+      if (d < D) {
+        float a = acc[e] * alpha;
+        for (int jj = 0; jj < cnt; ++jj) a = fmaf(ps[jj], (float)vb[(int64_t)(k0 + jj) * p.v_tok + d], a);
+        acc[e] = a;
+      }
+    }
+    __syncthreads();
+  }
+  half_t* op = p.o + (int64_t)b * p.o_batch + (int64_t)head * p.o_head + (int64_t)qi * p.o_tok;
+  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) {
+    const int d = lane + 64 * e;
+    if (d < D) op[d] = f32_to_f16(acc[e] * inv);
+  }
+}
+
+// ===========================================================================
+// Q/K prologue: per-(batch, token, head) RMSNorm with a shared [D] weight and
+// optional split-half RoPE, fp32 maths, fp16 dense head-major output
+// [batch][heads][rows][D].  One wave per row; lane p owns the pairs
+// (p + 64e, p + 64e + D/2) (the pairing of rms_rope_split_half,
+// AnimaKernels.metal:696-729; without RoPE rmsnorm_heads_half, :660-689).
+// ===========================================================================
+__global__ __launch_bounds__(256) void qk_prologue_kernel(PrologueParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t total = (int64_t)p.batch * p.rows * p.heads;
+  if (row >= total) return;
+  const int h = (int)(row % p.heads);
+  const int64_t t = (row / p.heads) % p.rows;
+  const int b = (int)(row / ((int64_t)p.heads * p.rows));
+  const half_t* x = p.in + (int64_t)b * p.in_batch + t * p.in_tok + (int64_t)h * p.in_head;
+  half_t* y = p.out + (((int64_t)b * p.heads + h) * p.rows + t) * p.D;
+  const int half = p.D / 2;
+  constexpr int EMAX = GEN_MAX_D / 128;  // pairs per lane
+  float a[EMAX], c[EMAX];
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) {
+    const int i = lane + 64 * e;
+    a[e] = 0.f;
+    c[e] = 0.f;
+    if (i < half) {
+      a[e] = (float)x[i];
+      c[e] = (float)x[i + half];
+      ss = fmaf(a[e], a[e], fmaf(c[e], c[e], ss));
+    }
+  }
+  // odd head_dim: the middle element has no RoPE partner
+  float mid = 0.f;
+  const bool odd = (p.D & 1) != 0;
+  if (odd && lane == 0) {
+    mid = (float)x[p.D - 1];
+    ss = fmaf(mid, mid, ss);
+  }
+  float inv = 1.f;
+  if (p.norm_w) {
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    inv = rsqrtf(ss / (float)p.D + p.eps);
+  }
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) {
+    const int i = lane + 64 * e;
+    if (i < half) {
+      float va = a[e], vc = c[e];
+      if (p.norm_w) {
+        va = va * inv * (float)p.norm_w[i];
+        vc = vc * inv * (float)p.norm_w[i + half];
+      }
+      if (p.rope) {
+        const float* blk = p.rope + (t * half + i) * 4;
+        const float cs = blk[0], ns = blk[1], sn = blk[2];
+        const float ra = cs * va + ns * vc;
+        const float rc = sn * va + cs * vc;
+        va = ra;
+        vc = rc;
+      }
+      y[i] = f32_to_f16(va);
+      y[i + half] = f32_to_f16(vc);
+    }
+  }
+  if (odd && lane == 0) {
+    float v = mid;
+    if (p.norm_w) v = v * inv * (float)p.norm_w[p.D - 1];
+    y[p.D - 1] = f32_to_f16(v);
+  }
+}
+
+// ===========================================================================
+// Host launchers.
+// ===========================================================================
+void launch_flash(const FlashParams& p, int D, int batch, hipStream_t stream) {
+  const int64_t blocks = (int64_t)p.q_tiles * p.H * batch;
+  if (blocks <= 0) return;
+  if (blocks > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "attention grid too large");
+  dim3 grid((unsigned)blocks), block(FA_NT);
+  if (D == 128)
+    hipLaunchKernelGGL(flash_attention_kernel<128>, grid, block, 0, stream, p);
+  else if (D == 64)
+    hipLaunchKernelGGL(flash_attention_kernel<64>, grid, block, 0, stream, p);
+  else
+    fail(ANIMA_E_UNSUPPORTED, "flash attention requires head_dim 64 or 128");
+  ANIMA_HIP(hipGetLastError());
+}
+
+void launch_generic(const FlashParams& p, int D, int batch, hipStream_t stream) {
+  if (D > GEN_MAX_D) fail(ANIMA_E_UNSUPPORTED, "generic attention supports head_dim <= 512");
+  if ((int64_t)p.H * batch > 65535) fail(ANIMA_E_INVALID_SHAPE, "attention heads * batch too large");
+  dim3 grid((unsigned)p.Sq, (unsigned)(p.H * batch)), block(64);
+  hipLaunchKernelGGL(generic_attention_kernel, grid, block, 0, stream, p, D);
+  ANIMA_HIP(hipGetLastError());
+}
+
+void launch_prologue(const PrologueParams& p, hipStream_t stream) {
+  if (p.D > GEN_MAX_D) fail(ANIMA_E_UNSUPPORTED, "Q/K prologue supports head_dim <= 512");
+  const int64_t rows = (int64_t)p.batch * p.rows * p.heads;
+  if (rows <= 0) return;
+  const int64_t blocks = (rows + 3) / 4;
+  if (blocks > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "prologue grid too large");
+  hipLaunchKernelGGL(qk_prologue_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+  ANIMA_HIP(hipGetLastError());
+}
+
+}  // namespace anima

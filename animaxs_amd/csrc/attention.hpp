@@ -1,0 +1,64 @@
+// AttentionExecutor for gfx950 (AnimaXS/Runtime/Metal/AttentionExecutor.swift:77-848).
+#pragma once
+
+#include "context.hpp"
+
+namespace anima {
+
+constexpr int MAX_HOST_BATCH = 64;  // host key lengths travel inside the kernel arguments
+
+struct FlashParams {
+  const half_t* q;
+  const half_t* k;
+  const half_t* v;
+  half_t* o;
+  int64_t q_tok, q_head, q_batch;  // element strides
+  int64_t k_tok, k_head, k_batch;
+  int64_t v_tok, v_head, v_batch;
+  int64_t o_tok, o_head, o_batch;
+  int Sq, Sk, H, group;
+  int q_tiles;
+  float scale_log2;                // scale * log2(e)
+  int causal;
+  const int* key_lengths_dev;      // device lengths (clamped in-kernel) or null
+  int use_host_lengths;
+  int host_lengths[MAX_HOST_BATCH];
+  const half_t* q_norm_w;          // fused Q RMSNorm weight or null
+  float eps;
+  const float* rope;               // fused Q RoPE table or null
+};
+
+struct PrologueParams {
+  const half_t* in;
+  int64_t in_tok, in_head, in_batch;
+  half_t* out;                     // dense [batch][heads][rows][D]
+  int batch, rows, heads, D;
+  const half_t* norm_w;
+  float eps;
+  const float* rope;
+};
+
+void launch_flash(const FlashParams& p, int D, int batch, hipStream_t stream);
+void launch_generic(const FlashParams& p, int D, int batch, hipStream_t stream);
+void launch_prologue(const PrologueParams& p, hipStream_t stream);
+
+class AttentionExecutor {
+ public:
+  AttentionExecutor(anima_ctx* ctx, const anima_attention_config& cfg);
+  void encode(const anima_attention_args& a);
+  int64_t maximum_score_scratch_bytes(int64_t key_count, int64_t query_count) const;
+  int64_t workspace_bytes() const { return ws_.capacity(); }
+  anima_ctx* context() const { return ctx_; }
+
+ private:
+  anima_ctx* ctx_;
+  anima_attention_config cfg_;
+  Workspace ws_;
+};
+
+}  // namespace anima
+
+struct anima_attention {
+  anima::AttentionExecutor impl;
+  anima_attention(anima_ctx* c, const anima_attention_config& cfg) : impl(c, cfg) {}
+};

@@ -1,0 +1,208 @@
+// Host side of the attention executor: the validation contract of
+// AttentionExecutor.validate (AnimaXS/Runtime/Metal/AttentionExecutor.swift:778-847)
+// plus the batch / key-length / prologue extensions, and kernel dispatch.
+#include <cmath>
+#include <string>
+
+#include "attention.hpp"
+
+namespace anima {
+
+AttentionExecutor::AttentionExecutor(anima_ctx* ctx, const anima_attention_config& cfg)
+    : ctx_(ctx), cfg_(cfg) {
+  if (cfg.tile_rows <= 0) fail(ANIMA_E_INVALID_ARGUMENT, "attention tile rows must be positive");
+  if (cfg.numerics < ANIMA_NUMERICS_LEGACY || cfg.numerics > ANIMA_NUMERICS_BF16_COMPUTE)
+    fail(ANIMA_E_INVALID_ARGUMENT, "unknown attention numerics");
+  if (cfg.backend < ANIMA_ATTENTION_BACKEND_AUTO || cfg.backend > ANIMA_ATTENTION_BACKEND_GENERIC)
+    fail(ANIMA_E_INVALID_ARGUMENT, "unknown attention backend");
+  if (cfg.layout != ANIMA_LAYOUT_HEAD_MAJOR && cfg.layout != ANIMA_LAYOUT_TOKEN_MAJOR)
+    fail(ANIMA_E_INVALID_ARGUMENT, "unknown attention layout");
+}
+
+int64_t AttentionExecutor::maximum_score_scratch_bytes(int64_t key_count, int64_t query_count) const {
+  if (key_count <= 0) fail(ANIMA_E_INVALID_SHAPE, "attention key count must be positive");
+  const int64_t tile = query_count > 0 ? std::min<int64_t>(cfg_.tile_rows, query_count) : cfg_.tile_rows;
+  const int64_t elem = cfg_.numerics == ANIMA_NUMERICS_LEGACY ? 2 : 4;
+  return checked_product({tile, key_count, elem}, "attention");
+}
+
+static int64_t round_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+void AttentionExecutor::encode(const anima_attention_args& a) {
+  const int layout = a.layout < 0 ? cfg_.layout : a.layout;
+  if (layout != ANIMA_LAYOUT_HEAD_MAJOR && layout != ANIMA_LAYOUT_TOKEN_MAJOR)
+    fail(ANIMA_E_INVALID_ARGUMENT, "unknown attention layout");
+  const bool token_major = layout == ANIMA_LAYOUT_TOKEN_MAJOR;
+  const int64_t ts = token_major ? (a.token_stride > 0 ? a.token_stride : cfg_.token_stride) : 0;
+  const int64_t H = a.heads, Sq = a.query_count, Sk = a.key_count, D = a.head_dim;
+  const int64_t kvh = a.key_value_heads == 0 ? H : a.key_value_heads;
+  const int64_t B = a.batch == 0 ? 1 : a.batch;
+
+  // ---- AttentionExecutor.validate (:778-825) ----
+  if (!(H > 0 && Sq > 0 && Sk > 0 && D > 0 && kvh > 0 && H % kvh == 0 && a.query_offset >= 0 &&
+        a.key_offset >= 0 && a.value_offset >= 0 && a.output_offset >= 0 && (!a.causal || Sq == Sk) &&
+        B > 0))
+    fail(ANIMA_E_INVALID_SHAPE, "invalid attention shape, offset, or causal dimensions");
+  if (token_major) {
+    if (!(ts > 0 && D <= ts && ts % D == 0 && H * D == ts && kvh == H))
+      fail(ANIMA_E_INVALID_SHAPE,
+           "P4 token-major attention requires tokenStride == heads * headDim and keyValueHeads == heads");
+    if (a.query_offset % 16 || a.key_offset % 16 || a.value_offset % 16 || a.output_offset % 16 || (ts * 2) % 16)
+      fail(ANIMA_E_MISALIGNED, "P4 token-major attention requires 16-byte-aligned offsets and row stride");
+  }
+  int64_t q_bytes, k_bytes;
+  if (token_major) {
+    q_bytes = checked_product({B, Sq, ts, 2}, "attention");
+    k_bytes = checked_product({B, Sk, ts, 2}, "attention");
+  } else {
+    q_bytes = checked_product({B, H, Sq, D, 2}, "attention");
+    k_bytes = checked_product({B, kvh, Sk, D, 2}, "attention");
+  }
+  if (checked_end(a.query_offset, q_bytes, "attention") > a.query.length ||
+      checked_end(a.key_offset, k_bytes, "attention") > a.key.length ||
+      checked_end(a.value_offset, k_bytes, "attention") > a.value.length ||
+      checked_end(a.output_offset, q_bytes, "attention") > a.output.length)
+    fail(ANIMA_E_OUT_OF_BOUNDS, "attention buffer range is out of bounds");
+  if (!a.query.ptr || !a.key.ptr || !a.value.ptr || !a.output.ptr)
+    fail(ANIMA_E_INVALID_ARGUMENT, "attention buffer pointer is null");
+  if ((a.query_offset | a.key_offset | a.value_offset | a.output_offset) & 1)
+    fail(ANIMA_E_MISALIGNED, "attention offsets must be multiples of the 2-byte fp16 element");
+  if (Sq > 0x7fffffff || Sk > 0x7fffffff || H > 0x7fffffff || D > 0x7fffffff)
+    fail(ANIMA_E_INVALID_SHAPE, "attention dimension exceeds int32");
+
+  // ---- numerics / extensions ----
+  if (cfg_.numerics == ANIMA_NUMERICS_BF16_COMPUTE)
+    fail(ANIMA_E_UNSUPPORTED, "bf16_compute attention numerics are not supported on MI355X; select legacy or fp32 scores");
+  const float scale = a.scale == 0.f ? (float)(1.0 / std::sqrt((double)D)) : a.scale;
+  if (!std::isfinite(scale)) fail(ANIMA_E_INVALID_ARGUMENT, "attention scale must be finite");
+
+  FlashParams p{};
+  if (a.key_lengths) {
+    if (a.key_lengths_on_device) {
+      p.key_lengths_dev = a.key_lengths;
+    } else {
+      if (B > MAX_HOST_BATCH)
+        fail(ANIMA_E_UNSUPPORTED, "host key lengths support batch <= 64; pass device key lengths");
+      for (int64_t b = 0; b < B; ++b) {
+        const int32_t L = a.key_lengths[b];
+        if (L < 1 || L > Sk) fail(ANIMA_E_INVALID_SHAPE, "attention key length out of range (1..keyCount)");
+        p.host_lengths[b] = L;
+      }
+      p.use_host_lengths = 1;
+    }
+  }
+
+  const anima_qk_prologue* pro = a.prologue;
+  const half_t* q_norm = nullptr;
+  const half_t* k_norm = nullptr;
+  const float* rope_q = nullptr;
+  const float* rope_k = nullptr;
+  float eps = 0.f;
+  if (pro) {
+    q_norm = static_cast<const half_t*>(pro->q_norm_weight);
+    k_norm = static_cast<const half_t*>(pro->k_norm_weight);
+    eps = pro->eps;
+    if (!std::isfinite(eps) || eps < 0.f) fail(ANIMA_E_INVALID_ARGUMENT, "RMSNorm epsilon must be finite and >= 0");
+    if (pro->rope) {
+      if (D % 2) fail(ANIMA_E_INVALID_SHAPE, "RoPE requires an even head_dim");
+      if (pro->rope_q) {
+        if (pro->rope_tokens < Sq) fail(ANIMA_E_OUT_OF_BOUNDS, "RoPE table has fewer rows than query_count");
+        rope_q = pro->rope;
+      }
+      if (pro->rope_k) {
+        if (pro->rope_tokens < Sk) fail(ANIMA_E_OUT_OF_BOUNDS, "RoPE table has fewer rows than key_count");
+        rope_k = pro->rope;
+      }
+    }
+  }
+
+  // ---- strides (elements) ----
+  const half_t* qp = reinterpret_cast<const half_t*>(byte_ptr(a.query, a.query_offset));
+  const half_t* kp = reinterpret_cast<const half_t*>(byte_ptr(a.key, a.key_offset));
+  const half_t* vp = reinterpret_cast<const half_t*>(byte_ptr(a.value, a.value_offset));
+  half_t* op = reinterpret_cast<half_t*>(byte_ptr_mut(a.output, a.output_offset));
+  int64_t q_tok, q_head, q_batch, k_tok, k_head, k_batch;
+  if (token_major) {
+    q_tok = ts; q_head = D; q_batch = Sq * ts;
+    k_tok = ts; k_head = D; k_batch = Sk * ts;
+  } else {
+    q_tok = D; q_head = Sq * D; q_batch = H * Sq * D;
+    k_tok = D; k_head = Sk * D; k_batch = kvh * Sk * D;
+  }
+
+  const bool flash_shape = (D == 64 || D == 128);
+  const bool rows_aligned = aligned16(qp) && aligned16(kp) && aligned16(vp) && aligned16(op) && (q_tok % 8 == 0) &&
+                            (k_tok % 8 == 0) && (q_head % 8 == 0) && (k_head % 8 == 0) && (q_batch % 8 == 0) &&
+                            (k_batch % 8 == 0);
+  bool use_flash;
+  switch (cfg_.backend) {
+    case ANIMA_ATTENTION_BACKEND_FLASH:
+      if (!(flash_shape && rows_aligned))
+        fail(ANIMA_E_UNSUPPORTED,
+             "flash attention requires head_dim 64 or 128 and 16-byte-aligned rows, offsets and strides");
+      use_flash = true;
+      break;
+    case ANIMA_ATTENTION_BACKEND_GENERIC:
+      use_flash = false;
+      break;
+    default:
+      use_flash = flash_shape && rows_aligned;
+  }
+  const bool q_fusable = use_flash && (!q_norm || aligned16(q_norm)) && (!rope_q || aligned16(rope_q));
+  const bool need_q_pro = (q_norm || rope_q) && !q_fusable;
+  const bool need_k_pro = (k_norm || rope_k);
+
+  const int64_t k_ws = need_k_pro ? round_up(checked_product({B, kvh, Sk, D, 2}, "attention"), 256) : 0;
+  const int64_t q_ws = need_q_pro ? round_up(checked_product({B, H, Sq, D, 2}, "attention"), 256) : 0;
+  DeviceGuard guard(ctx_);
+  hipStream_t stream = ctx_->stream;
+  char* ws = (k_ws + q_ws) > 0 ? static_cast<char*>(ws_.get(k_ws + q_ws, stream)) : nullptr;
+
+  if (need_k_pro) {
+    PrologueParams pp{};
+    pp.in = kp; pp.in_tok = k_tok; pp.in_head = k_head; pp.in_batch = k_batch;
+    pp.out = reinterpret_cast<half_t*>(ws);
+    pp.batch = (int)B; pp.rows = (int)Sk; pp.heads = (int)kvh; pp.D = (int)D;
+    pp.norm_w = k_norm; pp.eps = eps; pp.rope = rope_k;
+    launch_prologue(pp, stream);
+    kp = pp.out;
+    k_tok = D; k_head = Sk * D; k_batch = kvh * Sk * D;
+  }
+  if (need_q_pro) {
+    PrologueParams pp{};
+    pp.in = qp; pp.in_tok = q_tok; pp.in_head = q_head; pp.in_batch = q_batch;
+    pp.out = reinterpret_cast<half_t*>(ws + k_ws);
+    pp.batch = (int)B; pp.rows = (int)Sq; pp.heads = (int)H; pp.D = (int)D;
+    pp.norm_w = q_norm; pp.eps = eps; pp.rope = rope_q;
+    launch_prologue(pp, stream);
+    qp = pp.out;
+    q_tok = D; q_head = Sq * D; q_batch = H * Sq * D;
+  }
+
+  p.q = qp; p.k = kp; p.v = vp; p.o = op;
+  p.q_tok = q_tok; p.q_head = q_head; p.q_batch = q_batch;
+  p.k_tok = k_tok; p.k_head = k_head; p.k_batch = k_batch;
+  if (token_major) {
+    p.v_tok = ts; p.v_head = D; p.v_batch = Sk * ts;
+    p.o_tok = ts; p.o_head = D; p.o_batch = Sq * ts;
+  } else {
+    p.v_tok = D; p.v_head = Sk * D; p.v_batch = kvh * Sk * D;
+    p.o_tok = D; p.o_head = Sq * D; p.o_batch = H * Sq * D;
+  }
+  p.Sq = (int)Sq; p.Sk = (int)Sk; p.H = (int)H; p.group = (int)(H / kvh);
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.causal = a.causal ? 1 : 0;
+  p.eps = eps;
+  if (use_flash && !need_q_pro) {
+    p.q_norm_w = q_norm;
+    p.rope = rope_q;
+  }
+  if (use_flash) {
+    p.q_tiles = (int)((Sq + 127) / 128);
+    launch_flash(p, (int)D, (int)B, stream);
+  } else {
+    launch_generic(p, (int)D, (int)B, stream);
+  }
+}
+
+}  // namespace anima

@@ -1,0 +1,35 @@
+// DiT block support kernels and DiTBlockExecutor analog
+// (AnimaXS/Runtime/Metal/DiTBlockExecutor.swift:49-1319).
+#pragma once
+
+#include "attention.hpp"
+#include "linear.hpp"
+
+namespace anima {
+
+void launch_layernorm_modulate(const float* residual, const float* mod, half_t* out, int64_t n, int64_t rows, float eps,
+                               int64_t mod_offset, hipStream_t stream);
+void launch_gate_add(float* residual, const half_t* branch, const float* gate, int64_t n, int64_t count,
+                     hipStream_t stream);
+void launch_gelu(half_t* values, int64_t count, hipStream_t stream);
+void launch_silu(const float* in, float* out, int64_t count, hipStream_t stream);
+void launch_add(float* dst, const float* src, int64_t count, hipStream_t stream);
+
+class DitBlockExecutor {
+ public:
+  explicit DitBlockExecutor(anima_ctx* ctx);
+  void encode(const anima_dit_block_weights& w, const anima_dit_block_args& a);
+
+ private:
+  anima_ctx* ctx_;
+  AttentionExecutor attention_;
+  LinearExecutor linear_;
+  Workspace ws_;
+};
+
+}  // namespace anima
+
+struct anima_dit_block {
+  anima::DitBlockExecutor impl;
+  explicit anima_dit_block(anima_ctx* c) : impl(c) {}
+};

@@ -1,0 +1,88 @@
+// Shared host/device definitions for libanima_hip (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+#include "anima_hip.h"
+#include "status.hpp"
+
+namespace anima {
+
+typedef _Float16 half_t;
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Validation failures throw Error (status.hpp) with the status code the C ABI
+// returns; messages follow the reference's AnimapkError.validation strings where
+// one exists (AttentionExecutor.swift:778-847, LinearExecutor.swift:412-459).
+inline void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) fail(ANIMA_E_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define ANIMA_HIP(call) ::anima::hip_check((call), #call)
+
+// Overflow-checked products / ends (checkedProduct / checkedEnd of the reference).
+inline int64_t checked_mul(int64_t a, int64_t b, const char* what) {
+  int64_t r;
+  if (__builtin_mul_overflow(a, b, &r)) fail(ANIMA_E_OVERFLOW, std::string(what) + " byte size overflow");
+  return r;
+}
+inline int64_t checked_product(std::initializer_list<int64_t> v, const char* what) {
+  int64_t r = 1;
+  for (int64_t x : v) r = checked_mul(r, x, what);
+  return r;
+}
+inline int64_t checked_end(int64_t off, int64_t bytes, const char* what) {
+  int64_t r;
+  if (__builtin_add_overflow(off, bytes, &r)) fail(ANIMA_E_OVERFLOW, std::string(what) + " buffer range overflow");
+  return r;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline const char* byte_ptr(const anima_buffer& b, int64_t off) {
+  return static_cast<const char*>(b.ptr) + off;
+}
+inline char* byte_ptr_mut(const anima_buffer& b, int64_t off) { return static_cast<char*>(b.ptr) + off; }
+
+// ---------------------------------------------------------------------------
+// Device helpers.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ floatx16 mfma32(half8v a, half8v b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ floatx4 mfma16(half8v a, half8v b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// fp32 -> fp16 with the reference's double rounding: the fp32 result is
+// materialised first (an empty asm register barrier), then converted with RNE.
+// Without the barrier the compiler folds the producing FMA and the conversion
+// into v_fma_mix{lo,hi}_f16, a single rounding that differs from
+// Float16(Float(x)) at fp16 ties.
+__device__ __forceinline__ half_t f32_to_f16(float v) {
+  asm volatile("" : "+v"(v));
+  return (half_t)v;
+}
+
+// Workgroup id remapped so that consecutive logical ids share an XCD: the
+// dispatcher places workgroup i on XCD i % 8, so logical id L is given to
+// physical id (L % per) * 8 + L / per when the grid is a multiple of 8.
+__device__ __forceinline__ int xcd_logical_block(int bid, int nblk) {
+  if ((nblk & 7) != 0) return bid;
+  int per = nblk >> 3;
+  return (bid & 7) * per + (bid >> 3);
+}
+
+}  // namespace anima

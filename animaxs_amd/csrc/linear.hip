@@ -1,0 +1,372 @@
+// Quantized linear for gfx950: W4/W8/FP16-weight MFMA GEMM with the dequant
+// fused into the weight-tile load, the standalone dequant kernel and the fp32
+// matvec.
+//
+// Replaces LinearExecutor.encodeMPS / encodeQGEMM (AnimaXS/Runtime/Metal/
+// LinearExecutor.swift:137-361) and the Metal kernels dequant_w4_to_half,
+// dequant_w8_to_half, copy_half_rows, qgemm_*, w4/w8/fp16_matvec_f32
+// (AnimaXS/Shaders/AnimaKernels.metal:19-79, 804-1047).  Weight value
+// v = fl32(q*scale + zero) (q*scale is exact, so one rounding), fp16 weight
+// RNE16(v): bit-identical to the reference's dequant_*_to_half.
+#include <string>
+
+#include "linear.hpp"
+
+namespace anima {
+
+// ===========================================================================
+// GEMM: Y[M,N] = X[M,K] deq(W)[N,K]^T.
+//
+// Workgroup tile 256 (M) x 128 (N) x 64 (K = one quantisation group), 4 waves
+// as 2 (N) x 2 (M); each wave owns 64 x 128 of C^T = W X^T computed with
+// v_mfma_f32_32x32x16_f16 (weights on M so each lane ends with 4 consecutive
+// output columns -> 8-byte stores).  The weight tile is unpacked and
+// dequantised in registers (nibble -> v_cvt_f32_ubyte, one FMA, RNE pack) and
+// written to LDS as fp16; X and W tiles are double-buffered with an XOR
+// swizzle; the next K block's global loads are issued before this block's
+// MFMAs.
+// ===========================================================================
+constexpr int G_BM = 256, G_BN = 128, G_BK = 64, G_NT = 256;
+
+__device__ __forceinline__ half_t dq1(uint32_t q, float s, float z) {
+  return f32_to_f16(fmaf((float)q, s, z));
+}
+
+// 16 packed bytes of one W4 row (32 K values) -> four fp16 chunks of 8.
+__device__ __forceinline__ void dq_w4_16(const u32x4 raw, float s, float z, half8v out[4]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t x = raw[w];
+    const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
+    half8v o;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      o[2 * b] = dq1((lo >> (8 * b)) & 0xffu, s, z);
+      o[2 * b + 1] = dq1((hi >> (8 * b)) & 0xffu, s, z);
+    }
+    out[w] = o;
+  }
+}
+
+// 16 packed bytes of one W8 row (16 K values) -> two fp16 chunks of 8.
+__device__ __forceinline__ void dq_w8_16(const u32x4 raw, float s, float z, half8v out[2]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t x = raw[w];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) out[w >> 1][(w & 1) * 4 + b] = dq1((x >> (8 * b)) & 0xffu, s, z);
+  }
+}
+
+template <int STORAGE, bool FAST>
+__global__ __launch_bounds__(G_NT, 1) void gemm_kernel(GemmParams p, int vec_store) {
+  __shared__ __attribute__((aligned(16))) half_t Xs[2][G_BM * G_BK];
+  __shared__ __attribute__((aligned(16))) half_t Ws[2][G_BN * G_BK];
+  constexpr int XL = G_BM * G_BK / 8 / G_NT;      // 8 X chunks per thread
+  constexpr int WL = STORAGE == ANIMA_STORAGE_W4 ? 1 : (STORAGE == ANIMA_STORAGE_W8 ? 2 : 4);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c32 = lane & 31, hh = lane >> 5;
+  const int wn = wave & 1, wm = wave >> 1;
+  const int ntn = (p.N + G_BN - 1) / G_BN;
+  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int tn = lb % ntn, tm = lb / ntn;
+  const int m0 = tm * G_BM, n0 = tn * G_BN;
+  const int nk = (p.K + G_BK - 1) / G_BK;
+
+  half8v xr[XL];
+  u32x4 wr[WL];
+  float ws_s[WL], ws_z[WL];
+  const half8v zero8 = {};
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
+
+  auto load_global = [&](int kb) {
+    const int kbase = kb * G_BK;
+#pragma unroll
+    for (int r = 0; r < XL; ++r) {
+      const int c = tid + G_NT * r;
+      const int row = c >> 3, ch = c & 7;
+      const int m = m0 + row;
+      if (FAST) {
+        xr[r] = m < p.M ? *reinterpret_cast<const half8v*>(p.x + (int64_t)m * p.K + kbase + ch * 8) : zero8;
+      } else {
+        half8v v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int k = kbase + ch * 8 + e;
+          v[e] = (m < p.M && k < p.K) ? p.x[(int64_t)m * p.K + k] : (half_t)0.f;
+        }
+        xr[r] = v;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < WL; ++r) {
+      const int c = tid + G_NT * r;
+      int row, part;
+      if (STORAGE == ANIMA_STORAGE_W4) { row = c >> 1; part = c & 1; }
+      else if (STORAGE == ANIMA_STORAGE_W8) { row = c >> 2; part = c & 3; }
+      else { row = c >> 3; part = c & 7; }
+      const int n = n0 + row;
+      if (STORAGE != ANIMA_STORAGE_FP16) {
+        ws_s[r] = n < p.N ? (float)p.scale[(int64_t)n * p.groups + kb] : 0.f;
+        ws_z[r] = n < p.N ? (float)p.zero[(int64_t)n * p.groups + kb] : 0.f;
+      }
+      if (FAST) {
+        const uint8_t* src;
+        if (STORAGE == ANIMA_STORAGE_W4) src = p.w + (int64_t)n * p.row_stride + kb * 32 + part * 16;
+        else if (STORAGE == ANIMA_STORAGE_W8) src = p.w + (int64_t)n * p.row_stride + kbase + part * 16;
+        else src = p.w + ((int64_t)n * p.row_stride + kbase + part * 8) * 2;
+        wr[r] = n < p.N ? *reinterpret_cast<const u32x4*>(src) : zero4;
+      } else {
+        // byte-granular path: any row stride / offset / K tail
+        uint32_t bytes[4] = {0u, 0u, 0u, 0u};
+        if (STORAGE == ANIMA_STORAGE_W4) {
+          // 32 K values -> 16 nibble bytes (even K low nibble); out-of-range K -> q = 0, and the
+          // value itself is zeroed after dequant (see store_tile)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int k = kbase + part * 32 + 2 * i;
+            uint32_t b = 0;
+            if (n < p.N && k < p.K) b = p.w[(int64_t)n * p.row_stride + (k >> 1)];
+            if (k + 1 >= p.K) b &= 0x0Fu;
+            bytes[i >> 2] |= b << (8 * (i & 3));
+          }
+        } else if (STORAGE == ANIMA_STORAGE_W8) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int k = kbase + part * 16 + i;
+            const uint32_t b = (n < p.N && k < p.K) ? p.w[(int64_t)n * p.row_stride + k] : 0u;
+            bytes[i >> 2] |= b << (8 * (i & 3));
+          }
+        } else {
+          const half_t* w16 = reinterpret_cast<const half_t*>(p.w);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int k = kbase + part * 8 + i;
+            const half_t h = (n < p.N && k < p.K) ? w16[(int64_t)n * p.row_stride + k] : (half_t)0.f;
+            const uint32_t hb = __builtin_bit_cast(uint16_t, h);
+            bytes[i >> 1] |= hb << (16 * (i & 1));
+          }
+        }
+        wr[r] = u32x4{bytes[0], bytes[1], bytes[2], bytes[3]};
+      }
+    }
+  };
+
+  auto store_tile = [&](int st, int kb) {
+    const int kbase = kb * G_BK;
+#pragma unroll
+    for (int r = 0; r < XL; ++r) {
+      const int c = tid + G_NT * r;
+      const int row = c >> 3, ch = c & 7;
+      *reinterpret_cast<half8v*>(&Xs[st][row * G_BK + ((ch ^ (row & 7)) * 8)]) = xr[r];
+    }
+#pragma unroll
+    for (int r = 0; r < WL; ++r) {
+      const int c = tid + G_NT * r;
+      if (STORAGE == ANIMA_STORAGE_W4) {
+        const int row = c >> 1, part = c & 1;
+        half8v o[4];
+        dq_w4_16(wr[r], ws_s[r], ws_z[r], o);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (!FAST) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (kbase + part * 32 + j * 8 + e >= p.K) o[j][e] = (half_t)0.f;
+          }
+          const int ch = part * 4 + j;
+          *reinterpret_cast<half8v*>(&Ws[st][row * G_BK + ((ch ^ (row & 7)) * 8)]) = o[j];
+        }
+      } else if (STORAGE == ANIMA_STORAGE_W8) {
+        const int row = c >> 2, part = c & 3;
+        half8v o[2];
+        dq_w8_16(wr[r], ws_s[r], ws_z[r], o);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          if (!FAST) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (kbase + part * 16 + j * 8 + e >= p.K) o[j][e] = (half_t)0.f;
+          }
+          const int ch = part * 2 + j;
+          *reinterpret_cast<half8v*>(&Ws[st][row * G_BK + ((ch ^ (row & 7)) * 8)]) = o[j];
+        }
+      } else {
+        const int row = c >> 3, ch = c & 7;
+        *reinterpret_cast<u32x4*>(&Ws[st][row * G_BK + ((ch ^ (row & 7)) * 8)]) = wr[r];
+      }
+    }
+  };
+
+  floatx16 acc[2][4];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = floatx16{};
+
+  if (nk > 0) {
+    load_global(0);
+    store_tile(0, 0);
+  }
+  __syncthreads();
+  for (int kb = 0; kb < nk; ++kb) {
+    const int st = kb & 1;
+    if (kb + 1 < nk) load_global(kb + 1);
+#pragma unroll
+    for (int s = 0; s < G_BK / 16; ++s) {
+      half8v wf[2], xf[4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int row = 64 * wn + 32 * t + c32;
+        wf[t] = *reinterpret_cast<const half8v*>(&Ws[st][row * G_BK + (((2 * s + hh) ^ (row & 7)) * 8)]);
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int row = 128 * wm + 32 * t + c32;
+        xf[t] = *reinterpret_cast<const half8v*>(&Xs[st][row * G_BK + (((2 * s + hh) ^ (row & 7)) * 8)]);
+      }
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = mfma32(wf[a], xf[b], acc[a][b]);
+    }
+    if (kb + 1 < nk) store_tile(st ^ 1, kb + 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int m = m0 + 128 * wm + 32 * b + c32;
+      if (m >= p.M) continue;
+      half_t* yrow = p.y + (int64_t)m * p.N;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int n = n0 + 64 * wn + 32 * a + 8 * jj + 4 * hh;
+        const half4v v = {(half_t)acc[a][b][4 * jj], (half_t)acc[a][b][4 * jj + 1], (half_t)acc[a][b][4 * jj + 2],
+                          (half_t)acc[a][b][4 * jj + 3]};
+        if (vec_store && n + 3 < p.N) {
+          *reinterpret_cast<half4v*>(yrow + n) = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < p.N) yrow[n + e] = v[e];
+        }
+      }
+    }
+}
+
+// ===========================================================================
+// Standalone dequant (dequant_w4_to_half / dequant_w8_to_half): one thread per
+// (row, 8 consecutive K); exact reference element formula.
+// ===========================================================================
+__global__ __launch_bounds__(256) void dequant_kernel(DequantParams p) {
+  const int chunks = (p.K + 7) / 8;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)chunks * p.N) return;
+  const int r = (int)(idx / chunks);
+  const int k0 = (int)(idx % chunks) * 8;
+  half_t* out = p.out + (int64_t)r * p.out_stride;
+  if (p.storage == ANIMA_STORAGE_FP16) {
+    const half_t* w16 = reinterpret_cast<const half_t*>(p.w) + (int64_t)r * p.row_stride;
+    for (int k = k0; k < k0 + 8 && k < p.K; ++k) out[k] = w16[k];
+    return;
+  }
+  const uint8_t* row = p.w + (int64_t)r * p.row_stride;
+  for (int k = k0; k < k0 + 8 && k < p.K; ++k) {
+    uint32_t q;
+    if (p.storage == ANIMA_STORAGE_W4) {
+      const uint32_t b = row[k >> 1];
+      q = (k & 1) == 0 ? (b & 0x0Fu) : (b >> 4);
+    } else {
+      q = row[k];
+    }
+    const int64_t g = (int64_t)r * p.groups + k / 64;
+    out[k] = dq1(q, (float)p.scale[g], (float)p.zero[g]);
+  }
+}
+
+// ===========================================================================
+// fp32 matvec (w4/w8/fp16_matvec_f32): one wave per output row, fp32 FMA per
+// lane then a wave tree reduction.
+// ===========================================================================
+__global__ __launch_bounds__(256) void matvec_kernel(MatvecParams p) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= p.N) return;
+  float sum = 0.f;
+  if (p.storage == ANIMA_STORAGE_FP16) {
+    const half_t* w16 = reinterpret_cast<const half_t*>(p.w) + (int64_t)row * p.row_stride;
+    for (int k = lane; k < p.K; k += 64) sum = fmaf(p.x[k], (float)w16[k], sum);
+  } else {
+    const uint8_t* w = p.w + (int64_t)row * p.row_stride;
+    for (int k = lane; k < p.K; k += 64) {
+      uint32_t q;
+      if (p.storage == ANIMA_STORAGE_W4) {
+        const uint32_t b = w[k >> 1];
+        q = (k & 1) == 0 ? (b & 0x0Fu) : (b >> 4);
+      } else {
+        q = w[k];
+      }
+      const int64_t g = (int64_t)row * p.groups + k / 64;
+      const float v = (float)q * (float)p.scale[g] + (float)p.zero[g];
+      sum = fmaf(p.x[k], v, sum);
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  if (lane == 0) p.y[row] = sum;
+}
+
+// ===========================================================================
+// Launchers.
+// ===========================================================================
+template <int S>
+static void launch_gemm_t(const GemmParams& p, bool fast, int vec, dim3 grid, hipStream_t stream) {
+  if (fast)
+    hipLaunchKernelGGL((gemm_kernel<S, true>), grid, dim3(G_NT), 0, stream, p, vec);
+  else
+    hipLaunchKernelGGL((gemm_kernel<S, false>), grid, dim3(G_NT), 0, stream, p, vec);
+}
+
+void launch_gemm(const GemmParams& p, int storage, hipStream_t stream) {
+  const int64_t tiles = (int64_t)((p.M + G_BM - 1) / G_BM) * ((p.N + G_BN - 1) / G_BN);
+  if (tiles <= 0) return;
+  if (tiles > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "GEMM grid too large");
+  const bool x_ok = aligned16(p.x) && (p.K % 8 == 0);
+  bool w_ok;
+  if (storage == ANIMA_STORAGE_W4)
+    w_ok = aligned16(p.w) && (p.row_stride % 16 == 0);
+  else if (storage == ANIMA_STORAGE_W8)
+    w_ok = aligned16(p.w) && (p.row_stride % 16 == 0);
+  else
+    w_ok = aligned16(p.w) && (p.row_stride % 8 == 0);
+  const bool fast = x_ok && w_ok && (p.K % G_BK == 0);
+  const int vec = ((reinterpret_cast<uintptr_t>(p.y) & 7u) == 0 && p.N % 4 == 0) ? 1 : 0;
+  const dim3 grid((unsigned)tiles);
+  if (storage == ANIMA_STORAGE_W4)
+    launch_gemm_t<ANIMA_STORAGE_W4>(p, fast, vec, grid, stream);
+  else if (storage == ANIMA_STORAGE_W8)
+    launch_gemm_t<ANIMA_STORAGE_W8>(p, fast, vec, grid, stream);
+  else
+    launch_gemm_t<ANIMA_STORAGE_FP16>(p, fast, vec, grid, stream);
+  ANIMA_HIP(hipGetLastError());
+}
+
+void launch_dequant(const DequantParams& p, hipStream_t stream) {
+  const int64_t total = (int64_t)((p.K + 7) / 8) * p.N;
+  if (total <= 0) return;
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "dequant grid too large");
+  hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+  ANIMA_HIP(hipGetLastError());
+}
+
+void launch_matvec(const MatvecParams& p, hipStream_t stream) {
+  if (p.N <= 0) return;
+  hipLaunchKernelGGL(matvec_kernel, dim3((unsigned)((p.N + 3) / 4)), dim3(256), 0, stream, p);
+  ANIMA_HIP(hipGetLastError());
+}
+
+}  // namespace anima

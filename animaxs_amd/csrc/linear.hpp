@@ -1,0 +1,78 @@
+// LinearExecutor for gfx950 (AnimaXS/Runtime/Metal/LinearExecutor.swift:43-459).
+#pragma once
+
+#include "context.hpp"
+
+namespace anima {
+
+struct GemmParams {
+  const half_t* x;        // [M, K] row-major fp16
+  half_t* y;              // [M, N] row-major fp16
+  const uint8_t* w;       // packed [N, row_stride] (bytes; halfs for FP16 storage)
+  const half_t* scale;    // [N, groups]
+  const half_t* zero;     // [N, groups]
+  int64_t row_stride;     // bytes (W4/W8) or halfs (FP16)
+  int M, N, K, groups;
+};
+
+struct MatvecParams {
+  const uint8_t* w;
+  const half_t* scale;
+  const half_t* zero;
+  int64_t row_stride;
+  const float* x;
+  float* y;
+  int N, K, groups, storage;
+};
+
+struct DequantParams {
+  const uint8_t* w;
+  const half_t* scale;
+  const half_t* zero;
+  int64_t row_stride;
+  half_t* out;
+  int64_t out_stride;
+  int N, K, groups, storage;
+};
+
+// Validated, resolved view of an anima_qweight.
+struct QWeightView {
+  int storage;
+  const uint8_t* packed;
+  const half_t* scale;
+  const half_t* zero;
+  int64_t rows, cols, row_stride, groups;
+};
+
+// LinearExecutor.validate (LinearExecutor.swift:412-438) for the weight part;
+// input/output ranges are checked by the callers.
+QWeightView validate_weight(const anima_qweight& w, const char* who);
+
+void launch_gemm(const GemmParams& p, int storage, hipStream_t stream);
+void launch_matvec(const MatvecParams& p, hipStream_t stream);
+void launch_dequant(const DequantParams& p, hipStream_t stream);
+
+class LinearExecutor {
+ public:
+  LinearExecutor(anima_ctx* ctx, const anima_linear_config& cfg);
+  void encode(anima_buffer input, int64_t input_offset, const anima_qweight& weight, anima_buffer output,
+              int64_t output_offset, int64_t input_rows, int32_t family);
+  anima_ctx* context() const { return ctx_; }
+
+ private:
+  anima_ctx* ctx_;
+  anima_linear_config cfg_;
+  Workspace ws_;
+};
+
+void encode_matvec(anima_ctx* ctx, const anima_qweight& weight, anima_buffer input, int64_t input_offset,
+                   anima_buffer output, int64_t output_offset);
+void encode_dequant(anima_ctx* ctx, const anima_qweight& weight, anima_buffer output, int64_t output_offset,
+                    int64_t out_row_stride);
+
+}  // namespace anima
+
+struct anima_linear {
+  anima::LinearExecutor impl;
+  anima_linear(anima_ctx* c, const anima_linear_config& cfg) : impl(c, cfg) {}
+};

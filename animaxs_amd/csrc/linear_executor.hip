@@ -1,0 +1,138 @@
+// Host side of the linear executor: LinearExecutor.validate
+// (AnimaXS/Runtime/Metal/LinearExecutor.swift:412-438) and dispatch.
+#include <string>
+
+#include "linear.hpp"
+
+namespace anima {
+
+QWeightView validate_weight(const anima_qweight& w, const char* who) {
+  const std::string name(who);
+  if (w.storage != ANIMA_STORAGE_W4 && w.storage != ANIMA_STORAGE_W8 && w.storage != ANIMA_STORAGE_FP16)
+    fail(ANIMA_E_UNSUPPORTED, name + " requires W4, W8, or FP16 weights");
+  if (!(w.rows > 0 && w.columns > 0 && w.packed_offset >= 0 && w.scale_offset >= 0 && w.zero_offset >= 0))
+    fail(ANIMA_E_INVALID_SHAPE, "invalid " + name + " shape or offset");
+  const int64_t min_stride = w.storage == ANIMA_STORAGE_W4 ? (w.columns + 1) / 2 : w.columns;
+  if (w.packed_row_stride < min_stride) fail(ANIMA_E_INVALID_SHAPE, "packed linear row stride is too small");
+  if (w.rows > 0x7fffffff || w.columns > 0x7fffffff)
+    fail(ANIMA_E_INVALID_SHAPE, name + " dimension exceeds int32");
+  const int64_t elem = w.storage == ANIMA_STORAGE_FP16 ? 2 : 1;
+  const int64_t packed_bytes = checked_product({w.rows, w.packed_row_stride, elem}, "LinearExecutor");
+  const int64_t groups = (w.columns + 63) / 64;
+  if (checked_end(w.packed_offset, packed_bytes, "LinearExecutor") > w.packed.length)
+    fail(ANIMA_E_OUT_OF_BOUNDS, "LinearExecutor buffer range is out of bounds");
+  if (!w.packed.ptr) fail(ANIMA_E_INVALID_ARGUMENT, name + " weight pointer is null");
+  QWeightView v{};
+  v.storage = w.storage;
+  v.packed = reinterpret_cast<const uint8_t*>(byte_ptr(w.packed, w.packed_offset));
+  v.rows = w.rows;
+  v.cols = w.columns;
+  v.row_stride = w.packed_row_stride;
+  v.groups = groups;
+  if (w.storage == ANIMA_STORAGE_FP16) {
+    if (w.packed_offset & 1) fail(ANIMA_E_MISALIGNED, "FP16 weight offset must be 2-byte aligned");
+    return v;
+  }
+  const int64_t param_bytes = checked_product({w.rows, groups, 2}, "LinearExecutor");
+  if (checked_end(w.scale_offset, param_bytes, "LinearExecutor") > w.scale.length ||
+      checked_end(w.zero_offset, param_bytes, "LinearExecutor") > w.zero.length)
+    fail(ANIMA_E_OUT_OF_BOUNDS, "LinearExecutor buffer range is out of bounds");
+  if (!w.scale.ptr || !w.zero.ptr) fail(ANIMA_E_INVALID_ARGUMENT, name + " scale/zero pointer is null");
+  if ((w.scale_offset | w.zero_offset) & 1) fail(ANIMA_E_MISALIGNED, "scale/zero offsets must be 2-byte aligned");
+  v.scale = reinterpret_cast<const half_t*>(byte_ptr(w.scale, w.scale_offset));
+  v.zero = reinterpret_cast<const half_t*>(byte_ptr(w.zero, w.zero_offset));
+  return v;
+}
+
+LinearExecutor::LinearExecutor(anima_ctx* ctx, const anima_linear_config& cfg) : ctx_(ctx), cfg_(cfg) {
+  if (cfg.tile_rows <= 0) fail(ANIMA_E_INVALID_ARGUMENT, "linear tile rows must be positive");
+  if (cfg.backend < ANIMA_LINEAR_BACKEND_AUTO || cfg.backend > ANIMA_LINEAR_BACKEND_DEQUANT_THEN_GEMM)
+    fail(ANIMA_E_INVALID_ARGUMENT, "unknown linear backend");
+}
+
+void LinearExecutor::encode(anima_buffer input, int64_t input_offset, const anima_qweight& weight,
+                            anima_buffer output, int64_t output_offset, int64_t input_rows, int32_t family) {
+  if (family < ANIMA_FAMILY_OTHER || family > ANIMA_FAMILY_MLP_DOWN)
+    fail(ANIMA_E_INVALID_ARGUMENT, "unknown linear family");
+  if (!(input_rows > 0 && input_offset >= 0 && output_offset >= 0))
+    fail(ANIMA_E_INVALID_SHAPE, "invalid LinearExecutor shape or offset");
+  const QWeightView w = validate_weight(weight, "LinearExecutor");
+  const int64_t in_bytes = checked_product({input_rows, w.cols, 2}, "LinearExecutor");
+  const int64_t out_bytes = checked_product({input_rows, w.rows, 2}, "LinearExecutor");
+  if (checked_end(input_offset, in_bytes, "LinearExecutor") > input.length ||
+      checked_end(output_offset, out_bytes, "LinearExecutor") > output.length)
+    fail(ANIMA_E_OUT_OF_BOUNDS, "LinearExecutor buffer range is out of bounds");
+  if (!input.ptr || !output.ptr) fail(ANIMA_E_INVALID_ARGUMENT, "LinearExecutor buffer pointer is null");
+  if ((input_offset | output_offset) & 1) fail(ANIMA_E_MISALIGNED, "LinearExecutor offsets must be 2-byte aligned");
+  if (input_rows > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "LinearExecutor input rows exceed int32");
+
+  DeviceGuard guard(ctx_);
+  hipStream_t stream = ctx_->stream;
+  GemmParams p{};
+  p.x = reinterpret_cast<const half_t*>(byte_ptr(input, input_offset));
+  p.y = reinterpret_cast<half_t*>(byte_ptr_mut(output, output_offset));
+  p.M = (int)input_rows;
+  p.N = (int)w.rows;
+  p.K = (int)w.cols;
+  p.groups = (int)w.groups;
+  if (cfg_.backend == ANIMA_LINEAR_BACKEND_DEQUANT_THEN_GEMM && w.storage != ANIMA_STORAGE_FP16) {
+    // Reference default shape: dequantise the whole weight once into fp16
+    // scratch (LinearExecutor.swift:146-193), then the fp16 GEMM.
+    const int64_t stride = (w.cols + 7) / 8 * 8;
+    half_t* scratch = static_cast<half_t*>(ws_.get(checked_product({w.rows, stride, 2}, "LinearExecutor"), stream));
+    DequantParams dp{};
+    dp.w = w.packed; dp.scale = w.scale; dp.zero = w.zero; dp.row_stride = w.row_stride;
+    dp.out = scratch; dp.out_stride = stride; dp.N = (int)w.rows; dp.K = (int)w.cols;
+    dp.groups = (int)w.groups; dp.storage = w.storage;
+    launch_dequant(dp, stream);
+    p.w = reinterpret_cast<const uint8_t*>(scratch);
+    p.row_stride = stride;
+    launch_gemm(p, ANIMA_STORAGE_FP16, stream);
+    return;
+  }
+  p.w = w.packed;
+  p.scale = w.scale;
+  p.zero = w.zero;
+  p.row_stride = w.row_stride;
+  launch_gemm(p, w.storage, stream);
+}
+
+void encode_matvec(anima_ctx* ctx, const anima_qweight& weight, anima_buffer input, int64_t input_offset,
+                   anima_buffer output, int64_t output_offset) {
+  const QWeightView w = validate_weight(weight, "matvec");
+  if (!(input_offset >= 0 && output_offset >= 0)) fail(ANIMA_E_INVALID_SHAPE, "invalid matvec shape or offset");
+  if (checked_end(input_offset, checked_product({w.cols, 4}, "matvec"), "matvec") > input.length ||
+      checked_end(output_offset, checked_product({w.rows, 4}, "matvec"), "matvec") > output.length)
+    fail(ANIMA_E_OUT_OF_BOUNDS, "matvec buffer range is out of bounds");
+  if (!input.ptr || !output.ptr) fail(ANIMA_E_INVALID_ARGUMENT, "matvec buffer pointer is null");
+  if ((input_offset | output_offset) & 3) fail(ANIMA_E_MISALIGNED, "matvec offsets must be 4-byte aligned");
+  DeviceGuard guard(ctx);
+  MatvecParams p{};
+  p.w = w.packed; p.scale = w.scale; p.zero = w.zero; p.row_stride = w.row_stride;
+  p.x = reinterpret_cast<const float*>(byte_ptr(input, input_offset));
+  p.y = reinterpret_cast<float*>(byte_ptr_mut(output, output_offset));
+  p.N = (int)w.rows; p.K = (int)w.cols; p.groups = (int)w.groups; p.storage = w.storage;
+  launch_matvec(p, ctx->stream);
+}
+
+void encode_dequant(anima_ctx* ctx, const anima_qweight& weight, anima_buffer output, int64_t output_offset,
+                    int64_t out_row_stride) {
+  const QWeightView w = validate_weight(weight, "dequant");
+  if (!(output_offset >= 0 && out_row_stride >= w.cols))
+    fail(ANIMA_E_INVALID_SHAPE, "invalid dequant output stride or offset");
+  const int64_t out_bytes =
+      checked_product({w.rows - 1, out_row_stride, 2}, "dequant") + checked_product({w.cols, 2}, "dequant");
+  if (checked_end(output_offset, out_bytes, "dequant") > output.length)
+    fail(ANIMA_E_OUT_OF_BOUNDS, "dequant buffer range is out of bounds");
+  if (!output.ptr) fail(ANIMA_E_INVALID_ARGUMENT, "dequant buffer pointer is null");
+  if (output_offset & 1) fail(ANIMA_E_MISALIGNED, "dequant output offset must be 2-byte aligned");
+  DeviceGuard guard(ctx);
+  DequantParams p{};
+  p.w = w.packed; p.scale = w.scale; p.zero = w.zero; p.row_stride = w.row_stride;
+  p.out = reinterpret_cast<half_t*>(byte_ptr_mut(output, output_offset));
+  p.out_stride = out_row_stride;
+  p.N = (int)w.rows; p.K = (int)w.cols; p.groups = (int)w.groups; p.storage = w.storage;
+  launch_dequant(p, ctx->stream);
+}
+
+}  // namespace anima

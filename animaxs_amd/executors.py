@@ -1,0 +1,407 @@
+"""Python mirror of the reference operator surface over the C ABI.
+
+Same names and argument meaning as the Swift executors so callers (and the
+tests) read like the reference's own:
+
+  * ``AttentionExecutor``  AnimaXS/Runtime/Metal/AttentionExecutor.swift:77-848
+  * ``LinearExecutor`` / ``QuantizedLinearWeightBuffers``
+                           AnimaXS/Runtime/Metal/LinearExecutor.swift:18-459
+  * ``QuantDecoders``      AnimaXS/Runtime/Animapk/QuantDecoders.swift:17-164
+  * ``DitRoPE`` / ``qwen_rope``  Runtime/Text/DitRoPE.swift:58-107,
+                           Runtime/Metal/QwenEncoderMetal.swift:126-143
+  * ``DiTBlockExecutor``   AnimaXS/Runtime/Metal/DiTBlockExecutor.swift:155-282
+
+A "buffer" is anything with ``data_ptr()`` plus ``numel()``/``element_size()``
+(a device tensor), an ``(address, length)`` tuple, or an ``_abi.Buffer``.  The
+executors never allocate device memory for the caller; they never compute on
+the CPU (QuantDecoders and the RoPE builders are CPU functions by definition in
+the reference as well).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Any, Optional
+
+import numpy as np
+
+from . import _abi
+from ._abi import AnimaError, call
+
+__all__ = [
+    "AnimaError", "Context", "AttentionExecutor", "LinearExecutor", "QuantizedLinearWeightBuffers",
+    "QKPrologue", "QuantDecoders", "DitRoPE", "qwen_rope", "DiTBlockExecutor", "BlockOps", "as_buffer",
+]
+
+
+def as_buffer(x: Any) -> _abi.Buffer:
+    if x is None:
+        return _abi.Buffer(None, 0)
+    if isinstance(x, _abi.Buffer):
+        return x
+    if isinstance(x, tuple):
+        return _abi.Buffer(C.c_void_p(int(x[0])), int(x[1]))
+    if hasattr(x, "data_ptr"):
+        return _abi.Buffer(C.c_void_p(x.data_ptr()), int(x.numel() * x.element_size()))
+    raise TypeError(f"cannot use {type(x)!r} as a device buffer")
+
+
+def _ptr(x: Any) -> Optional[int]:
+    if x is None:
+        return None
+    if hasattr(x, "data_ptr"):
+        return x.data_ptr()
+    return int(x)
+
+
+class Context:
+    """MetalContext analog: a HIP device and the stream all encodes append to."""
+
+    def __init__(self, device: int = 0, stream: Any = None):
+        h = C.c_void_p()
+        call("anima_ctx_create", int(device), C.byref(h))
+        self._h = h
+        self.device = device
+        if stream is not None:
+            self.set_stream(stream)
+
+    @property
+    def handle(self) -> C.c_void_p:
+        return self._h
+
+    def set_stream(self, stream: Any) -> None:
+        """``stream`` is a raw hipStream_t address or an object with ``cuda_stream``."""
+        raw = getattr(stream, "cuda_stream", stream)
+        call("anima_ctx_set_stream", self._h, C.c_void_p(int(raw) if raw else None))
+
+    def synchronize(self) -> None:
+        call("anima_ctx_synchronize", self._h)
+
+    def close(self) -> None:
+        if self._h:
+            call("anima_ctx_destroy", self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+_NUMERICS = {"legacy": _abi.NUMERICS_LEGACY, "fp32ScoresAndSoftmax": _abi.NUMERICS_FP32_SCORES,
+             "fp32": _abi.NUMERICS_FP32_SCORES, "bf16_compute": _abi.NUMERICS_BF16_COMPUTE}
+_BACKENDS = {"auto": _abi.ATTN_AUTO, "flash": _abi.ATTN_FLASH, "generic": _abi.ATTN_GENERIC}
+
+
+@dataclass
+class QKPrologue:
+    """Fused per-head RMSNorm (+ split-half RoPE) applied to Q and K."""
+    q_norm_weight: Any = None
+    k_norm_weight: Any = None
+    eps: float = 1e-6
+    rope: Any = None
+    rope_tokens: int = 0
+    rope_q: bool = True
+    rope_k: bool = True
+
+    def to_c(self) -> _abi.QKPrologue:
+        return _abi.QKPrologue(_ptr(self.q_norm_weight), _ptr(self.k_norm_weight), float(self.eps),
+                               _ptr(self.rope), int(self.rope_tokens), int(bool(self.rope_q)),
+                               int(bool(self.rope_k)))
+
+
+class AttentionExecutor:
+    """AttentionExecutor (AttentionExecutor.swift:97-110); layout is
+    ``"headMajor"`` or ``("tokenMajor", token_stride)``."""
+
+    def __init__(self, context: Context, tile_rows: int = 128, numerics: str = "legacy",
+                 layout: Any = "headMajor", backend: str = "auto"):
+        lay, ts = self._layout(layout)
+        cfg = _abi.AttentionConfig(int(tile_rows), _NUMERICS[numerics], _BACKENDS[backend], lay, ts)
+        h = C.c_void_p()
+        call("anima_attention_create", context.handle, C.byref(cfg), C.byref(h))
+        self._h = h
+        self.context = context
+        self.tile_rows = tile_rows
+        self.numerics = numerics
+
+    @staticmethod
+    def _layout(layout):
+        if layout is None:
+            return -1, 0
+        if layout == "headMajor":
+            return _abi.LAYOUT_HEAD_MAJOR, 0
+        if isinstance(layout, tuple) and layout[0] == "tokenMajor":
+            return _abi.LAYOUT_TOKEN_MAJOR, int(layout[1])
+        raise ValueError(f"unknown layout {layout!r}")
+
+    def maximum_score_scratch_bytes(self, key_count: int, query_count: Optional[int] = None) -> int:
+        out = C.c_int64()
+        call("anima_attention_max_score_scratch_bytes", self._h, int(key_count),
+             int(query_count) if query_count is not None else 0, C.byref(out))
+        return out.value
+
+    def workspace_bytes(self) -> int:
+        out = C.c_int64()
+        call("anima_attention_workspace_bytes", self._h, C.byref(out))
+        return out.value
+
+    def _args(self, query, key, value, output, heads, query_count, key_count, head_dim,
+              query_offset=0, key_offset=0, value_offset=0, output_offset=0, key_value_heads=None,
+              causal=False, layout=None, batch=1, key_lengths=None, key_lengths_on_device=False,
+              scale=0.0, prologue: Optional[QKPrologue] = None):
+        lay, ts = self._layout(layout)
+        keep = []
+        kl = None
+        if key_lengths is not None:
+            if key_lengths_on_device:
+                kl = C.c_void_p(_ptr(key_lengths))
+            else:
+                arr = np.ascontiguousarray(np.asarray(key_lengths, dtype=np.int32))
+                keep.append(arr)
+                kl = C.c_void_p(arr.ctypes.data)
+        pro = None
+        if prologue is not None:
+            pc = prologue.to_c()
+            keep.append(pc)
+            pro = C.pointer(pc)
+        a = _abi.AttentionArgs(
+            as_buffer(query), int(query_offset), as_buffer(key), int(key_offset),
+            as_buffer(value), int(value_offset), as_buffer(output), int(output_offset),
+            int(heads), int(query_count), int(key_count), int(head_dim),
+            int(key_value_heads or 0), int(bool(causal)), lay, ts, int(batch), kl,
+            int(bool(key_lengths_on_device)), float(scale), pro)
+        return a, keep
+
+    def encode(self, **kw) -> None:
+        """AttentionExecutor.encode (AttentionExecutor.swift:122-133); appends to the context stream."""
+        a, keep = self._args(**kw)
+        call("anima_attention_encode", self._h, C.byref(a))
+        del keep
+
+    def execute(self, **kw) -> None:
+        """AttentionExecutor.execute (AttentionExecutor.swift:751-776): encode + wait."""
+        a, keep = self._args(**kw)
+        call("anima_attention_execute", self._h, C.byref(a))
+        del keep
+
+    def close(self):
+        if self._h:
+            call("anima_attention_destroy", self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+@dataclass
+class QuantizedLinearWeightBuffers:
+    """QuantizedLinearWeightBuffers (LinearExecutor.swift:18-29)."""
+    storage: int
+    packed: Any
+    scale: Any
+    zero: Any
+    rows: int
+    columns: int
+    packed_row_stride: int
+    packed_offset: int = 0
+    scale_offset: int = 0
+    zero_offset: int = 0
+
+    def to_c(self) -> _abi.QWeight:
+        return _abi.QWeight(int(self.storage), as_buffer(self.packed), int(self.packed_offset),
+                            as_buffer(self.scale), int(self.scale_offset), as_buffer(self.zero),
+                            int(self.zero_offset), int(self.rows), int(self.columns), int(self.packed_row_stride))
+
+
+_LBACK = {"auto": _abi.LINEAR_AUTO, "fused": _abi.LINEAR_FUSED, "dequantizedGEMM": _abi.LINEAR_DEQUANT_THEN_GEMM}
+_FAMILY = {"other": _abi.FAMILY_OTHER, "attentionProjection": _abi.FAMILY_ATTENTION_PROJECTION,
+           "mlpUp": _abi.FAMILY_MLP_UP, "mlpDown": _abi.FAMILY_MLP_DOWN}
+
+
+class LinearExecutor:
+    """LinearExecutor (LinearExecutor.swift:64-75)."""
+
+    def __init__(self, context: Context, tile_rows: int = 128, backend: str = "auto"):
+        cfg = _abi.LinearConfig(int(tile_rows), _LBACK[backend])
+        h = C.c_void_p()
+        call("anima_linear_create", context.handle, C.byref(cfg), C.byref(h))
+        self._h = h
+        self.context = context
+        self.tile_rows = tile_rows
+
+    def encode(self, input, weight: QuantizedLinearWeightBuffers, output, input_rows: int,
+               input_offset: int = 0, output_offset: int = 0, family: str = "other") -> None:
+        w = weight.to_c()
+        call("anima_linear_encode", self._h, as_buffer(input), int(input_offset), C.byref(w),
+             as_buffer(output), int(output_offset), int(input_rows), _FAMILY[family])
+
+    def execute(self, input, weight: QuantizedLinearWeightBuffers, output, input_rows: int,
+                input_offset: int = 0, output_offset: int = 0, family: str = "other") -> None:
+        w = weight.to_c()
+        call("anima_linear_execute", self._h, as_buffer(input), int(input_offset), C.byref(w),
+             as_buffer(output), int(output_offset), int(input_rows), _FAMILY[family])
+
+    @staticmethod
+    def encode_matvec(context: Context, weight: QuantizedLinearWeightBuffers, input_f32, output_f32,
+                      input_offset: int = 0, output_offset: int = 0) -> None:
+        """w4/w8/fp16_matvec_f32 (AnimaKernels.metal:804-933)."""
+        w = weight.to_c()
+        call("anima_matvec_encode", context.handle, C.byref(w), as_buffer(input_f32), int(input_offset),
+             as_buffer(output_f32), int(output_offset))
+
+    @staticmethod
+    def encode_dequant(context: Context, weight: QuantizedLinearWeightBuffers, output,
+                       out_row_stride: Optional[int] = None, output_offset: int = 0) -> None:
+        """dequant_w4_to_half / dequant_w8_to_half (AnimaKernels.metal:19-66)."""
+        w = weight.to_c()
+        call("anima_dequant_to_half_encode", context.handle, C.byref(w), as_buffer(output), int(output_offset),
+             int(out_row_stride if out_row_stride is not None else weight.columns))
+
+    def close(self):
+        if self._h:
+            call("anima_linear_destroy", self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _u8(a) -> np.ndarray:
+    return np.ascontiguousarray(np.frombuffer(bytes(a), np.uint8) if isinstance(a, (bytes, bytearray)) else np.asarray(a, np.uint8))
+
+
+def _u16(a) -> np.ndarray:
+    a = np.asarray(a)
+    if a.dtype == np.float16:
+        a = a.view(np.uint16)
+    return np.ascontiguousarray(a.astype(np.uint16, copy=False))
+
+
+class QuantDecoders:
+    """QuantDecoders (QuantDecoders.swift:17-164) through the library's C decoders."""
+
+    @staticmethod
+    def dequant_w4(data, scale, zero, k: int, group_size: int = 64) -> np.ndarray:
+        d, s, z = _u8(data), _u16(scale), _u16(zero)
+        out = np.zeros(max(k, 0), np.float32)
+        call("anima_dequant_w4", d.ctypes.data, s.ctypes.data, z.ctypes.data, int(k), int(group_size), out.ctypes.data)
+        return out
+
+    @staticmethod
+    def dequant_w4_matrix(data, scale, zero, rows: int, cols: int, group_size: int = 64) -> np.ndarray:
+        d, s, z = _u8(data), _u16(scale), _u16(zero)
+        out = np.zeros((rows, cols), np.float32)
+        call("anima_dequant_w4_matrix", d.ctypes.data, s.ctypes.data, z.ctypes.data, int(rows), int(cols),
+             int(group_size), out.ctypes.data)
+        return out
+
+    @staticmethod
+    def dequant_w8(data, scale, zero, k: int, group_size: int = 64) -> np.ndarray:
+        d, s, z = _u8(data), _u16(scale), _u16(zero)
+        out = np.zeros(max(k, 0), np.float32)
+        call("anima_dequant_w8", d.ctypes.data, s.ctypes.data, z.ctypes.data, int(k), int(group_size), out.ctypes.data)
+        return out
+
+    @staticmethod
+    def dequant_w8_matrix(data, scale, zero, rows: int, cols: int, group_size: int = 64) -> np.ndarray:
+        d, s, z = _u8(data), _u16(scale), _u16(zero)
+        out = np.zeros((rows, cols), np.float32)
+        call("anima_dequant_w8_matrix", d.ctypes.data, s.ctypes.data, z.ctypes.data, int(rows), int(cols),
+             int(group_size), out.ctypes.data)
+        return out
+
+    @staticmethod
+    def fp16_to_float32(bits, count: int) -> np.ndarray:
+        b = _u16(bits)
+        out = np.zeros(max(count, 0), np.float32)
+        call("anima_fp16_to_float32", b.ctypes.data, int(count), out.ctypes.data)
+        return out
+
+
+class DitRoPE:
+    """DitRoPE.generate (DitRoPE.swift:58-107): fp32 [T*H*W, 64, 2, 2]."""
+
+    @staticmethod
+    def generate(T: int = 1, H: int = 32, W: int = 32) -> np.ndarray:
+        out = np.zeros((T * H * W, 64, 2, 2), np.float32)
+        call("anima_rope_dit3d", int(T), int(H), int(W), out.ctypes.data)
+        return out
+
+
+def qwen_rope(tokens: int, head_dim: int = 128, theta: float = 1.0e6) -> np.ndarray:
+    """QwenEncoderMetal.makeRope (QwenEncoderMetal.swift:126-143): fp32 [tokens, hd/2, 2, 2]."""
+    out = np.zeros((tokens, head_dim // 2, 2, 2), np.float32)
+    call("anima_rope_neox", int(tokens), int(head_dim), float(theta), out.ctypes.data)
+    return out
+
+
+class BlockOps:
+    """DiT block support kernels (AnimaKernels.metal)."""
+
+    def __init__(self, context: Context):
+        self.context = context
+
+    def layernorm_modulate_to_half(self, residual, modulation, output, n: int, rows: int, eps: float = 1e-6,
+                                   modulation_offset: Optional[int] = None) -> None:
+        call("anima_layernorm_modulate_to_half_encode", self.context.handle, as_buffer(residual),
+             as_buffer(modulation), as_buffer(output), int(n), int(rows), float(eps),
+             int(n if modulation_offset is None else modulation_offset))
+
+    def gate_add_half_f32(self, residual, branch, gate, n: int, count: int) -> None:
+        call("anima_gate_add_half_f32_encode", self.context.handle, as_buffer(residual), as_buffer(branch),
+             as_buffer(gate), int(n), int(count))
+
+    def gelu_half_inplace(self, values, count: int) -> None:
+        call("anima_gelu_half_inplace_encode", self.context.handle, as_buffer(values), int(count))
+
+    def silu(self, input, output, count: int) -> None:
+        call("anima_silu_f32_encode", self.context.handle, as_buffer(input), as_buffer(output), int(count))
+
+    def add_f32(self, destination, source, count: int) -> None:
+        call("anima_add_f32_encode", self.context.handle, as_buffer(destination), as_buffer(source), int(count))
+
+
+class DiTBlockExecutor:
+    """One DiT block (DiTBlockExecutor.execute, :155-282); fp32 residual updated in place."""
+
+    NAMES = ("self_q", "self_k", "self_v", "self_o", "cross_q", "cross_k", "cross_v", "cross_o", "mlp1", "mlp2",
+             "mod_self_w1", "mod_self_w2", "mod_cross_w1", "mod_cross_w2", "mod_mlp_w1", "mod_mlp_w2")
+
+    def __init__(self, context: Context):
+        h = C.c_void_p()
+        call("anima_dit_block_create", context.handle, C.byref(h))
+        self._h = h
+        self.context = context
+
+    def encode(self, weights: dict, norms: dict, residual, emb, adaln_lora, context_tokens_buf, rope,
+               tokens: int, dim: int = 2048, heads: int = 16, head_dim: int = 128, context_tokens: int = 512,
+               context_dim: int = 1024, mlp_hidden: int = 8192, eps: float = 1e-6) -> None:
+        w = _abi.DitBlockWeights()
+        for n in self.NAMES:
+            setattr(w, n, weights[n].to_c())
+        for n in ("self_q_norm", "self_k_norm", "cross_q_norm", "cross_k_norm"):
+            setattr(w, n, _ptr(norms[n]))
+        a = _abi.DitBlockArgs(as_buffer(residual), as_buffer(emb), as_buffer(adaln_lora), as_buffer(context_tokens_buf),
+                              _ptr(rope), int(tokens), int(dim), int(heads), int(head_dim), int(context_tokens),
+                              int(context_dim), int(mlp_hidden), float(eps))
+        call("anima_dit_block_encode", self._h, C.byref(w), C.byref(a))
+
+    def close(self):
+        if self._h:
+            call("anima_dit_block_destroy", self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

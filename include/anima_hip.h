@@ -1,0 +1,340 @@
+/*
+ * anima_hip.h — C ABI of libanima_hip, the MI355X (gfx950) attention and
+ * quantized-linear hot path of AnimaXS.
+ *
+ * The ABI replaces the reference's Swift/Metal operator executors:
+ *   AttentionExecutor   AnimaXS/Runtime/Metal/AttentionExecutor.swift:77-848
+ *   LinearExecutor      AnimaXS/Runtime/Metal/LinearExecutor.swift:43-459
+ *   QuantDecoders       AnimaXS/Runtime/Animapk/QuantDecoders.swift:17-164
+ * plus the DiT-block support kernels of AnimaXS/Shaders/AnimaKernels.metal that
+ * DiTBlockExecutor (AnimaXS/Runtime/Metal/DiTBlockExecutor.swift:1035-1319) encodes
+ * around them.
+ *
+ * Conventions (mirroring the reference):
+ *   - A Metal buffer + byte offset becomes an anima_buffer {device pointer, byte
+ *     length} + byte offset; every range is validated against the length before
+ *     anything is launched (AttentionExecutor.validate, LinearExecutor.validate).
+ *   - *_encode appends work to the context's HIP stream (the analog of encoding
+ *     into a caller-owned MTLCommandBuffer); *_execute = encode + stream
+ *     synchronize (the async execute of the reference).
+ *   - Executors own their scratch workspaces and are NOT re-entrant
+ *     (AttentionExecutor.swift:70): one caller at a time per executor.
+ *   - Failures return a non-zero anima_status; anima_last_error() returns the
+ *     thread-local message.  Nothing silently falls back.
+ *   - Plain C types only: no torch, no HIP types in signatures (streams are
+ *     passed as void* holding a hipStream_t).
+ */
+#ifndef ANIMA_HIP_H
+#define ANIMA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ANIMA_HIP_ABI_VERSION 1
+
+/* Status codes.  The reference throws AnimapkError.validation(String)
+ * (Runtime/Animapk/MappedFile.swift:14) for every failure; the codes split that
+ * one error by cause. */
+typedef enum anima_status {
+  ANIMA_OK = 0,
+  ANIMA_E_INVALID_SHAPE = 1,   /* non-positive / inconsistent dimensions */
+  ANIMA_E_OUT_OF_BOUNDS = 2,   /* a byte range exceeds its buffer */
+  ANIMA_E_OVERFLOW = 3,        /* a size product or range end overflows int64 */
+  ANIMA_E_MISALIGNED = 4,      /* offsets / strides violate the alignment contract */
+  ANIMA_E_UNSUPPORTED = 5,     /* valid request this backend refuses (loudly) */
+  ANIMA_E_DEVICE = 6,          /* HIP runtime error */
+  ANIMA_E_INVALID_ARGUMENT = 7 /* null handle / unknown enum value */
+} anima_status;
+
+/* Thread-local message of the last failure on this thread ("" after success). */
+const char* anima_last_error(void);
+/* ABI version (ANIMA_HIP_ABI_VERSION of the built library). */
+int32_t anima_abi_version(void);
+
+/* ------------------------------------------------------------------------- */
+/* Device buffers: MTLBuffer analog.                                          */
+/* ------------------------------------------------------------------------- */
+typedef struct anima_buffer {
+  void* ptr;        /* device pointer (hipMalloc'ed or any device-visible pointer) */
+  int64_t length;   /* bytes addressable from ptr */
+} anima_buffer;
+
+/* ------------------------------------------------------------------------- */
+/* Context: MetalContext analog (Runtime/Metal/MetalContext.swift:14-81).     */
+/* ------------------------------------------------------------------------- */
+typedef struct anima_ctx anima_ctx;
+
+/* MetalContext.init (MetalContext.swift:24-42): binds HIP device `device`; the
+ * context starts on the device's null stream. */
+anima_status anima_ctx_create(int32_t device, anima_ctx** out);
+anima_status anima_ctx_destroy(anima_ctx* ctx);
+/* Replace the stream all *_encode calls append to (the command buffer analog). */
+anima_status anima_ctx_set_stream(anima_ctx* ctx, void* hip_stream);
+/* Wait for all work encoded on the context stream (command buffer completion). */
+anima_status anima_ctx_synchronize(anima_ctx* ctx);
+
+/* ------------------------------------------------------------------------- */
+/* Attention: AttentionExecutor (AttentionExecutor.swift:77-848).              */
+/* ------------------------------------------------------------------------- */
+
+/* AttentionInputLayout (AttentionExecutor.swift:55-64). */
+typedef enum anima_layout {
+  ANIMA_LAYOUT_HEAD_MAJOR = 0,  /* [batch][heads][rows][head_dim], tight */
+  ANIMA_LAYOUT_TOKEN_MAJOR = 1  /* [batch][rows][token_stride]; head h at columns h*head_dim */
+} anima_layout;
+
+/* AttentionNumerics (AttentionExecutor.swift:5-12).  Every kernel here keeps
+ * scores, softmax and accumulation in fp32 (P is rounded to fp16 for the PV
+ * product on the matrix cores); LEGACY and FP32_SCORES therefore both select it,
+ * BF16_COMPUTE is refused with ANIMA_E_UNSUPPORTED. */
+typedef enum anima_attention_numerics {
+  ANIMA_NUMERICS_LEGACY = 0,
+  ANIMA_NUMERICS_FP32_SCORES = 1,
+  ANIMA_NUMERICS_BF16_COMPUTE = 2
+} anima_attention_numerics;
+
+/* DiTAttentionBackend (AttentionExecutor.swift:29-44) re-cut for MI355X:
+ * AUTO picks the MFMA flash kernel when its contract holds (head_dim 64/128,
+ * 16-byte aligned rows) and the generic fp32 kernel otherwise; FLASH demands the
+ * MFMA kernel and fails loudly when the shape is outside it (the metalFlash gate,
+ * :685-705); GENERIC forces the generic kernel (the fp32 diagnostic path). */
+typedef enum anima_attention_backend {
+  ANIMA_ATTENTION_BACKEND_AUTO = 0,
+  ANIMA_ATTENTION_BACKEND_FLASH = 1,
+  ANIMA_ATTENTION_BACKEND_GENERIC = 2
+} anima_attention_backend;
+
+/* AttentionExecutor.init (AttentionExecutor.swift:97-110). */
+typedef struct anima_attention_config {
+  int32_t tile_rows;      /* query rows per tile; > 0 (reference default 128) */
+  int32_t numerics;       /* anima_attention_numerics */
+  int32_t backend;        /* anima_attention_backend */
+  int32_t layout;         /* anima_layout default of encode() */
+  int64_t token_stride;   /* half elements per token row for TOKEN_MAJOR */
+} anima_attention_config;
+
+typedef struct anima_attention anima_attention;
+
+anima_status anima_attention_create(anima_ctx* ctx, const anima_attention_config* cfg,
+                                    anima_attention** out);
+anima_status anima_attention_destroy(anima_attention* attn);
+
+/* Fused per-head Q/K prologue: RMSNorm with a shared [head_dim] fp16 weight
+ * (rmsnorm_heads_half, AnimaKernels.metal:660-689) and/or split-half RoPE on the
+ * pairs (p, p+head_dim/2) from an fp32 [rope_tokens][head_dim/2][2][2] table of
+ * [cos,-sin,sin,cos] blocks (rms_rope_split_half, AnimaKernels.metal:696-729).
+ * Pointers are device pointers; NULL disables that step.  Query row r uses table
+ * row r, key row r uses table row r (rope_tokens >= max(query_count, key_count)). */
+typedef struct anima_qk_prologue {
+  const void* q_norm_weight;   /* fp16 [head_dim] or NULL */
+  const void* k_norm_weight;   /* fp16 [head_dim] or NULL */
+  float eps;                   /* RMSNorm epsilon (DiT and Qwen use 1e-6) */
+  const float* rope;           /* fp32 table or NULL (no RoPE, e.g. cross attention) */
+  int64_t rope_tokens;
+  int32_t rope_q;              /* apply RoPE to Q (1) */
+  int32_t rope_k;              /* apply RoPE to K (1) */
+} anima_qk_prologue;
+
+/* AttentionExecutor.encode (AttentionExecutor.swift:122-133).  The first block of
+ * fields is exactly the reference's parameter list; the rest are extensions whose
+ * zero values reproduce the reference behaviour (batch 1, no key mask, scale
+ * 1/sqrt(head_dim), no prologue). */
+typedef struct anima_attention_args {
+  anima_buffer query;  int64_t query_offset;
+  anima_buffer key;    int64_t key_offset;
+  anima_buffer value;  int64_t value_offset;
+  anima_buffer output; int64_t output_offset;
+  int64_t heads;
+  int64_t query_count;
+  int64_t key_count;
+  int64_t head_dim;
+  int64_t key_value_heads;     /* 0 -> heads; GQA map kv = h / (heads/key_value_heads) */
+  int32_t causal;              /* requires query_count == key_count */
+  int32_t layout;              /* -1 -> executor default, else anima_layout */
+  int64_t token_stride;        /* TOKEN_MAJOR row stride in halfs (0 -> executor default) */
+  /* --- extensions --- */
+  int64_t batch;               /* 0 or 1 -> single sequence; batches are contiguous */
+  const int32_t* key_lengths;  /* per-batch valid key count or NULL (all keys) */
+  int32_t key_lengths_on_device; /* 0: host array, validated 1..key_count; 1: device
+                                    array, clamped to [1, key_count] by the kernel */
+  float scale;                 /* 0 -> 1/sqrt(head_dim) (AttentionExecutor.swift:153) */
+  const anima_qk_prologue* prologue; /* NULL -> none */
+} anima_attention_args;
+
+anima_status anima_attention_encode(anima_attention* attn, const anima_attention_args* args);
+anima_status anima_attention_execute(anima_attention* attn, const anima_attention_args* args);
+/* AttentionExecutor.maximumScoreScratchBytes (AttentionExecutor.swift:112-120):
+ * the score scratch the reference's query-tiled path would need (fp16 legacy /
+ * fp32 scores) for min(tile_rows, query_count) x key_count.  The flash kernels
+ * here keep no score tile; the figure is reported for API parity. query_count<=0
+ * means "unbounded" (nil in the reference). */
+anima_status anima_attention_max_score_scratch_bytes(anima_attention* attn, int64_t key_count,
+                                                     int64_t query_count, int64_t* out_bytes);
+/* Bytes of device workspace the executor currently holds. */
+anima_status anima_attention_workspace_bytes(anima_attention* attn, int64_t* out_bytes);
+
+/* ------------------------------------------------------------------------- */
+/* Quantized linear: LinearExecutor (LinearExecutor.swift:43-459).             */
+/* ------------------------------------------------------------------------- */
+
+/* StorageDtype codes (Runtime/Animapk/AnimapkTensor.swift:4-9). */
+typedef enum anima_storage {
+  ANIMA_STORAGE_W4 = 0,
+  ANIMA_STORAGE_W8 = 1,
+  ANIMA_STORAGE_FP16 = 2,
+  ANIMA_STORAGE_FP32 = 3
+} anima_storage;
+
+/* QuantizedLinearWeightBuffers (LinearExecutor.swift:18-29): a packed [rows=N,
+ * columns=K] matrix; W4 packs the even K index in the low nibble; fp16 scale and
+ * zero per (row, 64-wide K group), groups reset at every row; value =
+ * q*scale + zero.  FP16 storage reuses the struct with packed_row_stride = K
+ * halfs' worth of bytes / 2 (stride counted in elements, as the reference). */
+typedef struct anima_qweight {
+  int32_t storage;             /* anima_storage (W4, W8 or FP16) */
+  anima_buffer packed; int64_t packed_offset;
+  anima_buffer scale;  int64_t scale_offset;
+  anima_buffer zero;   int64_t zero_offset;
+  int64_t rows;                /* N (output features) */
+  int64_t columns;             /* K (input features) */
+  int64_t packed_row_stride;   /* bytes per row for W4/W8, halfs per row for FP16 */
+} anima_qweight;
+
+/* DiTLinearBackend (LinearExecutor.swift:43-75) re-cut for MI355X: AUTO = fused
+ * dequant-in-registers MFMA GEMM (small-M rows use the group-scaled weight-stream
+ * kernel); DEQUANT_THEN_GEMM = the reference default shape (dequantize the whole
+ * weight to fp16 scratch, then an fp16 MFMA GEMM). */
+typedef enum anima_linear_backend {
+  ANIMA_LINEAR_BACKEND_AUTO = 0,
+  ANIMA_LINEAR_BACKEND_FUSED = 1,
+  ANIMA_LINEAR_BACKEND_DEQUANT_THEN_GEMM = 2
+} anima_linear_backend;
+
+/* DiTLinearFamily (LinearExecutor.swift:10-15); informational tag. */
+typedef enum anima_linear_family {
+  ANIMA_FAMILY_OTHER = 0,
+  ANIMA_FAMILY_ATTENTION_PROJECTION = 1,
+  ANIMA_FAMILY_MLP_UP = 2,
+  ANIMA_FAMILY_MLP_DOWN = 3
+} anima_linear_family;
+
+typedef struct anima_linear_config {
+  int32_t tile_rows;   /* > 0 (reference default 128); informational for the fused kernels */
+  int32_t backend;     /* anima_linear_backend */
+} anima_linear_config;
+
+typedef struct anima_linear anima_linear;
+
+anima_status anima_linear_create(anima_ctx* ctx, const anima_linear_config* cfg, anima_linear** out);
+anima_status anima_linear_destroy(anima_linear* lin);
+
+/* LinearExecutor.encode (LinearExecutor.swift:79-88): output[M,N] fp16 =
+ * input[M,K] fp16 x deq(weight)[N,K]^T, fp32 accumulation; input and output are
+ * tight row-major. */
+anima_status anima_linear_encode(anima_linear* lin, anima_buffer input, int64_t input_offset,
+                                 const anima_qweight* weight, anima_buffer output,
+                                 int64_t output_offset, int64_t input_rows, int32_t family);
+anima_status anima_linear_execute(anima_linear* lin, anima_buffer input, int64_t input_offset,
+                                  const anima_qweight* weight, anima_buffer output,
+                                  int64_t output_offset, int64_t input_rows, int32_t family);
+
+/* M=1 fp32 matvec w4_matvec_f32 / w8_matvec_f32 / fp16_matvec_f32
+ * (AnimaKernels.metal:804-933; DiTQuantizedWeightFactory.matvecKernel,
+ * LinearExecutor.swift:520-528): output_f32[N] = deq(W)[N,K] . input_f32[K]. */
+anima_status anima_matvec_encode(anima_ctx* ctx, const anima_qweight* weight,
+                                 anima_buffer input_f32, int64_t input_offset,
+                                 anima_buffer output_f32, int64_t output_offset);
+
+/* Standalone dequant dequant_w4_to_half / dequant_w8_to_half
+ * (AnimaKernels.metal:19-66): out[r*out_row_stride + k] = RNE16(q*s + z) for
+ * k < columns; out_row_stride in halfs (>= columns). */
+anima_status anima_dequant_to_half_encode(anima_ctx* ctx, const anima_qweight* weight,
+                                          anima_buffer output, int64_t output_offset,
+                                          int64_t out_row_stride);
+
+/* ------------------------------------------------------------------------- */
+/* CPU decoders: QuantDecoders (QuantDecoders.swift:17-164).                   */
+/* scale/zero are raw binary16 payloads; outputs are fp32.                     */
+/* ------------------------------------------------------------------------- */
+anima_status anima_dequant_w4(const uint8_t* data, const uint16_t* scale, const uint16_t* zero,
+                              int64_t k, int64_t group_size, float* out);            /* :23-48 */
+anima_status anima_dequant_w4_matrix(const uint8_t* data, const uint16_t* scale,
+                                     const uint16_t* zero, int64_t rows, int64_t cols,
+                                     int64_t group_size, float* out);                 /* :54-87 */
+anima_status anima_dequant_w8(const uint8_t* data, const uint16_t* scale, const uint16_t* zero,
+                              int64_t k, int64_t group_size, float* out);            /* :90-114 */
+anima_status anima_dequant_w8_matrix(const uint8_t* data, const uint16_t* scale,
+                                     const uint16_t* zero, int64_t rows, int64_t cols,
+                                     int64_t group_size, float* out);                 /* :117-147 */
+anima_status anima_fp16_to_float32(const uint16_t* bits, int64_t count, float* out);  /* :150-163 */
+
+/* ------------------------------------------------------------------------- */
+/* RoPE tables (CPU): fp32 [tokens][head_dim/2][2][2] of [cos,-sin,sin,cos].   */
+/* ------------------------------------------------------------------------- */
+/* DitRoPE.generate (Runtime/Text/DitRoPE.swift:58-107), any T/H/W grid,
+ * head_dim 128 (t/h/w dims 44/42/42).  out holds T*H*W*64*4 floats. */
+anima_status anima_rope_dit3d(int64_t T, int64_t H, int64_t W, float* out);
+/* QwenEncoderMetal.makeRope (Runtime/Metal/QwenEncoderMetal.swift:126-143):
+ * angle = pos / theta^(2j/head_dim).  out holds tokens*(head_dim/2)*4 floats. */
+anima_status anima_rope_neox(int64_t tokens, int64_t head_dim, float theta, float* out);
+
+/* ------------------------------------------------------------------------- */
+/* DiT block support kernels (AnimaKernels.metal), fp32 residual stream.       */
+/* ------------------------------------------------------------------------- */
+/* dit_layernorm_modulate_to_half (AnimaKernels.metal:477-524): out_f16[r,i] =
+ * half(LN(residual[r])[i] * (1 + modulation[modulation_offset + i]) + modulation[i]). */
+anima_status anima_layernorm_modulate_to_half_encode(anima_ctx* ctx, anima_buffer residual,
+                                                     anima_buffer modulation, anima_buffer output,
+                                                     int64_t n, int64_t rows, float eps,
+                                                     int64_t modulation_offset);
+/* gate_add_half_f32 (AnimaKernels.metal:624-634): residual[i] += float(branch[i]) * gate[i % n]. */
+anima_status anima_gate_add_half_f32_encode(anima_ctx* ctx, anima_buffer residual,
+                                            anima_buffer branch, anima_buffer gate, int64_t n,
+                                            int64_t count);
+/* dit_gelu_half_inplace (AnimaKernels.metal:312-322), exact-erf GELU in fp32. */
+anima_status anima_gelu_half_inplace_encode(anima_ctx* ctx, anima_buffer values, int64_t count);
+/* silu (AnimaKernels.metal:388-397), fp32. */
+anima_status anima_silu_f32_encode(anima_ctx* ctx, anima_buffer input, anima_buffer output,
+                                   int64_t count);
+/* add_f32 (AnimaKernels.metal:649-656): destination[i] += source[i]. */
+anima_status anima_add_f32_encode(anima_ctx* ctx, anima_buffer destination, anima_buffer source,
+                                  int64_t count);
+
+/* ------------------------------------------------------------------------- */
+/* DiT block: DiTBlockExecutor.execute (DiTBlockExecutor.swift:155-282) for one  */
+/* block at any square token count, fp32 residual updated in place.            */
+/* ------------------------------------------------------------------------- */
+typedef struct anima_dit_block_weights {
+  anima_qweight self_q, self_k, self_v, self_o;
+  anima_qweight cross_q, cross_k, cross_v, cross_o;
+  anima_qweight mlp1, mlp2;
+  /* modulation W1 [256, dim] and W2 [3*dim, 256] per branch (fp16/W4/W8) */
+  anima_qweight mod_self_w1, mod_self_w2, mod_cross_w1, mod_cross_w2, mod_mlp_w1, mod_mlp_w2;
+  const void* self_q_norm; const void* self_k_norm;   /* fp16 [head_dim] */
+  const void* cross_q_norm; const void* cross_k_norm; /* fp16 [head_dim] */
+} anima_dit_block_weights;
+
+typedef struct anima_dit_block_args {
+  anima_buffer residual;       /* fp32 [tokens, dim], updated in place */
+  anima_buffer emb;            /* fp32 [dim] timestep embedding */
+  anima_buffer adaln_lora;     /* fp32 [3*dim] */
+  anima_buffer context;        /* fp16 [context_tokens, context_dim] */
+  const float* rope;           /* device fp32 [tokens][64][2][2] */
+  int64_t tokens, dim, heads, head_dim, context_tokens, context_dim, mlp_hidden;
+  float eps;
+} anima_dit_block_args;
+
+typedef struct anima_dit_block anima_dit_block;
+anima_status anima_dit_block_create(anima_ctx* ctx, anima_dit_block** out);
+anima_status anima_dit_block_destroy(anima_dit_block* blk);
+anima_status anima_dit_block_encode(anima_dit_block* blk, const anima_dit_block_weights* w,
+                                    const anima_dit_block_args* args);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ANIMA_HIP_H */

@@ -1,0 +1,55 @@
+"""CPU oracle for the AnimaXS attention + quantized-linear hot path.
+
+TEST INFRASTRUCTURE ONLY.  This package restates the reference algorithms on
+the CPU (numpy for byte/integer arithmetic, torch-CPU fp32 for floating point)
+so the HIP library can be checked against them.  Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it, and only as the checker: the product library (``animaxs_amd``)
+never imports, links or calls anything here, and has no CPU fallback.
+
+Every function cites the reference file:line it follows (paths relative to the
+reference repository root).  How each function is pinned (golden vectors,
+known answers, closed forms, brute force) is listed in ``PINNING`` below and
+exercised by ``tests/test_oracle_*.py``.
+"""
+
+from . import quant, rope, norms, attention, inputs, blocks  # noqa: F401
+
+# function -> the independent checks that pin it (see tests/test_oracle_*.py)
+PINNING = {
+    "quant.dequant_w4 / dequant_w4_matrix": (
+        "known answers of AnimaXSTests/QuantDecoderTests.swift:23-60 and "
+        "MetalExecutionTests.swift:28-65,170-257; row reset at K=68; "
+        "bit patterns compared with an independent per-element fp64 decode"),
+    "quant.dequant_w8 / dequant_w8_matrix": (
+        "QuantDecoderTests.swift:64-93; fp16-subnormal scale/zero bit patterns of "
+        "MetalExecutionTests.swift:115-168; row reset at K=65"),
+    "quant.dequant_to_half": (
+        "MetalExecutionTests.swift:28-65 (0x6E,0.5,-0.25 -> 6.75, 2.75) and the "
+        "row-aware RNE16 bit patterns of :170-257; exhaustive check against "
+        "fp64 arithmetic followed by numpy's RNE cast"),
+    "rope.dit_rope_table": (
+        "golden table scripts/oracle_out/dit_rope_oracle.npz (32x32 grid, "
+        "fixture tests/golden/dit_rope_subset.npz); anchors of "
+        "DitRoPETests.swift:24-88; grid-size invariance (token h*W+w)"),
+    "rope.neox_rope_table": (
+        "closed form cos/sin(pos * theta^(-2j/128)) checked in fp64; "
+        "QwenNumerics.ropeNeoX equivalence (rotate-half form) on random input"),
+    "rope.apply_split_half": (
+        "DiTBlockTests.swift:18-63 hand values (90/180 degree rotations, "
+        "split-half vs adjacent pairing)"),
+    "norms.rms_norm / rms_norm_heads": (
+        "DiTBlockTests.swift:92-114 closed form; torch.nn.functional.rms_norm"),
+    "norms.layer_norm_modulated": (
+        "DiTBlockTests.swift:66-88 hand values; torch.nn.functional.layer_norm"),
+    "norms.gelu_erf": "DiTBlockTests.swift:168-172 values; math.erf in fp64",
+    "attention.sdpa": (
+        "fp64 brute force on small shapes; zero-Q/K mean-of-V special case "
+        "(AttentionExecutorTests.swift:460-504); last-V-row (c+1)/512 case "
+        "(:64-88); GQA 0,0,1,1 (:90-111, GqaHeadMappingTests.swift:23-89); "
+        "tiny 2x3 case (DiTBlockTests.swift:117-147); additive finfo.min/4 mask "
+        "equivalence (scripts/qwen_comfy_oracle.py:233-248)"),
+    "blocks.dit_block": (
+        "composition of pinned parts following scripts/dit_block0_oracle.py:327-391; "
+        "zero-gate identity and zero-weight invariants"),
+}

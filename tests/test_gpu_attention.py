@@ -1,0 +1,215 @@
+"""GPU parity of the attention path against the CPU oracle (through the C ABI).
+
+Bar: max-abs <= 1e-2 and mean-rel (sum|y-ref|/sum|ref|) <= 1e-3 against the fp32
+oracle for every workload; the reference's own special-case answers
+(AttentionExecutorTests.swift) at their own tolerances.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import animaxs_amd
+from animaxs_amd import AnimaError, AttentionExecutor, QKPrologue
+from oracle import attention as oatt
+from oracle import inputs, rope as orope
+from tests.helpers import assert_attention_close, dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(ctx, q, k, v, *, layout, heads, Sq, Sk, D, out_shape, backend="auto", **kw):
+    o = torch.full(out_shape, float("nan"), dtype=torch.float16, device="cuda")
+    ex = AttentionExecutor(ctx, layout=layout, backend=backend)
+    ex.execute(query=q, key=k, value=v, output=o, heads=heads, query_count=Sq, key_count=Sk, head_dim=D, **kw)
+    torch.cuda.synchronize()
+    return o
+
+
+def test_workload1_self_attention_s1024(ctx):
+    d = inputs.self_attention(1)
+    q, k, v = (dev(d[n]) for n in "qkv")
+    o = _run(ctx, q, k, v, layout=("tokenMajor", 2048), heads=16, Sq=1024, Sk=1024, D=128, out_shape=(1, 1024, 16, 128))
+    ref = oatt.sdpa(d["q"], d["k"], d["v"])
+    assert_attention_close(o, ref, label="workload1 S1024")
+
+
+def test_workload2_self_attention_s4096_norm_rope(ctx):
+    d = inputs.self_attention(2)
+    q, k, v = (dev(d[n]) for n in "qkv")
+    rope = dev(d["rope"])
+    pro = QKPrologue(dev(d["q_norm_w"]), dev(d["k_norm_w"]), d["eps"], rope, 4096, True, True)
+    o = _run(ctx, q, k, v, layout=("tokenMajor", 2048), heads=16, Sq=4096, Sk=4096, D=128,
+             out_shape=(1, 4096, 16, 128), prologue=pro)
+    qq = oatt.qk_prologue(d["q"], d["q_norm_w"], d["eps"], d["rope"])
+    kk = oatt.qk_prologue(d["k"], d["k_norm_w"], d["eps"], d["rope"])
+    ref = oatt.sdpa(qq, kk, d["v"])
+    assert_attention_close(o, ref, label="workload2 S4096 norm+rope")
+
+
+@pytest.mark.parametrize("device_lengths", [False, True])
+def test_workload3_cross_attention_masked(ctx, device_lengths):
+    d = inputs.cross_attention()
+    q, k, v = (dev(d[n]) for n in "qkv")
+    L = d["key_lengths"]
+    lengths = dev(L) if device_lengths else L.numpy()
+    pro = QKPrologue(dev(d["q_norm_w"]), dev(d["k_norm_w"]), d["eps"], None, 0, False, False)
+    o = _run(ctx, q, k, v, layout=("tokenMajor", 2048), heads=16, Sq=4096, Sk=512, D=128,
+             out_shape=(4, 4096, 16, 128), batch=4, key_lengths=lengths, key_lengths_on_device=device_lengths,
+             prologue=pro)
+    qq = oatt.qk_prologue(d["q"], d["q_norm_w"], d["eps"], None)
+    kk = oatt.qk_prologue(d["k"], d["k_norm_w"], d["eps"], None)
+    ref = oatt.sdpa(qq, kk, d["v"], key_lengths=L.tolist())
+    assert_attention_close(o, ref, label=f"workload3 cross masked dev={device_lengths}")
+
+
+def test_workload3_reference_faithful_unmasked_zero_context(ctx):
+    """Reference behaviour: no mask; context rows >= L_b are zero
+    (scripts/animapk_cuda/comfy_stub/comfy/ldm/anima/model.py:204-205)."""
+    d = inputs.cross_attention(B=2, Sq=512)
+    L = d["key_lengths"][:2]
+    k, v = d["k"].clone(), d["v"].clone()
+    for b in range(2):
+        k[b, int(L[b]):] = 0
+        v[b, int(L[b]):] = 0
+    pro = QKPrologue(dev(d["q_norm_w"]), dev(d["k_norm_w"]), d["eps"], None, 0, False, False)
+    o = _run(ctx, dev(d["q"]), dev(k), dev(v), layout=("tokenMajor", 2048), heads=16, Sq=512, Sk=512, D=128,
+             out_shape=(2, 512, 16, 128), batch=2, prologue=pro)
+    qq = oatt.qk_prologue(d["q"], d["q_norm_w"], d["eps"], None)
+    kk = oatt.qk_prologue(k, d["k_norm_w"], d["eps"], None)
+    ref = oatt.sdpa(qq, kk, v)
+    assert_attention_close(o, ref, label="workload3 unmasked zero-padded")
+
+
+def test_workload4_qwen_causal_gqa(ctx):
+    d = inputs.qwen_attention()
+    # head-major [B, H, S, D] like the reference's Qwen path (QwenEncoderMetal.swift:269-279)
+    qh = d["q"].permute(0, 2, 1, 3).contiguous()
+    kh = d["k"].permute(0, 2, 1, 3).contiguous()
+    vh = d["v"].permute(0, 2, 1, 3).contiguous()
+    L = d["key_lengths"]
+    pro = QKPrologue(dev(d["q_norm_w"]), dev(d["k_norm_w"]), d["eps"], dev(d["rope"]), 512, True, True)
+    o = _run(ctx, dev(qh), dev(kh), dev(vh), layout="headMajor", heads=16, Sq=512, Sk=512, D=128,
+             out_shape=(4, 16, 512, 128), batch=4, key_value_heads=8, causal=True, key_lengths=L.numpy(),
+             prologue=pro)
+    qq = oatt.qk_prologue(d["q"], d["q_norm_w"], d["eps"], d["rope"])
+    kk = oatt.qk_prologue(d["k"], d["k_norm_w"], d["eps"], d["rope"])
+    ref = oatt.sdpa(qq, kk, d["v"], causal=True, key_lengths=L.tolist())
+    assert_attention_close(o.permute(0, 2, 1, 3), ref, label="workload4 qwen causal gqa")
+
+
+# ---------------------------------------------------------------------------
+# Reference special cases (AnimaXSTests/AttentionExecutorTests.swift)
+# ---------------------------------------------------------------------------
+def test_cross_attention_last_value_row_tail_tile(ctx):
+    """AttentionExecutorTests.swift:64-88: Q=K=0, only the last V row nonzero ->
+    every output row equals (c+1)/512 (129 queries exercise a tail tile)."""
+    Sq, Sk, D = 129, 512, 64
+    q = torch.zeros(Sq * D, dtype=torch.float16)
+    k = torch.zeros(Sk * D, dtype=torch.float16)
+    v = torch.zeros(Sk, D, dtype=torch.float16)
+    v[-1] = torch.arange(1, D + 1, dtype=torch.float16)
+    o = _run(ctx, dev(q), dev(k), dev(v), layout="headMajor", heads=1, Sq=Sq, Sk=Sk, D=D, out_shape=(Sq, D))
+    expect = (torch.arange(1, D + 1, dtype=torch.float32) / 512).expand(Sq, D)
+    assert float((o.float().cpu() - expect).abs().max()) <= 1e-4
+
+
+def test_grouped_query_attention_contiguous_kv_heads(ctx):
+    """AttentionExecutorTests.swift:90-111: heads 4, kv heads 2 -> mapping 0,0,1,1."""
+    q = torch.zeros(4 * 4, dtype=torch.float16)
+    k = torch.zeros(2 * 4, dtype=torch.float16)
+    v = torch.tensor([2.0] * 4 + [9.0] * 4, dtype=torch.float16)
+    o = _run(ctx, dev(q), dev(k), dev(v), layout="headMajor", heads=4, Sq=1, Sk=1, D=4, out_shape=(16,),
+             key_value_heads=2)
+    assert o.float().cpu().tolist() == [2.0] * 8 + [9.0] * 8
+
+
+def test_token_major_no_head_mixing(ctx):
+    """AttentionExecutorTests.swift:460-504: Q=K=0 -> per-head mean of V rows."""
+    heads, D, rows = 2, 4, 3
+    model = heads * D
+    vals = torch.zeros(rows, model)
+    for t in range(rows):
+        for h in range(heads):
+            for c in range(D):
+                vals[t, h * D + c] = t * 10 + h + c / 10
+    vals = vals.half()
+    zeros = torch.zeros(rows, model, dtype=torch.float16)
+    o = _run(ctx, dev(zeros), dev(zeros), dev(vals), layout=("tokenMajor", model), heads=heads, Sq=rows, Sk=rows,
+             D=D, out_shape=(rows, model))
+    expect = vals.float().mean(0, keepdim=True).expand(rows, model)
+    assert float((o.float().cpu() - expect).abs().max()) <= 0.05
+
+
+def test_query_tiled_self_attention_hd64(ctx):
+    """AttentionExecutorTests.swift:28-62 generator (Q=K=1024, hd=64), tol 0.012."""
+    count, dim = 1024, 64
+    idx = torch.arange(count * dim, dtype=torch.float64)
+    q = (torch.sin(((idx * 13) % 997) * 0.017) * 0.25).half()
+    k = (torch.cos(((idx * 7) % 991) * 0.019) * 0.25).half()
+    v = ((((idx * 17) % 101) - 50) / 50).half()
+    o = _run(ctx, dev(q), dev(k), dev(v), layout="headMajor", heads=1, Sq=count, Sk=count, D=dim,
+             out_shape=(count, dim))
+    ref = oatt.sdpa(q.view(1, count, 1, dim), k.view(1, count, 1, dim), v.view(1, count, 1, dim))[0, :, 0]
+    err = float((o.float().cpu() - ref).abs().max())
+    assert err <= 0.012, err
+
+
+def test_flash_backend_rejects_non_dit_head_dim(ctx):
+    """AttentionExecutorTests.swift:404-423: the flash backend refuses loudly."""
+    heads, D, n = 4, 32, 4
+    buf = torch.zeros(n * heads * D, dtype=torch.float16, device="cuda")
+    ex = AttentionExecutor(ctx, layout=("tokenMajor", heads * D), backend="flash")
+    with pytest.raises(AnimaError) as e:
+        ex.execute(query=buf, key=buf, value=buf, output=buf, heads=heads, query_count=n, key_count=n, head_dim=D)
+    assert e.value.status == animaxs_amd._abi.E_UNSUPPORTED
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("Sq,Sk,causal", [(200, 77, False), (1, 1, False), (130, 130, True), (257, 700, False)])
+def test_flash_matches_oracle_ragged(ctx, D, Sq, Sk, causal):
+    g = torch.Generator().manual_seed(Sq * 1000 + Sk + D)
+    H = 3
+    q = torch.randn(1, H, Sq, D, generator=g).half()
+    k = torch.randn(1, H, Sk, D, generator=g).half()
+    v = torch.randn(1, H, Sk, D, generator=g).half()
+    outs = {}
+    for backend in ("flash", "generic"):
+        outs[backend] = _run(ctx, dev(q), dev(k), dev(v), layout="headMajor", heads=H, Sq=Sq, Sk=Sk, D=D,
+                             out_shape=(1, H, Sq, D), backend=backend, causal=causal)
+    ref = oatt.sdpa(q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3), causal=causal)
+    for backend, o in outs.items():
+        assert_attention_close(o.permute(0, 2, 1, 3), ref, label=f"{backend} D{D} Sq{Sq} Sk{Sk} causal={causal}")
+
+
+def test_generic_odd_head_dim_with_prologue(ctx):
+    """Generic path, head_dim 6 (even, not 64/128) with norm + RoPE prologue."""
+    g = torch.Generator().manual_seed(7)
+    B, S, H, D = 2, 37, 4, 6
+    q = torch.randn(B, S, H, D, generator=g).half()
+    k = torch.randn(B, S, H, D, generator=g).half()
+    v = torch.randn(B, S, H, D, generator=g).half()
+    w = (0.8 + 0.4 * torch.rand(D, generator=g)).half()
+    rope = orope.neox_rope_table(S, 1.0e4, D)
+    pro = QKPrologue(dev(w), dev(w), 1e-6, dev(rope), S, True, True)
+    o = _run(ctx, dev(q), dev(k), dev(v), layout=("tokenMajor", H * D), heads=H, Sq=S, Sk=S, D=D,
+             out_shape=(B, S, H, D), batch=B, prologue=pro)
+    qq = oatt.qk_prologue(q, w, 1e-6, rope)
+    kk = oatt.qk_prologue(k, w, 1e-6, rope)
+    ref = oatt.sdpa(qq, kk, v)
+    assert_attention_close(o, ref, label="generic D6 prologue")
+
+
+def test_validation_errors_do_not_launch(ctx):
+    """AttentionExecutor.validate (AttentionExecutor.swift:778-825) error contract."""
+    buf = torch.zeros(64, dtype=torch.float16, device="cuda")
+    ex = AttentionExecutor(ctx)
+    with pytest.raises(AnimaError) as e:
+        ex.execute(query=buf, key=buf, value=buf, output=buf, heads=2, query_count=4, key_count=3, head_dim=4,
+                   causal=True)
+    assert "invalid attention shape" in e.value.message
+    with pytest.raises(AnimaError) as e:
+        ex.execute(query=buf, key=buf, value=buf, output=buf, heads=4, query_count=8, key_count=8, head_dim=8)
+    assert e.value.status == animaxs_amd._abi.E_OUT_OF_BOUNDS

@@ -1,0 +1,91 @@
+"""GPU parity of the DiT block composition and its support kernels (through the C ABI).
+
+The block is compared with the oracle block run with fp16 boundaries
+(``--boundary-dtype fp16`` of scripts/dit_block0_oracle.py), i.e. rounding at the
+same places the HIP block stores fp16 activations; the residual is fp32 in both.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from animaxs_amd import BlockOps, DiTBlockExecutor
+from oracle import blocks, inputs, norms
+from tests.helpers import dev, device_weight, fp16_weight, max_abs, mean_rel
+
+pytestmark = pytest.mark.gpu
+
+BLOCK_MEAN_REL = 1e-3
+
+
+def _device_block(d):
+    keep = []
+    weights = {}
+    for name, w in d["w"].items():
+        qw, k = device_weight(w)
+        weights[name] = qw
+        keep.append(k)
+    for br in ("self", "cross", "mlp"):
+        for i in (1, 2):
+            qw, k = fp16_weight(d[f"mod_{br}_w{i}"])
+            weights[f"mod_{br}_w{i}"] = qw
+            keep.append(k)
+    norms_d = {n: dev(d[n]) for n in ("self_q_norm", "self_k_norm", "cross_q_norm", "cross_k_norm")}
+    return weights, norms_d, keep
+
+
+@pytest.mark.parametrize("S", [256, 4096])
+def test_dit_block_matches_oracle(ctx, S):
+    d = inputs.dit_block(S=S)
+    weights, norms_d, keep = _device_block(d)
+    residual = dev(d["x"].clone())
+    emb, adaln, ctxb, rope = dev(d["emb"]), dev(d["adaln"]), dev(d["ctx"]), dev(d["rope"])
+    blk = DiTBlockExecutor(ctx)
+    blk.encode(weights, norms_d, residual, emb, adaln, ctxb, rope, tokens=S)
+    torch.cuda.synchronize()
+    ref = blocks.dit_block(d, boundary="fp16")
+    y = residual.cpu()
+    assert torch.isfinite(y).all()
+    ma, mr = max_abs(y, ref), mean_rel(y, ref)
+    print(f"PARITY dit_block S{S}: max_abs={ma:.3e} mean_rel={mr:.3e} max_ref={float(ref.abs().max()):.3e}", flush=True)
+    assert mr <= BLOCK_MEAN_REL
+    assert ma <= 5e-3 * float(ref.abs().max())
+
+
+def test_layernorm_modulate_gelu_gate_add(ctx):
+    """dit_layernorm_modulate_to_half / dit_gelu_half_inplace / gate_add_half_f32 / silu / add_f32
+    (AnimaKernels.metal:477-524, 312-322, 624-634, 388-397, 649-656)."""
+    g = torch.Generator().manual_seed(3)
+    rows, n = 37, 2048
+    x = torch.randn(rows, n, generator=g) * 3 + 0.5
+    mod = torch.randn(3 * n, generator=g)
+    ops = BlockOps(ctx)
+    out = torch.zeros(rows, n, dtype=torch.float16, device="cuda")
+    ops.layernorm_modulate_to_half(dev(x), dev(mod), out, n, rows, 1e-6)
+    torch.cuda.synchronize()
+    ref = norms.layer_norm_modulated(x, mod[n:2 * n], mod[:n]).half()
+    diff = (out.cpu().float() - ref.float()).abs()
+    assert float(diff.max()) <= 2 ** -9 * float(ref.float().abs().max())
+
+    h = (torch.randn(4099, generator=g) * 4).half()
+    hd = dev(h)
+    ops.gelu_half_inplace(hd, h.numel())
+    torch.cuda.synchronize()
+    gref = norms.gelu_erf(h.float()).half()
+    assert float((hd.cpu().float() - gref.float()).abs().max()) <= 2 ** -9 * 8
+
+    res = torch.randn(rows, n, generator=g)
+    br = torch.randn(rows, n, generator=g).half()
+    gate = torch.randn(n, generator=g)
+    rd = dev(res.clone())
+    ops.gate_add_half_f32(rd, dev(br), dev(gate), n, rows * n)
+    torch.cuda.synchronize()
+    assert torch.allclose(rd.cpu(), res + br.float() * gate, atol=1e-5, rtol=1e-6)
+
+    e = torch.randn(2048, generator=g)
+    so = torch.zeros(2048, device="cuda")
+    ops.silu(dev(e), so, 2048)
+    a = dev(torch.ones(2048))
+    ops.add_f32(a, so, 2048)
+    torch.cuda.synchronize()
+    assert torch.allclose(a.cpu(), 1 + norms.silu(e), atol=1e-6, rtol=1e-5)

@@ -1,0 +1,245 @@
+"""GPU parity of the dequant / GEMM / matvec path against the oracle (through the C ABI).
+
+Bar: dequant is bit-exact (fp16 payloads identical); GEMMs match an fp64 product
+of the same fp16 activations and the exact RNE16 weights to within the fp16
+output rounding plus fp32 accumulation-order noise; the fp32 matvec follows the
+reference's own thresholds (LinearExecutorTests.swift:411-414,
+MetalExecutionTests.swift:110,165).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import animaxs_amd
+from animaxs_amd import AnimaError, LinearExecutor, QuantizedLinearWeightBuffers
+from oracle import inputs, quant
+from tests.helpers import dev, device_weight
+
+pytestmark = pytest.mark.gpu
+
+
+def _dequant_gpu(ctx, w, out_stride=None, guard=32):
+    qw, keep = device_weight(w)
+    stride = out_stride or w["cols"]
+    n = (w["rows"] - 1) * stride + w["cols"]
+    out = torch.full((n + guard,), float("nan"), dtype=torch.float16, device="cuda")
+    LinearExecutor.encode_dequant(ctx, qw, out, stride)
+    torch.cuda.synchronize()
+    bits = out.cpu().numpy().view(np.uint16)
+    assert np.all(bits[n:] == np.float16(np.nan).view(np.uint16)), "kernel wrote past the logical output"
+    rows = np.stack([bits[r * stride: r * stride + w["cols"]] for r in range(w["rows"])])
+    return rows
+
+
+def _wdict(storage, packed, scale_bits, zero_bits, rows, cols, stride):
+    return {"storage": storage, "packed": np.asarray(packed, np.uint8), "scale_bits": np.asarray(scale_bits, np.uint16),
+            "zero_bits": np.asarray(zero_bits, np.uint16), "rows": rows, "cols": cols, "row_stride": stride}
+
+
+def test_w4_kernel_known_answer(ctx):
+    """MetalExecutionTests.swift:28-65: 0x6E, scale 0.5, zero -0.25 -> 6.75, 2.75."""
+    w = _wdict(0, [0x6E], np.array([0.5], np.float16).view(np.uint16), np.array([-0.25], np.float16).view(np.uint16),
+               1, 2, 1)
+    bits = _dequant_gpu(ctx, w)
+    assert bits.view(np.float16).astype(np.float32).tolist() == [[6.75, 2.75]]
+
+
+def test_row_aware_dequant_bit_exact(ctx):
+    """MetalExecutionTests.swift:170-257 shapes (W4 [2,68], W8 [2,65]) with the guard tail."""
+    rows, cols = 2, 68
+    q = np.array([[(r * 7 + c) & 15 for c in range(cols)] for r in range(rows)], np.uint8)
+    s = np.array([0.5, 0.25, 1.0, 2.0], np.float16).view(np.uint16)
+    z = np.array([-1, 1, 3, -2], np.float16).view(np.uint16)
+    w4 = _wdict(0, quant.pack_w4(q), s, z, rows, cols, 34)
+    assert np.array_equal(_dequant_gpu(ctx, w4), quant.dequant_to_half(0, w4["packed"], s, z, rows, cols, 34))
+    cols = 65
+    p8 = np.array([(i * 13) & 255 for i in range(rows * cols)], np.uint8)
+    s8 = np.array([0.125, 0.5, 0.25, 2], np.float16).view(np.uint16)
+    z8 = np.array([-2, 1, 4, -3], np.float16).view(np.uint16)
+    w8 = _wdict(1, p8, s8, z8, rows, cols, cols)
+    assert np.array_equal(_dequant_gpu(ctx, w8), quant.dequant_to_half(1, p8, s8, z8, rows, cols, cols))
+
+
+@pytest.mark.parametrize("storage", [0, 1])
+def test_dequant_random_bit_exact_with_subnormals_and_padding(ctx, storage):
+    rng = np.random.default_rng(11 + storage)
+    rows, cols = 37, 200
+    stride = ((cols + 1) // 2 + 5) if storage == 0 else cols + 3
+    groups = (cols + 63) // 64
+    packed = rng.integers(0, 256, size=(rows, stride), dtype=np.uint8)
+    # mix of normal, subnormal and negative fp16 payloads (MetalExecutionTests.swift:115-168 class)
+    s = rng.integers(0, 0x7BFF, size=(rows, groups)).astype(np.uint16)
+    s[::3] = rng.integers(1, 0x03FF, size=s[::3].shape)
+    z = rng.integers(0, 0xFBFF, size=(rows, groups)).astype(np.uint16)
+    z[z >= 0x7C00] &= 0x83FF
+    w = _wdict(storage, packed, s, z, rows, cols, stride)
+    got = _dequant_gpu(ctx, w, out_stride=cols + 8)
+    ref = quant.dequant_to_half(storage, packed, s, z, rows, cols, stride)
+    bad = np.argwhere(got != ref)
+    for r, c in bad[:8]:
+        g = r * groups + c // 64
+        print(f"MISMATCH r={r} c={c} got={got[r, c]:#06x} ref={ref[r, c]:#06x} "
+              f"scale={s.reshape(-1)[g]:#06x} zero={z.reshape(-1)[g]:#06x}", flush=True)
+    assert len(bad) == 0
+
+
+def _gemm_ref(x16: torch.Tensor, w: dict) -> torch.Tensor:
+    """fp64 product of the fp16 activations and the exact RNE16 dequantized weights."""
+    wh = quant.dequant_to_half(w["storage"], w["packed"], w["scale_bits"], w["zero_bits"], w["rows"], w["cols"],
+                               w["row_stride"]).view(np.float16).astype(np.float64)
+    return torch.from_numpy(x16.double().numpy() @ wh.T)
+
+
+def _check_gemm(y: torch.Tensor, ref: torch.Tensor, label: str):
+    y = y.double().cpu()
+    # fp16 output rounding (half an ulp) + fp32 accumulation noise
+    tol = ref.abs() * 2.0 ** -10 + 1e-3 * float(ref.abs().max())
+    err = (y - ref).abs()
+    bad = int((err > tol).sum())
+    print(f"GEMM {label}: max_err={float(err.max()):.3e} max_ref={float(ref.abs().max()):.3e} "
+          f"mean_rel={float(err.sum() / ref.abs().sum()):.3e}", flush=True)
+    assert bad == 0, f"{label}: {bad} elements outside tolerance"
+    assert float(err.sum() / ref.abs().sum()) < 1e-3
+
+
+@pytest.mark.parametrize("backend", ["auto", "dequantizedGEMM"])
+@pytest.mark.parametrize("M,N,K", [(4096, 2048, 2048), (512, 2048, 1024), (300, 8192 // 4, 8192), (1, 2048, 2048),
+                                   (16, 8192, 2048), (64, 2048, 8192)])
+def test_w4_gemm_block_shapes(ctx, backend, M, N, K):
+    d = inputs.small_m_gemm(M, N, K)
+    qw, keep = device_weight(d["w"])
+    x = dev(d["x"])
+    y = torch.full((M, N), float("nan"), dtype=torch.float16, device="cuda")
+    LinearExecutor(ctx, backend=backend).execute(x, qw, y, M)
+    torch.cuda.synchronize()
+    _check_gemm(y, _gemm_ref(d["x"], d["w"]), f"W4 {backend} M{M} N{N} K{K}")
+
+
+def test_w8_padded_stride_tail_tile_and_guards(ctx):
+    """LinearExecutorTests.swift:33-103: W8, M=133 N=16 K=16, packed stride 20, byte offsets 32,
+    guard bytes on both sides of the output untouched."""
+    m, n, k, stride, pre = 133, 16, 16, 20, 32
+    xv = np.array([[((r * 3 + c * 5) % 17 - 8) / 8 for c in range(k)] for r in range(m)], np.float16)
+    packed = np.full(pre + n * stride + 32, 0xEE, np.uint8)
+    for r in range(n):
+        for c in range(k):
+            packed[pre + r * stride + c] = (r * 19 + c * 7) & 31
+    sc = np.zeros(pre // 2 + n + 16, np.float16)
+    ze = np.zeros(pre // 2 + n + 16, np.float16)
+    sc[pre // 2: pre // 2 + n] = [(r + 1) / 64 for r in range(n)]
+    ze[pre // 2: pre // 2 + n] = [(r - 3) / 16 for r in range(n)]
+    xbuf = np.concatenate([np.full(pre // 2, 7, np.float16), xv.reshape(-1), np.full(16, 7, np.float16)])
+    out = torch.full((pre // 2 + m * n + 16,), 0, dtype=torch.int16)
+    out.fill_(0x7B7B)
+    out_d = dev(out)
+    P, S, Z, X = dev(torch.from_numpy(packed)), dev(torch.from_numpy(sc.view(np.int16))), \
+        dev(torch.from_numpy(ze.view(np.int16))), dev(torch.from_numpy(xbuf))
+    qw = QuantizedLinearWeightBuffers(1, P, S, Z, n, k, stride, packed_offset=pre, scale_offset=pre, zero_offset=pre)
+    LinearExecutor(ctx).execute(X, qw, out_d, m, input_offset=pre, output_offset=pre)
+    torch.cuda.synchronize()
+    o = out_d.cpu()
+    assert torch.all(o[: pre // 2] == 0x7B7B) and torch.all(o[pre // 2 + m * n:] == 0x7B7B)
+    y = o[pre // 2: pre // 2 + m * n].numpy().view(np.float16).astype(np.float64).reshape(m, n)
+    w = _wdict(1, packed[pre: pre + n * stride], sc[pre // 2: pre // 2 + n].view(np.uint16),
+               ze[pre // 2: pre // 2 + n].view(np.uint16), n, k, stride)
+    ref = _gemm_ref(torch.from_numpy(xv), w).numpy()
+    assert np.abs(y - ref).max() <= 0.025
+
+
+def test_w4_nibble_order_and_padded_rows(ctx):
+    """LinearExecutorTests.swift:105-155: W4 M=3 N=16 K=16, packed stride 12 (pad 0xCC)."""
+    m, n, k, stride = 3, 16, 16, 12
+    xv = np.array([((i * 11) % 13 - 6) / 4 for i in range(m * k)], np.float16).reshape(m, k)
+    packed = np.full((n, stride), 0xCC, np.uint8)
+    for r in range(n):
+        for c in range(k):
+            q = (r * 5 + c * 3) & 15
+            b = packed[r, c // 2]
+            packed[r, c // 2] = ((b & 0xF0) | q) if c % 2 == 0 else ((b & 0x0F) | (q << 4))
+    sc = np.full(n, 0.125, np.float16).view(np.uint16)
+    ze = np.full(n, -0.5, np.float16).view(np.uint16)
+    w = _wdict(0, packed, sc, ze, n, k, stride)
+    qw, keep = device_weight(w)
+    y = torch.zeros((m, n), dtype=torch.float16, device="cuda")
+    LinearExecutor(ctx, tile_rows=2).execute(dev(torch.from_numpy(xv)), qw, y, m)
+    torch.cuda.synchronize()
+    ref = _gemm_ref(torch.from_numpy(xv), w)
+    assert float((y.double().cpu() - ref).abs().max()) <= 0.015
+
+
+def test_fp16_storage_gemm(ctx):
+    g = torch.Generator().manual_seed(5)
+    M, N, K = 257, 300, 192
+    x = torch.randn(M, K, generator=g).half()
+    w16 = (torch.randn(N, K, generator=g) * 0.05).half()
+    qw = QuantizedLinearWeightBuffers(2, dev(w16), dev(w16), dev(w16), N, K, K)
+    y = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+    LinearExecutor(ctx).execute(dev(x), qw, y, M)
+    torch.cuda.synchronize()
+    ref = torch.from_numpy(x.double().numpy() @ w16.double().numpy().T)
+    _check_gemm(y, ref, "FP16 storage")
+
+
+def test_linear_rejects_undersized_stride(ctx):
+    """LinearExecutorTests.swift:157-168."""
+    buf = torch.zeros(64, dtype=torch.uint8, device="cuda")
+    qw = QuantizedLinearWeightBuffers(0, buf, buf, buf, 1, 16, 7)
+    with pytest.raises(AnimaError) as e:
+        LinearExecutor(ctx).encode(buf, qw, buf, 1)
+    assert "row stride is too small" in e.value.message
+
+
+def test_matvec_w8_row_boundary_and_subnormal_metadata(ctx):
+    """MetalExecutionTests.swift:67-168: K=65 row boundary; fp16-subnormal scale/zero."""
+    rows, cols = 2, 65
+    cases = [
+        (np.array([(i * 17 + 3) & 255 for i in range(rows * cols)], np.uint8),
+         np.array([0.125, 0.5, 0.25, 2.0], np.float16).view(np.uint16),
+         np.array([-2.0, 1.0, 4.0, -3.0], np.float16).view(np.uint16),
+         np.array([(c % 11) * 0.125 - 0.5 for c in range(cols)], np.float32), 2e-3),
+        (np.array([(i * 29 + 17) & 255 for i in range(rows * cols)], np.uint8),
+         np.array([0x0001, 0x03FF, 0x0011, 0x0200], np.uint16),
+         np.array([0x8001, 0x0002, 0x8010, 0x03FF], np.uint16),
+         np.array([((c % 13) - 6) * 0.25 for c in range(cols)], np.float32), 2e-6),
+    ]
+    for packed, s, z, x, tol in cases:
+        w = _wdict(1, packed, s, z, rows, cols, cols)
+        qw, keep = device_weight(w)
+        y = torch.zeros(rows, dtype=torch.float32, device="cuda")
+        LinearExecutor.encode_matvec(ctx, qw, dev(torch.from_numpy(x)), y)
+        torch.cuda.synchronize()
+        ref = quant.dequant_w8_matrix(packed, s, z, rows, cols).astype(np.float64) @ x.astype(np.float64)
+        assert np.abs(y.cpu().numpy() - ref).max() <= tol
+
+
+@pytest.mark.parametrize("K", [2048, 8192])
+def test_matvec_w4_precision(ctx, K):
+    """LinearExecutorTests.swift:308-415 generator: direct matvec maxAbs < 1e-3 vs fp64."""
+    n, groups, stride = 16, K // 64, K // 2
+    state = (0xA51A0000 + K) & 0xFFFFFFFF
+    norm = 1 / np.sqrt(K)
+    xin = np.zeros(K, np.float32)
+    for c in range(K):
+        state = (state * 1664525 + 1013904223) & 0xFFFFFFFF
+        xin[c] = ((int((state >> 16) % 2001) - 1000) / 1000) * norm
+    packed = np.zeros((n, stride), np.uint8)
+    sc = np.zeros((n, groups), np.float16)
+    ze = np.zeros((n, groups), np.float16)
+    for r in range(n):
+        for g in range(groups):
+            sc[r, g] = (1 + (r + g) % 3) / 64
+            ze[r, g] = ((r + g) % 5 - 2) / 16
+        for c in range(K):
+            q = (r * 11 + c * 7 + c // 64 * 3) & 15
+            packed[r, c // 2] |= q if c % 2 == 0 else q << 4
+    w = _wdict(0, packed, sc.view(np.uint16), ze.view(np.uint16), n, K, stride)
+    qw, keep = device_weight(w)
+    y = torch.zeros(n, dtype=torch.float32, device="cuda")
+    LinearExecutor.encode_matvec(ctx, qw, dev(torch.from_numpy(xin)), y)
+    torch.cuda.synchronize()
+    ref = quant.dequant_w4_matrix(packed, sc.view(np.uint16), ze.view(np.uint16), n, K).astype(np.float64) @ xin.astype(np.float64)
+    got = y.cpu().numpy().astype(np.float64)
+    assert np.abs(got - ref).max() < 1e-3
+    cos = got @ ref / (np.linalg.norm(got) * np.linalg.norm(ref))
+    assert cos > 0.999999
