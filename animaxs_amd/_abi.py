@@ -44,7 +44,7 @@ class Buffer(C.Structure):
 
 class AttentionConfig(C.Structure):
     _fields_ = [("tile_rows", C.c_int32), ("numerics", C.c_int32), ("backend", C.c_int32),
-                ("layout", C.c_int32), ("token_stride", C.c_int64)]
+                ("layout", C.c_int32), ("token_stride", C.c_int64), ("flash_rows", C.c_int32)]
 
 
 class QKPrologue(C.Structure):

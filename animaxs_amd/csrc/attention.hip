@@ -7,6 +7,7 @@
 // rms_rope_split_half and rmsnorm_heads_half (AnimaXS/Shaders/AnimaKernels.metal:
 // 660-729, 1051-1185, 2069-2427).  Maths: O = softmax(scale * Q K^T + mask) V per
 // head, kv head = h / (heads / kv_heads) (AttentionExecutor.swift:222).
+#include <algorithm>
 #include <cmath>
 #include <vector>
 
@@ -416,17 +417,30 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(PrologueParams p) {
 // ===========================================================================
 // Host launchers.
 // ===========================================================================
-void launch_flash(const FlashParams& p, int D, int batch, hipStream_t stream) {
+// Number of compute units the 256-row variant must cover to be chosen by default.
+constexpr int64_t F2_MIN_BLOCKS = 256;
+
+void launch_flash(FlashParams p, int D, int batch, int flash_rows, hipStream_t stream) {
+  if (D != 128 && D != 64) fail(ANIMA_E_UNSUPPORTED, "flash attention requires head_dim 64 or 128");
+  const int64_t t256 = (int64_t)((p.Sq + FLASH_V2_ROWS - 1) / FLASH_V2_ROWS) * p.H * batch;
+  // The 256-row kernel addresses one 64-key tile with 32-bit byte offsets.
+  const bool v2_fits = 64 * std::max(p.k_tok, p.v_tok) * (int64_t)sizeof(half_t) < ((int64_t)1 << 31);
+  if (flash_rows == 256 && !v2_fits)
+    fail(ANIMA_E_INVALID_SHAPE, "256-row flash attention requires 64 key rows to span < 2 GiB");
+  const bool v2 = flash_rows == 256 || (flash_rows == 0 && v2_fits && t256 >= F2_MIN_BLOCKS);
+  p.q_tiles = v2 ? (p.Sq + FLASH_V2_ROWS - 1) / FLASH_V2_ROWS : (p.Sq + FA_BM - 1) / FA_BM;
   const int64_t blocks = (int64_t)p.q_tiles * p.H * batch;
   if (blocks <= 0) return;
   if (blocks > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "attention grid too large");
-  dim3 grid((unsigned)blocks), block(FA_NT);
-  if (D == 128)
-    hipLaunchKernelGGL(flash_attention_kernel<128>, grid, block, 0, stream, p);
-  else if (D == 64)
-    hipLaunchKernelGGL(flash_attention_kernel<64>, grid, block, 0, stream, p);
-  else
-    fail(ANIMA_E_UNSUPPORTED, "flash attention requires head_dim 64 or 128");
+  const dim3 grid((unsigned)blocks);
+  if (v2) {
+    launch_flash_v2(p, D, grid, stream);
+  } else {
+    if (D == 128)
+      hipLaunchKernelGGL(flash_attention_kernel<128>, grid, dim3(FA_NT), 0, stream, p);
+    else
+      hipLaunchKernelGGL(flash_attention_kernel<64>, grid, dim3(FA_NT), 0, stream, p);
+  }
   ANIMA_HIP(hipGetLastError());
 }
 

@@ -38,7 +38,11 @@ struct PrologueParams {
   const float* rope;
 };
 
-void launch_flash(const FlashParams& p, int D, int batch, hipStream_t stream);
+void launch_flash(FlashParams p, int D, int batch, int flash_rows, hipStream_t stream);
+
+// 256-row flash variant (attention_v2.hip); p.q_tiles counts 256-row tiles.
+constexpr int FLASH_V2_ROWS = 256;
+void launch_flash_v2(const FlashParams& p, int D, dim3 grid, hipStream_t stream);
 void launch_generic(const FlashParams& p, int D, int batch, hipStream_t stream);
 void launch_prologue(const PrologueParams& p, hipStream_t stream);
 

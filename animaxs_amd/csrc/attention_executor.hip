@@ -17,6 +17,8 @@ AttentionExecutor::AttentionExecutor(anima_ctx* ctx, const anima_attention_confi
     fail(ANIMA_E_INVALID_ARGUMENT, "unknown attention backend");
   if (cfg.layout != ANIMA_LAYOUT_HEAD_MAJOR && cfg.layout != ANIMA_LAYOUT_TOKEN_MAJOR)
     fail(ANIMA_E_INVALID_ARGUMENT, "unknown attention layout");
+  if (cfg.flash_rows != 0 && cfg.flash_rows != 128 && cfg.flash_rows != 256)
+    fail(ANIMA_E_INVALID_ARGUMENT, "flash_rows must be 0 (auto), 128 or 256");
 }
 
 int64_t AttentionExecutor::maximum_score_scratch_bytes(int64_t key_count, int64_t query_count) const {
@@ -198,8 +200,7 @@ void AttentionExecutor::encode(const anima_attention_args& a) {
     p.rope = rope_q;
   }
   if (use_flash) {
-    p.q_tiles = (int)((Sq + 127) / 128);
-    launch_flash(p, (int)D, (int)B, stream);
+    launch_flash(p, (int)D, (int)B, cfg_.flash_rows, stream);
   } else {
     launch_generic(p, (int)D, (int)B, stream);
   }

@@ -138,7 +138,7 @@ void launch_add(float* dst, const float* src, int64_t count, hipStream_t stream)
 DitBlockExecutor::DitBlockExecutor(anima_ctx* ctx)
     : ctx_(ctx),
       attention_(ctx, anima_attention_config{128, ANIMA_NUMERICS_FP32_SCORES, ANIMA_ATTENTION_BACKEND_AUTO,
-                                             ANIMA_LAYOUT_TOKEN_MAJOR, 0}),
+                                             ANIMA_LAYOUT_TOKEN_MAJOR, 0, 0}),
       linear_(ctx, anima_linear_config{128, ANIMA_LINEAR_BACKEND_AUTO}) {}
 
 static anima_buffer sub(char* base, int64_t off, int64_t bytes) { return anima_buffer{base + off, bytes}; }

@@ -117,9 +117,9 @@ class AttentionExecutor:
     ``"headMajor"`` or ``("tokenMajor", token_stride)``."""
 
     def __init__(self, context: Context, tile_rows: int = 128, numerics: str = "legacy",
-                 layout: Any = "headMajor", backend: str = "auto"):
+                 layout: Any = "headMajor", backend: str = "auto", flash_rows: int = 0):
         lay, ts = self._layout(layout)
-        cfg = _abi.AttentionConfig(int(tile_rows), _NUMERICS[numerics], _BACKENDS[backend], lay, ts)
+        cfg = _abi.AttentionConfig(int(tile_rows), _NUMERICS[numerics], _BACKENDS[backend], lay, ts, int(flash_rows))
         h = C.c_void_p()
         call("anima_attention_create", context.handle, C.byref(cfg), C.byref(h))
         self._h = h

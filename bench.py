@@ -1,0 +1,350 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention + W4 linear hot path (one GPU).
+
+Headline: DiT self-attention at S=4096 (1x64x64 patch grid), B=1, H=16, D=128,
+fp16 in/out, per-head RMSNorm on Q/K and 3-D RoPE fused in — TFLOP/s and the
+fraction of the fp16 dense MFMA peak — plus ms per full DiT block (hidden 2048,
+S=4096, 512-token context, all ten linears W4 group-64).
+
+One "step" = one attention call on fresh synthetic inputs already resident in
+HBM (4 rotating input sets, 256 MiB, so the 256 MB Infinity Cache does not hold
+a step's inputs).  Prints ONE JSON line.  The CPU baseline is the repository's
+torch-CPU fp32 oracle timed on the same workload on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "DiT self-attn TFLOP/s + % fp16 MFMA peak at S=4096; ms per DiT block (1 GPU)"
+FP16_PEAK_TFLOPS = 2516.6   # 256 CU x 4096 FLOP/clk x 2.4 GHz, dense
+HBM_PEAK_GBS = 8000.0
+B, H, D, S = 1, 16, 128, 4096
+SIDE = 64
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--block-steps", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-block", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the per-workload table")
+    return ap.parse_args()
+
+
+def attn_flops(Sq, Sk, heads=H, batch=B, d=D):
+    return 4.0 * batch * heads * Sq * Sk * d
+
+
+def gen_attention_inputs(torch, sets, seed=1002):
+    """Workload: Q/K/V ~N(0,1) fp16 [1,4096,16,128], norm weights ~U(0.8,1.2)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    out = []
+    for _ in range(sets):
+        q = torch.randn(B, S, H, D, device="cuda", generator=g).half()
+        k = torch.randn(B, S, H, D, device="cuda", generator=g).half()
+        v = torch.randn(B, S, H, D, device="cuda", generator=g).half()
+        o = torch.empty(B, S, H, D, device="cuda", dtype=torch.float16)
+        out.append((q, k, v, o))
+    qw = (0.8 + 0.4 * torch.rand(D, device="cuda", generator=g)).half()
+    kw = (0.8 + 0.4 * torch.rand(D, device="cuda", generator=g)).half()
+    return out, qw, kw
+
+
+def time_region(torch, stream, fn, steps, warmup):
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        fn(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per step
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the attention/W4 hot path is "
+              "benchmarked per GPU and multi-GPU sharding is a design note, not a measured mode.", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    import animaxs_amd as A
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.init()
+    dev_name = torch.cuda.get_device_name(0)
+    stream = torch.cuda.current_stream()
+    ctx = A.Context(0, stream)
+    print(f"# device {dev_name}", file=sys.stderr, flush=True)
+
+    # ---------------- headline: S=4096 self-attention with fused norm+RoPE ----------------
+    sets, qw, kw = gen_attention_inputs(torch, 4)
+    rope = torch.from_numpy(A.DitRoPE.generate(1, SIDE, SIDE)).cuda()
+    pro = A.QKPrologue(qw, kw, 1e-6, rope, S, True, True)
+    ex = A.AttentionExecutor(ctx, layout=("tokenMajor", H * D), backend="flash")
+
+    def step(i):
+        q, k, v, o = sets[i % len(sets)]
+        ex.encode(query=q, key=k, value=v, output=o, heads=H, query_count=S, key_count=S, head_dim=D, prologue=pro)
+
+    ms = time_region(torch, stream, step, args.steps, args.warmup)
+    flops = attn_flops(S, S)
+    tflops = flops / (ms * 1e-3) / 1e12
+    print(f"# self-attn S4096 (norm+rope, incl. K prologue): {ms:.4f} ms  {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+
+    # Dominant kernel alone: the flash kernel with Q norm+RoPE fused and K given already
+    # normalised (torch maths on device, input preparation only), so each encode is
+    # exactly one flash launch and the event pair brackets back-to-back launches.
+    pro_q = A.QKPrologue(qw, None, 1e-6, rope, S, True, False)
+    knorm = []
+    c_ = rope[:, :, 0, 0][None, :, None, :]
+    s_ = rope[:, :, 1, 0][None, :, None, :]
+    for (q, k, v, o) in sets:
+        kf = k.float()
+        kf = kf * torch.rsqrt(kf.pow(2).mean(-1, keepdim=True) + 1e-6) * kw.float()
+        a, bb = kf[..., :64], kf[..., 64:]
+        knorm.append(torch.cat([c_ * a - s_ * bb, s_ * a + c_ * bb], dim=-1).half().contiguous())
+
+    def kstep(i):
+        q, k, v, o = sets[i % len(sets)]
+        ex.encode(query=q, key=knorm[i % len(sets)], value=v, output=o, heads=H, query_count=S, key_count=S,
+                  head_dim=D, prologue=pro_q)
+
+    kms = time_region(torch, stream, kstep, args.steps, args.warmup)
+    k_tflops = flops / (kms * 1e-3) / 1e12
+    print(f"# flash kernel alone: {kms:.4f} ms  {k_tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+
+    roofline = {
+        "bound": "mfma", "kernel": "flash_attention_v2_kernel<128>", "achieved": round(k_tflops, 2),
+        "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(k_tflops / FP16_PEAK_TFLOPS, 4),
+        "traffic": load_traffic(), "flops_per_launch": flops, "avg_launch_ms": round(kms, 5),
+    }
+
+    extra = {}
+    if not args.no_extra:
+        extra = other_workloads(torch, A, ctx, stream, args)
+
+    block_ms = None
+    if not args.no_block:
+        block_ms = time_block(torch, A, ctx, stream, args)
+        print(f"# DiT block S4096: {block_ms:.3f} ms", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline()
+
+    line = {
+        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": "dit_self_attention_1024px", "batch": B, "heads": H, "head_dim": D, "seq_len": S,
+                   "qk_rmsnorm": True, "rope": "dit3d 1x64x64", "layout": "token-major stride 2048",
+                   "includes": "K RMSNorm+RoPE prologue kernel + flash kernel (Q norm+RoPE fused)"},
+        "mfma_peak_frac": round(tflops / FP16_PEAK_TFLOPS, 4),
+        "dit_block_ms": None if block_ms is None else round(block_ms, 4),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "workloads": extra,
+        "device": dev_name,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def load_traffic():
+    """HBM bytes per flash launch from the committed rocprofv3 --pmc summary, or None."""
+    p = os.path.join(ROOT, "profiles", "flash_attention_s4096_traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def other_workloads(torch, A, ctx, stream, args):
+    """ms/call and throughput of the other attention workloads (parity configs) and the
+    small-M W4 GEMMs, each against its binding roofline."""
+    res = {}
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1001)
+    # workload 1: S=1024 plain self-attention
+    q, k, v = (torch.randn(1, 1024, H, D, device="cuda", generator=g).half() for _ in range(3))
+    o = torch.empty_like(q)
+    ex = A.AttentionExecutor(ctx, layout=("tokenMajor", H * D), backend="flash")
+    ms = time_region(torch, stream, lambda i: ex.encode(query=q, key=k, value=v, output=o, heads=H, query_count=1024,
+                                                        key_count=1024, head_dim=D), args.steps, args.warmup)
+    f = attn_flops(1024, 1024)
+    res["self_attention_s1024"] = {"ms": round(ms, 5), "tflops": round(f / ms / 1e9, 2),
+                                   "mfma_frac": round(f / ms / 1e9 / FP16_PEAK_TFLOPS, 4)}
+    # workload 3: cross attention B4, 4096 queries, 512 keys, masked, q/k RMSNorm
+    g.manual_seed(1003)
+    sets = []
+    for _ in range(4):
+        q = torch.randn(4, 4096, H, D, device="cuda", generator=g).half()
+        k = torch.randn(4, 512, H, D, device="cuda", generator=g).half()
+        v = torch.randn(4, 512, H, D, device="cuda", generator=g).half()
+        sets.append((q, k, v, torch.empty_like(q)))
+    nw = (0.8 + 0.4 * torch.rand(D, device="cuda", generator=g)).half()
+    lengths = torch.randint(77, 513, (4,), generator=torch.Generator().manual_seed(1003)).int().numpy()
+    pro = A.QKPrologue(nw, nw, 1e-6, None, 0, False, False)
+    ex3 = A.AttentionExecutor(ctx, layout=("tokenMajor", H * D), backend="flash")
+
+    def s3(i):
+        q, k, v, o = sets[i % 4]
+        ex3.encode(query=q, key=k, value=v, output=o, heads=H, query_count=4096, key_count=512, head_dim=D, batch=4,
+                   key_lengths=lengths, prologue=pro)
+
+    ms = time_region(torch, stream, s3, args.steps, args.warmup)
+    L = [int(x) for x in lengths]
+    f = sum(4.0 * H * 4096 * l * D for l in L)
+    byts = 2.0 * (4 * 4096 * H * D * 2) + sum(2.0 * l * H * D * 2 for l in L)
+    res["cross_attention_b4_masked"] = {"ms": round(ms, 5), "tflops": round(f / ms / 1e9, 2),
+                                        "gbs": round(byts / ms / 1e6, 1), "key_lengths": L,
+                                        "hbm_frac": round(byts / ms / 1e6 / HBM_PEAK_GBS, 4),
+                                        "mfma_frac": round(f / ms / 1e9 / FP16_PEAK_TFLOPS, 4)}
+    # workload 4: Qwen causal GQA B4 S512, head-major, norm + rope 1e6, right padding
+    g.manual_seed(1004)
+    qh = torch.randn(4, 16, 512, D, device="cuda", generator=g).half()
+    kh = torch.randn(4, 8, 512, D, device="cuda", generator=g).half()
+    vh = torch.randn(4, 8, 512, D, device="cuda", generator=g).half()
+    oh = torch.empty_like(qh)
+    rq = torch.from_numpy(A.qwen_rope(512)).cuda()
+    lens = torch.randint(8, 513, (4,), generator=torch.Generator().manual_seed(1004)).int().numpy()
+    pro4 = A.QKPrologue(nw, nw, 1e-6, rq, 512, True, True)
+    ex4 = A.AttentionExecutor(ctx, layout="headMajor", backend="flash")
+    ms = time_region(torch, stream, lambda i: ex4.encode(query=qh, key=kh, value=vh, output=oh, heads=16, query_count=512,
+                                                         key_count=512, head_dim=D, key_value_heads=8, causal=True,
+                                                         batch=4, key_lengths=lens, prologue=pro4),
+                     args.steps, args.warmup)
+    pairs = sum(sum(min(i + 1, int(l)) for i in range(512)) for l in lens)
+    f = 4.0 * D * 16 * pairs
+    byts = (4 * 16 * 512 * D * 2) * 2 + (4 * 8 * 512 * D * 2) * 2
+    res["qwen_causal_gqa_b4_s512_per_layer"] = {"ms": round(ms, 5), "tflops": round(f / ms / 1e9, 2),
+                                                "gbs": round(byts / ms / 1e6, 1), "key_lengths": [int(x) for x in lens]}
+    # small-M W4 GEMMs (HBM-bound): rotate weight sets so > 512 MB is touched per sweep
+    lin = A.LinearExecutor(ctx)
+    for (M, N, K) in [(1, 8192, 2048), (16, 8192, 2048), (64, 8192, 2048), (4096, 2048, 2048), (4096, 8192, 2048)]:
+        nsets = max(1, min(64, (600 << 20) // (N * K // 2)))
+        ws = []
+        for _ in range(nsets):
+            p = torch.randint(0, 256, (N, K // 2), device="cuda", dtype=torch.uint8)
+            sc = (0.005 + 0.015 * torch.rand(N, K // 64, device="cuda")).half()
+            z = (-8 * sc.float()).half()
+            ws.append((A.QuantizedLinearWeightBuffers(0, p, sc, z, N, K, K // 2), p, sc, z))
+        x = torch.randn(M, K, device="cuda").half()
+        y = torch.empty(M, N, device="cuda", dtype=torch.float16)
+        ms = time_region(torch, stream, lambda i: lin.encode(x, ws[i % nsets][0], y, M), max(args.steps, nsets),
+                         args.warmup)
+        byts = N * K / 2 + 2 * 2 * N * (K // 64) + 2 * M * K + 2 * M * N
+        f = 2.0 * M * N * K
+        res[f"w4_gemm_m{M}_n{N}_k{K}"] = {"ms": round(ms, 5), "gbs": round(byts / ms / 1e6, 1),
+                                          "hbm_frac": round(byts / ms / 1e6 / HBM_PEAK_GBS, 4),
+                                          "tflops": round(f / ms / 1e9, 2),
+                                          "mfma_frac": round(f / ms / 1e9 / FP16_PEAK_TFLOPS, 4)}
+    for k_, v_ in res.items():
+        print(f"# {k_}: {v_}", file=sys.stderr, flush=True)
+    return res
+
+
+def time_block(torch, A, ctx, stream, args):
+    """ms per DiT block at S=4096 (all linears W4 symmetric int4, group 64)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1005)
+    dim, hidden, T, C = 2048, 8192, 512, 1024
+    keep = []
+
+    def w4(n, k):
+        p = torch.randint(0, 256, (n, k // 2), device="cuda", generator=g, dtype=torch.uint8)
+        sc = (0.005 + 0.015 * torch.rand(n, k // 64, device="cuda", generator=g)).half()
+        z = (-8 * sc.float()).half()
+        keep.extend([p, sc, z])
+        return A.QuantizedLinearWeightBuffers(0, p, sc, z, n, k, k // 2)
+
+    def f16(n, k):
+        w = (0.02 * torch.randn(n, k, device="cuda", generator=g)).half()
+        keep.append(w)
+        return A.QuantizedLinearWeightBuffers(2, w, w, w, n, k, k)
+
+    shapes = {"self_q": (dim, dim), "self_k": (dim, dim), "self_v": (dim, dim), "self_o": (dim, dim),
+              "cross_q": (dim, dim), "cross_k": (dim, C), "cross_v": (dim, C), "cross_o": (dim, dim),
+              "mlp1": (hidden, dim), "mlp2": (dim, hidden)}
+    weights = {n: w4(*s) for n, s in shapes.items()}
+    for br in ("self", "cross", "mlp"):
+        weights[f"mod_{br}_w1"] = f16(256, dim)
+        weights[f"mod_{br}_w2"] = f16(3 * dim, 256)
+    norms = {n: (0.8 + 0.4 * torch.rand(128, device="cuda", generator=g)).half()
+             for n in ("self_q_norm", "self_k_norm", "cross_q_norm", "cross_k_norm")}
+    residual = torch.randn(S, dim, device="cuda", generator=g)
+    emb = torch.randn(dim, device="cuda", generator=g)
+    adaln = torch.randn(3 * dim, device="cuda", generator=g)
+    ctxt = torch.randn(T, C, device="cuda", generator=g).half()
+    rope = torch.from_numpy(A.DitRoPE.generate(1, SIDE, SIDE)).cuda()
+    blk = A.DiTBlockExecutor(ctx)
+
+    def step(i):
+        blk.encode(weights, norms, residual, emb, adaln, ctxt, rope, tokens=S)
+
+    return time_region(torch, stream, step, args.block_steps, 2)
+
+
+def cpu_baseline():
+    """The torch-CPU fp32 oracle on the headline workload (all 16 heads, S=4096, norm+RoPE),
+    median of up to 3 timed runs after one warm-up, on this host's torch threads."""
+    import torch
+    from oracle import attention as oatt
+    from oracle import inputs as oin
+    threads = torch.get_num_threads()
+    d = oin.self_attention(2)
+
+    def run():
+        qq = oatt.qk_prologue(d["q"], d["q_norm_w"], d["eps"], d["rope"])
+        kk = oatt.qk_prologue(d["k"], d["k_norm_w"], d["eps"], d["rope"])
+        return oatt.sdpa(qq, kk, d["v"])
+
+    t0 = time.perf_counter()
+    run()
+    first = time.perf_counter() - t0
+    times = []
+    budget = 30.0
+    spent = first
+    while len(times) < 3 and spent + first < budget:
+        t0 = time.perf_counter()
+        run()
+        dt = time.perf_counter() - t0
+        times.append(dt)
+        spent += dt
+    if not times:
+        times = [first]
+    times.sort()
+    med = times[len(times) // 2]
+    tf = attn_flops(S, S) / med / 1e12
+    try:
+        model = next((l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")), "?")
+    except OSError:
+        model = "?"
+    print(f"# cpu oracle: {med:.3f} s/call ({tf:.4f} TFLOP/s) on {threads} threads", file=sys.stderr, flush=True)
+    return {"value": round(tf, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"full workload: S=4096 H=16 D=128 self-attention with q/k RMSNorm + DiT RoPE, fp32 torch "
+                      f"oracle, median of {len(times)} run(s) after 1 warm-up",
+            "ms_per_call": round(med * 1e3, 2), "cpu_model": model, "torch": torch.__version__}
+
+
+if __name__ == "__main__":
+    main()

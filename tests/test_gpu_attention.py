@@ -20,9 +20,9 @@ from tests.helpers import assert_attention_close, dev
 pytestmark = pytest.mark.gpu
 
 
-def _run(ctx, q, k, v, *, layout, heads, Sq, Sk, D, out_shape, backend="auto", **kw):
+def _run(ctx, q, k, v, *, layout, heads, Sq, Sk, D, out_shape, backend="auto", flash_rows=0, **kw):
     o = torch.full(out_shape, float("nan"), dtype=torch.float16, device="cuda")
-    ex = AttentionExecutor(ctx, layout=layout, backend=backend)
+    ex = AttentionExecutor(ctx, layout=layout, backend=backend, flash_rows=flash_rows)
     ex.execute(query=q, key=k, value=v, output=o, heads=heads, query_count=Sq, key_count=Sk, head_dim=D, **kw)
     torch.cuda.synchronize()
     return o
@@ -168,7 +168,8 @@ def test_flash_backend_rejects_non_dit_head_dim(ctx):
 
 
 @pytest.mark.parametrize("D", [64, 128])
-@pytest.mark.parametrize("Sq,Sk,causal", [(200, 77, False), (1, 1, False), (130, 130, True), (257, 700, False)])
+@pytest.mark.parametrize("Sq,Sk,causal", [(200, 77, False), (1, 1, False), (130, 130, True), (257, 700, False),
+                                          (600, 600, True), (513, 33, False)])
 def test_flash_matches_oracle_ragged(ctx, D, Sq, Sk, causal):
     g = torch.Generator().manual_seed(Sq * 1000 + Sk + D)
     H = 3
@@ -176,12 +177,33 @@ def test_flash_matches_oracle_ragged(ctx, D, Sq, Sk, causal):
     k = torch.randn(1, H, Sk, D, generator=g).half()
     v = torch.randn(1, H, Sk, D, generator=g).half()
     outs = {}
-    for backend in ("flash", "generic"):
-        outs[backend] = _run(ctx, dev(q), dev(k), dev(v), layout="headMajor", heads=H, Sq=Sq, Sk=Sk, D=D,
-                             out_shape=(1, H, Sq, D), backend=backend, causal=causal)
+    for name, backend, rows in (("flash128", "flash", 128), ("flash256", "flash", 256), ("generic", "generic", 0)):
+        outs[name] = _run(ctx, dev(q), dev(k), dev(v), layout="headMajor", heads=H, Sq=Sq, Sk=Sk, D=D,
+                          out_shape=(1, H, Sq, D), backend=backend, flash_rows=rows, causal=causal)
     ref = oatt.sdpa(q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3), causal=causal)
-    for backend, o in outs.items():
-        assert_attention_close(o.permute(0, 2, 1, 3), ref, label=f"{backend} D{D} Sq{Sq} Sk{Sk} causal={causal}")
+    for name, o in outs.items():
+        assert_attention_close(o.permute(0, 2, 1, 3), ref, label=f"{name} D{D} Sq{Sq} Sk{Sk} causal={causal}")
+
+
+@pytest.mark.parametrize("flash_rows", [128, 256])
+def test_flash_variants_masked_batch_gqa(ctx, flash_rows):
+    """Both flash variants on batch + GQA + causal + right-padding key lengths + prologue."""
+    g = torch.Generator().manual_seed(99)
+    B, S, H, Hkv, D = 3, 700, 4, 2, 128
+    q = torch.randn(B, H, S, D, generator=g).half()
+    k = torch.randn(B, Hkv, S, D, generator=g).half()
+    v = torch.randn(B, Hkv, S, D, generator=g).half()
+    w = (0.8 + 0.4 * torch.rand(D, generator=g)).half()
+    rope = orope.neox_rope_table(S, 1.0e6, D)
+    L = [700, 301, 64]
+    pro = QKPrologue(dev(w), dev(w), 1e-6, dev(rope), S, True, True)
+    o = _run(ctx, dev(q), dev(k), dev(v), layout="headMajor", heads=H, Sq=S, Sk=S, D=D, out_shape=(B, H, S, D),
+             backend="flash", flash_rows=flash_rows, batch=B, key_value_heads=Hkv, causal=True, key_lengths=L,
+             prologue=pro)
+    qq = oatt.qk_prologue(q.permute(0, 2, 1, 3), w, 1e-6, rope)
+    kk = oatt.qk_prologue(k.permute(0, 2, 1, 3), w, 1e-6, rope)
+    ref = oatt.sdpa(qq, kk, v.permute(0, 2, 1, 3), causal=True, key_lengths=L)
+    assert_attention_close(o.permute(0, 2, 1, 3), ref, label=f"flash{flash_rows} batch gqa causal masked")
 
 
 def test_generic_odd_head_dim_with_prologue(ctx):
