@@ -40,6 +40,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-block", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the per-workload table")
+    ap.add_argument("--profile-kernel", action="store_true",
+                    help="only launch the dominant flash kernel (--warmup + --steps times) and a 256 MiB "
+                         "calibration copy, for rocprofv3 counter passes; prints no JSON")
     return ap.parse_args()
 
 
@@ -106,10 +109,12 @@ def main():
         q, k, v, o = sets[i % len(sets)]
         ex.encode(query=q, key=k, value=v, output=o, heads=H, query_count=S, key_count=S, head_dim=D, prologue=pro)
 
-    ms = time_region(torch, stream, step, args.steps, args.warmup)
     flops = attn_flops(S, S)
-    tflops = flops / (ms * 1e-3) / 1e12
-    print(f"# self-attn S4096 (norm+rope, incl. K prologue): {ms:.4f} ms  {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    if not args.profile_kernel:
+        ms = time_region(torch, stream, step, args.steps, args.warmup)
+        tflops = flops / (ms * 1e-3) / 1e12
+        print(f"# self-attn S4096 (norm+rope, incl. K prologue): {ms:.4f} ms  {tflops:.1f} TFLOP/s", file=sys.stderr,
+              flush=True)
 
     # Dominant kernel alone: the flash kernel with Q norm+RoPE fused and K given already
     # normalised (torch maths on device, input preparation only), so each encode is
@@ -128,6 +133,19 @@ def main():
         q, k, v, o = sets[i % len(sets)]
         ex.encode(query=q, key=knorm[i % len(sets)], value=v, output=o, heads=H, query_count=S, key_count=S,
                   head_dim=D, prologue=pro_q)
+
+    if args.profile_kernel:
+        for i in range(args.warmup + args.steps):
+            kstep(i)
+        torch.cuda.synchronize()
+        # calibration: a plain copy of known size (256 MiB read + 256 MiB written)
+        src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"# profile-kernel: {args.warmup + args.steps} flash launches, 3 x 256 MiB copies", file=sys.stderr)
+        return
 
     kms = time_region(torch, stream, kstep, args.steps, args.warmup)
     k_tflops = flops / (kms * 1e-3) / 1e12
@@ -171,11 +189,14 @@ def main():
 
 def load_traffic():
     """HBM bytes per flash launch from the committed rocprofv3 --pmc summary, or None."""
-    p = os.path.join(ROOT, "profiles", "flash_attention_s4096_traffic.json")
+    p = os.path.join(ROOT, "profiles", "flash_attention_v2_s4096_traffic.md")
     if not os.path.exists(p):
         return None
     with open(p) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+        for line in f:
+            if line.startswith("hbm_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    return None
 
 
 def other_workloads(torch, A, ctx, stream, args):

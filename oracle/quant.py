@@ -39,6 +39,13 @@ def fp16_bits_to_f32(bits) -> np.ndarray:
     return np.asarray(bits, dtype=np.uint16).view(np.float16).astype(np.float32)
 
 
+def _u8(data) -> np.ndarray:
+    """Byte payload (bytes-like or array) as a flat uint8 array."""
+    if isinstance(data, (bytes, bytearray, memoryview)):
+        return np.frombuffer(bytes(data), dtype=np.uint8)
+    return np.asarray(data, dtype=np.uint8).reshape(-1)
+
+
 def _w4_nibbles(packed_rows: np.ndarray, cols: int) -> np.ndarray:
     """Even K index -> low nibble, odd K index -> high nibble
     (QuantDecoders.swift:7-8, :36, :74)."""
@@ -50,7 +57,7 @@ def _w4_nibbles(packed_rows: np.ndarray, cols: int) -> np.ndarray:
 
 def dequant_w4(data, scale_bits, zero_bits, k: int, group: int = GROUP) -> np.ndarray:
     """Flat W4 decode (QuantDecoders.swift:23-48): group = i / group (no row reset)."""
-    d = np.frombuffer(bytes(data), dtype=np.uint8) if not isinstance(data, np.ndarray) else data.astype(np.uint8)
+    d = _u8(data)
     if k == 0:
         return np.zeros(0, np.float32)
     i = np.arange(k)
@@ -63,7 +70,7 @@ def dequant_w4(data, scale_bits, zero_bits, k: int, group: int = GROUP) -> np.nd
 
 def dequant_w8(data, scale_bits, zero_bits, k: int, group: int = GROUP) -> np.ndarray:
     """Flat W8 decode (QuantDecoders.swift:90-114)."""
-    d = np.frombuffer(bytes(data), dtype=np.uint8) if not isinstance(data, np.ndarray) else data.astype(np.uint8)
+    d = _u8(data)
     if k == 0:
         return np.zeros(0, np.float32)
     i = np.arange(k)
@@ -85,7 +92,7 @@ def dequant_w4_matrix(packed, scale_bits, zero_bits, rows: int, cols: int,
     ``(cols+1)//2`` and may be padded (LinearExecutor.swift:423-425 allows
     ``packedRowStride >= (K+1)/2``).  Groups index ``r*ceil(cols/64) + c/64``."""
     stride = (cols + 1) // 2 if row_stride is None else row_stride
-    p = np.asarray(packed, dtype=np.uint8).reshape(-1)[: rows * stride].reshape(rows, stride)
+    p = _u8(packed)[: rows * stride].reshape(rows, stride)
     groups = (cols + group - 1) // group
     q = _w4_nibbles(p[:, : (cols + 1) // 2], cols).astype(np.float32)
     gidx = np.arange(cols) // group
@@ -98,7 +105,7 @@ def dequant_w8_matrix(packed, scale_bits, zero_bits, rows: int, cols: int,
                       row_stride: int | None = None, group: int = GROUP) -> np.ndarray:
     """Row-aware W8 decode (QuantDecoders.swift:117-147; quant.py:55-76)."""
     stride = cols if row_stride is None else row_stride
-    p = np.asarray(packed, dtype=np.uint8).reshape(-1)[: rows * stride].reshape(rows, stride)
+    p = _u8(packed)[: rows * stride].reshape(rows, stride)
     groups = (cols + group - 1) // group
     q = p[:, :cols].astype(np.float32)
     gidx = np.arange(cols) // group
