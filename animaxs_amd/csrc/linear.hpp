@@ -49,6 +49,12 @@ struct QWeightView {
 QWeightView validate_weight(const anima_qweight& w, const char* who);
 
 void launch_gemm(const GemmParams& p, int storage, hipStream_t stream);
+
+// Weight-streaming GEMM for M <= SMALLM_MAX_ROWS (linear_smallm.hip); requires K a
+// multiple of 128 and 16-byte aligned X and weight rows.
+constexpr int SMALLM_MAX_ROWS = 64;
+bool smallm_supported(const GemmParams& p, int storage);
+void launch_smallm(const GemmParams& p, int storage, hipStream_t stream);
 void launch_matvec(const MatvecParams& p, hipStream_t stream);
 void launch_dequant(const DequantParams& p, hipStream_t stream);
 

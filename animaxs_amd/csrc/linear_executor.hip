@@ -94,7 +94,10 @@ void LinearExecutor::encode(anima_buffer input, int64_t input_offset, const anim
   p.scale = w.scale;
   p.zero = w.zero;
   p.row_stride = w.row_stride;
-  launch_gemm(p, w.storage, stream);
+  if (smallm_supported(p, w.storage))
+    launch_smallm(p, w.storage, stream);
+  else
+    launch_gemm(p, w.storage, stream);
 }
 
 void encode_matvec(anima_ctx* ctx, const anima_qweight& weight, anima_buffer input, int64_t input_offset,

@@ -243,3 +243,64 @@ def test_matvec_w4_precision(ctx, K):
     assert np.abs(got - ref).max() < 1e-3
     cos = got @ ref / (np.linalg.norm(got) * np.linalg.norm(ref))
     assert cos > 0.999999
+
+
+def _affine_weight(storage: int, N: int, K: int, seed: int, pad: int = 0) -> dict:
+    """Random affine weight (codes, fp16 scale/zero) in the pack layout, optional row padding."""
+    rng = np.random.default_rng(seed)
+    groups = (K + 63) // 64
+    s = (rng.random((N, groups)) * 0.02 + 0.002).astype(np.float16).view(np.uint16)
+    z = ((rng.random((N, groups)) - 0.5) * 0.2).astype(np.float16).view(np.uint16)
+    if storage == 0:
+        q = rng.integers(0, 16, (N, K)).astype(np.uint8)
+        stride = (K + 1) // 2 + pad
+        packed = quant.pack_w4(q, stride, pad_value=0xA5)
+    elif storage == 1:
+        stride = K + pad
+        packed = np.full((N, stride), 0x5A, np.uint8)
+        packed[:, :K] = rng.integers(0, 256, (N, K)).astype(np.uint8)
+    else:
+        stride = K + pad // 2
+        w16 = np.full((N, stride), np.float16(7.0), np.float16)
+        w16[:, :K] = (rng.standard_normal((N, K)) * 0.05).astype(np.float16)
+        packed = w16.view(np.uint8)
+    return _wdict(storage, packed, s, z, N, K, stride)
+
+
+@pytest.mark.parametrize("storage", [0, 1, 2])
+@pytest.mark.parametrize("M,N,K,pad", [(1, 2048, 2048, 0), (5, 1000, 384, 16), (16, 8192, 2048, 0),
+                                       (17, 130, 1280, 32), (33, 2048, 1024, 0), (64, 2048, 8192, 0),
+                                       (64, 4000, 2048, 16)])
+def test_small_m_weight_stream_gemm(ctx, storage, M, N, K, pad):
+    """M <= 64 with K a multiple of 128 takes the weight-streaming kernel: every storage, ragged N,
+    padded row strides; the output's neighbours stay untouched."""
+    w = _affine_weight(storage, N, K, seed=M * 1000 + N + K + storage, pad=pad)
+    qw, keep = device_weight(w)
+    g = torch.Generator().manual_seed(M + N)
+    x = torch.randn(M, K, generator=g).half()
+    guard = 8
+    out = torch.full((M * N + 2 * guard,), float("nan"), dtype=torch.float16, device="cuda")
+    print(f"SMALLM storage={storage} M={M} N={N} K={K} pad={pad}", flush=True)
+    LinearExecutor(ctx).execute(dev(x), qw, out, M, output_offset=2 * guard)
+    torch.cuda.synchronize()
+    o = out.cpu()
+    assert torch.isnan(o[:guard]).all() and torch.isnan(o[guard + M * N:]).all()
+    _check_gemm(o[guard: guard + M * N].reshape(M, N), _gemm_ref(x, w), f"small-M s{storage} M{M} N{N} K{K}")
+
+
+def test_small_m_unaligned_output_and_repeat(ctx):
+    """An output offset of one half (not 8-byte aligned) takes the scalar store path; two calls in a
+    row give identical bits (fixed-order reduction)."""
+    M, N, K = 3, 260, 512
+    w = _affine_weight(0, N, K, seed=11)
+    qw, keep = device_weight(w)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(2)).half()
+    out = torch.zeros(M * N + 1, dtype=torch.float16, device="cuda")
+    ex = LinearExecutor(ctx)
+    ex.execute(dev(x), qw, out, M, output_offset=2)
+    first = out.clone()
+    ex.execute(dev(x), qw, out, M, output_offset=2)
+    torch.cuda.synchronize()
+    assert torch.equal(first.view(torch.int16), out.view(torch.int16))
+    assert float(out[0]) == 0.0
+    _check_gemm(out[1:].reshape(M, N), _gemm_ref(x, w), "small-M unaligned")
