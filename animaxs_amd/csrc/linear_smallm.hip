@@ -34,6 +34,8 @@ struct SmallMParams {
 };
 
 constexpr int SM_CHUNK = 128;
+constexpr int SMALLM_MAX_STEPS = 8;   // steps per wave, each of NCH chunks
+constexpr int SM_PARAM_REGS = 8;      // scale (and zero) halfs each thread stages into LDS
 
 template <int STORAGE>
 struct SmallMChunk {
@@ -41,14 +43,40 @@ struct SmallMChunk {
   static constexpr int WORDS = STORAGE == ANIMA_STORAGE_W4 ? 4 : (STORAGE == ANIMA_STORAGE_W8 ? 8 : 16);
 };
 
-__device__ __forceinline__ half_t dq1(uint32_t q, float s, float z) {
-  return f32_to_f16(fmaf((float)q, s, z));
+// One weight value: half(fl32(q*s + z)), the reference decoder's two roundings.
+// With ONE_ROUNDING the fp32 step is skipped (the compiler may fuse multiply, add and
+// conversion into v_fma_mix); the caller only asks for that when q*s + z is exact in
+// fp32 (one_rounding_exact), where both give the same bits.
+template <bool ONE_ROUNDING>
+__device__ __forceinline__ half_t dq1(uint32_t q, half_t s, half_t z) {
+  if constexpr (ONE_ROUNDING)
+    return (half_t)fmaf((float)q, (float)s, (float)z);
+  else
+    return f32_to_f16(fmaf((float)q, (float)s, (float)z));
+}
+
+// Exponent of the unit in the last place of an fp16 value, as a biased field (1..31).
+__device__ __forceinline__ int fp16_unit_exponent(half_t v) {
+  const int e = (__builtin_bit_cast(uint16_t, v) >> 10) & 31;
+  return e < 1 ? 1 : e;
+}
+
+// True when q*s + z is exactly representable in fp32 for every code q < 2^QBITS.
+// q*s is an integer of at most QBITS+11 bits times s's unit, z one of at most 11
+// bits times its own unit; their sum spans at most 24 bits exactly when the unit
+// exponents differ by d = u(s) - u(z) with -12 <= d <= 12 - QBITS (or when s or z
+// is zero).
+template <int QBITS>
+__device__ __forceinline__ bool one_rounding_exact(half_t s, half_t z) {
+  if ((__builtin_bit_cast(uint16_t, s) & 0x7fff) == 0 || (__builtin_bit_cast(uint16_t, z) & 0x7fff) == 0) return true;
+  const int d = fp16_unit_exponent(s) - fp16_unit_exponent(z);
+  return d >= -12 && d <= 12 - QBITS;
 }
 
 // A fragment t (k = 32g + 8t .. +7 of the chunk) from a lane's raw weight words.
-template <int STORAGE>
-__device__ __forceinline__ half8v dequant_frag(const uint32_t (&wv)[SmallMChunk<STORAGE>::WORDS], int t, float s,
-                                               float z) {
+template <int STORAGE, bool ONE_ROUNDING>
+__device__ __forceinline__ half8v dequant_frag(const uint32_t (&wv)[SmallMChunk<STORAGE>::WORDS], int t, half_t s,
+                                               half_t z) {
   half8v a;
   if constexpr (STORAGE == ANIMA_STORAGE_W4) {
     const uint32_t d = wv[t];
@@ -56,15 +84,15 @@ __device__ __forceinline__ half8v dequant_frag(const uint32_t (&wv)[SmallMChunk<
     const uint32_t hi = (d >> 4) & 0x0F0F0F0Fu;   // odd k
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      a[2 * b] = dq1((lo >> (8 * b)) & 0xFFu, s, z);
-      a[2 * b + 1] = dq1((hi >> (8 * b)) & 0xFFu, s, z);
+      a[2 * b] = dq1<ONE_ROUNDING>((lo >> (8 * b)) & 0xFFu, s, z);
+      a[2 * b + 1] = dq1<ONE_ROUNDING>((hi >> (8 * b)) & 0xFFu, s, z);
     }
   } else if constexpr (STORAGE == ANIMA_STORAGE_W8) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const uint32_t d = wv[2 * t + h];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) a[4 * h + b] = dq1((d >> (8 * b)) & 0xFFu, s, z);
+      for (int b = 0; b < 4; ++b) a[4 * h + b] = dq1<ONE_ROUNDING>((d >> (8 * b)) & 0xFFu, s, z);
     }
   } else {
     const u32x4 raw = {wv[4 * t], wv[4 * t + 1], wv[4 * t + 2], wv[4 * t + 3]};
@@ -80,14 +108,15 @@ constexpr int smallm_max_waves() { return MB == 1 ? 16 : 8; }
 // Chunks preloaded per step, bounded by the registers the raw weight words take.
 template <int STORAGE, int MB>
 constexpr int smallm_max_chunks() {
-  return MB == 1 ? (STORAGE == ANIMA_STORAGE_W4 ? 8 : 4)
-                 : (STORAGE == ANIMA_STORAGE_W4 ? 4 : (STORAGE == ANIMA_STORAGE_W8 ? 2 : 1));
+  return STORAGE == ANIMA_STORAGE_W8 ? 1 : (MB <= 2 ? 2 : 1);
 }
 
-template <int STORAGE, int MB, int R, int NCH>
+template <int STORAGE, int MB, int R, int NCH, int NST>
 __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kernel(SmallMParams p) {
   constexpr int WORDS = SmallMChunk<STORAGE>::WORDS;
-  extern __shared__ float red[];   // [S][R*MB][4][64]
+  // Dynamic LDS: the S x R*MB partial-sum tiles of the final reduction, then the
+  // workgroup's scale and zero rows ([16R][groups] halfs each).
+  extern __shared__ float red[];   // [S][R*MB][4][64], then scale, zero
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int S = blockDim.x >> 6;
@@ -98,14 +127,31 @@ __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kerne
 
   // Rows past N re-read row N-1 (computed, never stored).
   const uint8_t* wrow[R];
-  const half_t* srow[R];
-  const half_t* zrow[R];
 #pragma unroll
   for (int rb = 0; rb < R; ++rb) {
     const int n = min(n0 + rb * 16 + r, p.N - 1);
     wrow[rb] = p.w + (int64_t)n * p.row_stride * (STORAGE == ANIMA_STORAGE_FP16 ? 2 : 1);
-    srow[rb] = p.scale + (int64_t)n * p.groups;
-    zrow[rb] = p.zero + (int64_t)n * p.groups;
+  }
+  // Scale / zero of the workgroup's 16R rows are one contiguous run of the
+  // [N][groups] arrays: copy them into LDS with coalesced loads (lanes read
+  // consecutive halfs) rather than one scattered 2-byte load per lane and chunk.
+  constexpr int PAIRS = R * MB;
+  half_t* s_lds = reinterpret_cast<half_t*>(red + S * PAIRS * 4 * 64);
+  half_t* z_lds = s_lds + 16 * R * p.groups;
+  const int nrows = min(16 * R, p.N - n0);
+  const int nparam = nrows * p.groups;
+  constexpr int PARAM_REGS = SM_PARAM_REGS;
+  half_t sreg[PARAM_REGS], zreg[PARAM_REGS];
+  if constexpr (STORAGE != ANIMA_STORAGE_FP16) {
+    const half_t* sbase = p.scale + (int64_t)n0 * p.groups;
+    const half_t* zbase = p.zero + (int64_t)n0 * p.groups;
+#pragma unroll
+    for (int i = 0; i < PARAM_REGS; ++i) {
+      const int e = threadIdx.x + i * (int)blockDim.x;
+      const int ec = min(e, nparam - 1);
+      sreg[i] = sbase[ec];
+      zreg[i] = zbase[ec];
+    }
   }
   const half_t* xrow[MB];
   bool xvalid[MB];
@@ -122,68 +168,129 @@ __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kerne
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[rb][mb] = floatx4{};
 
-  for (int kbeg = kslice; kbeg < kstop; kbeg += NCH * SM_CHUNK) {
-  // Issue every weight load of this step (NCH chunks) before any arithmetic, so
-  // their HBM latency is paid once per step.
-  uint32_t wv[NCH][R][WORDS];
-  float sc[NCH][R], zc[NCH][R];
+  // One step = NCH chunks whose weight words are loaded together.  Steps are
+  // double-buffered: the next step's loads are in flight while this step's
+  // dequantization and MFMAs run, so a wave pays HBM latency about once.  Every
+  // load is unconditional (chunks past the slice re-read its last chunk and are
+  // masked through zero X), which keeps the in-order load counter exact: a wait
+  // for this step never waits for the next step's loads.
+  struct Step {
+    uint32_t wv[NCH][R][WORDS];
+  };
+  constexpr int STEP_K = NCH * SM_CHUNK;
+  const int klast = kstop - SM_CHUNK;   // start of the slice's last chunk (every wave has one)
+
+  auto load_step = [&](int step, Step& st) {
+    const int kbeg = kslice + step * STEP_K;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int kl = kbeg + c * SM_CHUNK + 32 * g;
-    const bool live = kbeg + c * SM_CHUNK < kstop;
+    for (int c = 0; c < NCH; ++c) {
+      const int kl = min(kbeg + c * SM_CHUNK, klast) + 32 * g;
 #pragma unroll
-    for (int rb = 0; rb < R; ++rb) {
-      const int64_t boff = STORAGE == ANIMA_STORAGE_W4 ? kl / 2 : (STORAGE == ANIMA_STORAGE_W8 ? kl : 2 * kl);
-      const u32x4* src = reinterpret_cast<const u32x4*>(wrow[rb] + (live ? boff : 0));
+      for (int rb = 0; rb < R; ++rb) {
+        const int64_t boff = STORAGE == ANIMA_STORAGE_W4 ? kl / 2 : (STORAGE == ANIMA_STORAGE_W8 ? kl : 2 * kl);
+        const u32x4* src = reinterpret_cast<const u32x4*>(wrow[rb] + boff);
 #pragma unroll
-      for (int v = 0; v < WORDS / 4; ++v) {
-        const u32x4 t4 = __builtin_nontemporal_load(src + v);
-        wv[c][rb][4 * v] = t4[0];
-        wv[c][rb][4 * v + 1] = t4[1];
-        wv[c][rb][4 * v + 2] = t4[2];
-        wv[c][rb][4 * v + 3] = t4[3];
+        for (int v = 0; v < WORDS / 4; ++v) {
+          const u32x4 t4 = __builtin_nontemporal_load(src + v);
+          st.wv[c][rb][4 * v] = t4[0];
+          st.wv[c][rb][4 * v + 1] = t4[1];
+          st.wv[c][rb][4 * v + 2] = t4[2];
+          st.wv[c][rb][4 * v + 3] = t4[3];
+        }
       }
-      if constexpr (STORAGE != ANIMA_STORAGE_FP16) {
-        const int gi = live ? (kl >> 6) : 0;
-        sc[c][rb] = (float)srow[rb][gi];
-        zc[c][rb] = (float)zrow[rb][gi];
+    }
+  };
+
+  // X fragments of chunk c of a step; rows past M and chunks past the slice are
+  // loaded from valid addresses and zeroed with a mask (no branch around the load).
+  auto load_x = [&](int step, int c, half8v (&xf)[MB][4]) {
+    const int kc = kslice + step * STEP_K + c * SM_CHUNK;
+    const uint32_t live = kc < kstop ? 0xffffffffu : 0u;
+    const int kl = min(kc, klast) + 32 * g;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const uint32_t mask = xvalid[mb] ? live : 0u;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        u32x4 v = *reinterpret_cast<const u32x4*>(xrow[mb] + kl + 8 * t);
+        v &= mask;
+        xf[mb][t] = __builtin_bit_cast(half8v, v);
+      }
+    }
+  };
+
+  // Order per iteration: this step's X fragments (L2), then the next step's weight
+  // prefetch (HBM), then the arithmetic.  Loads retire in issue order, so waiting for
+  // X and this step's weights never waits for the prefetch.
+  auto compute_step = [&](int step, const Step& st, const half8v (&xs)[NCH][MB][4]) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int kl = min(kslice + step * STEP_K + c * SM_CHUNK, klast) + 32 * g;
+      half_t sc[R], zc[R];
+#pragma unroll
+      for (int rb = 0; rb < R; ++rb) {
+        if constexpr (STORAGE != ANIMA_STORAGE_FP16) {
+          const int li = (rb * 16 + r) * p.groups + (kl >> 6);
+          sc[rb] = s_lds[li];
+          zc[rb] = z_lds[li];
+        } else {
+          sc[rb] = zc[rb] = (half_t)0.f;
+        }
+      }
+      constexpr int QBITS = STORAGE == ANIMA_STORAGE_W4 ? 4 : 8;
+      bool fast = true;
+#pragma unroll
+      for (int rb = 0; rb < R; ++rb) fast = fast && one_rounding_exact<QBITS>(sc[rb], zc[rb]);
+      half8v a[R][4];
+      if (__all(fast)) {
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) a[rb][t] = dequant_frag<STORAGE, true>(st.wv[c][rb], t, sc[rb], zc[rb]);
       } else {
-        sc[c][rb] = zc[c][rb] = 0.f;
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) a[rb][t] = dequant_frag<STORAGE, false>(st.wv[c][rb], t, sc[rb], zc[rb]);
+      }
+#pragma unroll
+      for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) acc[rb][mb] = mfma16(a[rb][t], xs[c][mb][t], acc[rb][mb]);
+    }
+  };
+
+  // NST steps, fully unrolled (straight-line code keeps every wait exact) and
+  // ping-ponged; steps past the slice re-read its last chunk and multiply zero X.
+  Step sa, sb;
+  half8v xs[NCH][MB][4];
+  load_step(0, sa);
+  // Park the scale/zero copy in LDS (waits only for those loads, issued before the
+  // weight loads) and make it visible to every wave.
+  if constexpr (STORAGE != ANIMA_STORAGE_FP16) {
+#pragma unroll
+    for (int i = 0; i < PARAM_REGS; ++i) {
+      const int e = threadIdx.x + i * (int)blockDim.x;
+      if (e < nparam) {
+        s_lds[(e / p.groups) * p.groups + e % p.groups] = sreg[i];
+        z_lds[(e / p.groups) * p.groups + e % p.groups] = zreg[i];
       }
     }
   }
-
-  auto load_x = [&](int c, half8v (&xf)[MB][4]) {
-    const int kl = kbeg + c * SM_CHUNK + 32 * g;
-    const bool live = kbeg + c * SM_CHUNK < kstop;
+  __syncthreads();
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+  for (int step = 0; step < NST; ++step) {
+    Step& cur = (step & 1) ? sb : sa;
+    Step& nxt = (step & 1) ? sa : sb;
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        xf[mb][t] = (live && xvalid[mb]) ? *reinterpret_cast<const half8v*>(xrow[mb] + kl + 8 * t) : half8v{};
-  };
-
-  half8v xa[MB][4], xb[MB][4];
-  load_x(0, xa);
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    half8v (&xc)[MB][4] = (c & 1) ? xb : xa;
-    half8v (&xn)[MB][4] = (c & 1) ? xa : xb;
-    if (c + 1 < NCH) load_x(c + 1, xn);
-    // A chunk past K has zero X, so its (clamped, in-bounds) weight bytes add nothing.
-#pragma unroll
-    for (int rb = 0; rb < R; ++rb)
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const half8v a = dequant_frag<STORAGE>(wv[c][rb], t, sc[c][rb], zc[c][rb]);
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[rb][mb] = mfma16(a, xc[mb][t], acc[rb][mb]);
-      }
-  }
+    for (int c = 0; c < NCH; ++c) load_x(step, c, xs[c]);
+    if (step + 1 < NST) load_step(step + 1, nxt);
+    compute_step(step, cur, xs);
   }
 
   // Fixed-order reduction of the S K-slices through LDS.
-  constexpr int PAIRS = R * MB;
 #pragma unroll
   for (int pi = 0; pi < PAIRS; ++pi)
 #pragma unroll
@@ -214,49 +321,79 @@ __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kerne
   }
 }
 
-template <int STORAGE, int MB, int R, int NCH>
-static void launch_smallm_t(SmallMParams p, hipStream_t stream) {
-  // About 2048 waves over the grid, at most smallm_max_waves per workgroup, a K
-  // slice per wave of whole steps of NCH chunks, and a reduction buffer
-  // (S x R*MB KiB) within 64 KiB of LDS.
+template <int STORAGE, int MB, int R, int NCH, int NST>
+static void launch_smallm_t(SmallMParams p, int S, hipStream_t stream) {
+  p.kw = NCH * NST * SM_CHUNK;
   const int wgs = (p.N + 16 * R - 1) / (16 * R);
-  const int chunks = p.K / SM_CHUNK;
-  const int max_s = std::min(smallm_max_waves<MB>(), 64 / (R * MB));
-  const int want_s = std::max(1, std::min(max_s, 2048 / std::max(1, wgs)));
-  const int steps = (chunks + NCH - 1) / NCH;
-  const int steps_per_wave = (steps + want_s - 1) / want_s;
-  p.kw = steps_per_wave * NCH * SM_CHUNK;
-  const int S = (p.K + p.kw - 1) / p.kw;
-  const size_t lds = (size_t)S * R * MB * 4 * 64 * sizeof(float);
-  hipLaunchKernelGGL((smallm_gemm_kernel<STORAGE, MB, R, NCH>), dim3(wgs), dim3(64 * S), lds, stream, p);
+  const size_t lds = (size_t)S * R * MB * 4 * 64 * sizeof(float) + (size_t)2 * 16 * R * p.groups * sizeof(half_t);
+  hipLaunchKernelGGL((smallm_gemm_kernel<STORAGE, MB, R, NCH, NST>), dim3(wgs), dim3(64 * S), lds, stream, p);
 }
 
-template <int STORAGE, int MB, int R>
-static void launch_smallm_r(const SmallMParams& p, hipStream_t stream) {
+template <int STORAGE, int MB>
+constexpr int smallm_rows() { return MB == 2 ? 2 : 1; }
+
+// Waves per workgroup (S) times chunks per wave (NCH x NST) must cover K; the
+// fewest chunks per wave wins (the most waves share the dequantization), within
+// smallm_max_waves and a reduction buffer (S x R*MB KiB) of at most 64 KiB.
+template <int STORAGE, int MB>
+static int smallm_steps(int K, int* S) {
+  constexpr int R = smallm_rows<STORAGE, MB>();
   constexpr int NCH = smallm_max_chunks<STORAGE, MB>();
-  // Fewer chunks per step when K is short, so waves are not left empty.
-  const int chunks = p.K / SM_CHUNK;
-  if (NCH >= 8 && chunks <= 16 * 4)
-    launch_smallm_t<STORAGE, MB, R, (NCH >= 4 ? 4 : NCH)>(p, stream);
-  else
-    launch_smallm_t<STORAGE, MB, R, NCH>(p, stream);
+  const int chunks = K / SM_CHUNK;
+  const int max_s = std::min(smallm_max_waves<MB>(), 64 / (R * MB));
+  const int groups = (K + 63) / 64;
+  for (int nst = 1; nst <= SMALLM_MAX_STEPS; nst *= 2) {
+    const int per = NCH * nst;
+    const int s = (chunks + per - 1) / per;
+    // the scale/zero copy: 16R rows x groups halfs over 64*S threads
+    if (s <= max_s && 16 * R * groups <= SM_PARAM_REGS * 64 * s) {
+      *S = s;
+      return nst;
+    }
+  }
+  return 0;
+}
+
+template <int STORAGE, int MB>
+static void launch_smallm_r(const SmallMParams& p, hipStream_t stream) {
+  constexpr int R = smallm_rows<STORAGE, MB>();
+  constexpr int NCH = smallm_max_chunks<STORAGE, MB>();
+  int S = 0;
+  switch (smallm_steps<STORAGE, MB>(p.K, &S)) {
+    case 1: launch_smallm_t<STORAGE, MB, R, NCH, 1>(p, S, stream); break;
+    case 2: launch_smallm_t<STORAGE, MB, R, NCH, 2>(p, S, stream); break;
+    case 4: launch_smallm_t<STORAGE, MB, R, NCH, 4>(p, S, stream); break;
+    case 8: launch_smallm_t<STORAGE, MB, R, NCH, 8>(p, S, stream); break;
+    default: fail(ANIMA_E_UNSUPPORTED, "small-M GEMM: K too large for the weight-streaming kernel");
+  }
 }
 
 template <int STORAGE>
 static void launch_smallm_s(const SmallMParams& p, hipStream_t stream) {
-  const int MB = (p.M + 15) / 16;
-  switch (MB) {
-    case 1: launch_smallm_r<STORAGE, 1, 1>(p, stream); break;
-    case 2: launch_smallm_r<STORAGE, 2, 2>(p, stream); break;
-    case 3: launch_smallm_r<STORAGE, 3, 2>(p, stream); break;
-    default: launch_smallm_r<STORAGE, 4, 2>(p, stream); break;
+  switch ((p.M + 15) / 16) {
+    case 1: launch_smallm_r<STORAGE, 1>(p, stream); break;
+    case 2: launch_smallm_r<STORAGE, 2>(p, stream); break;
+    case 3: launch_smallm_r<STORAGE, 3>(p, stream); break;
+    default: launch_smallm_r<STORAGE, 4>(p, stream); break;
+  }
+}
+
+template <int STORAGE>
+static bool smallm_fits(int M, int K) {
+  int S = 0;
+  switch ((M + 15) / 16) {
+    case 1: return smallm_steps<STORAGE, 1>(K, &S) > 0;
+    case 2: return smallm_steps<STORAGE, 2>(K, &S) > 0;
+    case 3: return smallm_steps<STORAGE, 3>(K, &S) > 0;
+    default: return smallm_steps<STORAGE, 4>(K, &S) > 0;
   }
 }
 
 bool smallm_supported(const GemmParams& p, int storage) {
   if (p.M < 1 || p.M > SMALLM_MAX_ROWS || p.K % SM_CHUNK != 0 || !aligned16(p.x) || !aligned16(p.w)) return false;
-  if (storage == ANIMA_STORAGE_FP16) return p.row_stride % 8 == 0;
-  return p.row_stride % 16 == 0;
+  if (storage == ANIMA_STORAGE_FP16) return p.row_stride % 8 == 0 && smallm_fits<ANIMA_STORAGE_FP16>(p.M, p.K);
+  if (p.row_stride % 16 != 0) return false;
+  return storage == ANIMA_STORAGE_W4 ? smallm_fits<ANIMA_STORAGE_W4>(p.M, p.K) : smallm_fits<ANIMA_STORAGE_W8>(p.M, p.K);
 }
 
 void launch_smallm(const GemmParams& g, int storage, hipStream_t stream) {

@@ -304,3 +304,66 @@ def test_small_m_unaligned_output_and_repeat(ctx):
     assert torch.equal(first.view(torch.int16), out.view(torch.int16))
     assert float(out[0]) == 0.0
     _check_gemm(out[1:].reshape(M, N), _gemm_ref(x, w), "small-M unaligned")
+
+
+def _one_hot_params(rng, N: int, groups: int) -> tuple:
+    """fp16 scale/zero bit patterns per (row, group): ordinary values, subnormals, zeros and
+    pairs whose exponents differ by up to 20 (q*s + z no longer exact in fp32)."""
+    kinds = rng.integers(0, 6, (N, groups))
+    s = np.zeros((N, groups), np.float16)
+    z = np.zeros((N, groups), np.float16)
+    base = (rng.random((N, groups)) * 0.02 + 0.001)
+    gap = 2.0 ** rng.integers(9, 21, (N, groups))
+    sign = np.where(rng.random((N, groups)) < 0.5, -1.0, 1.0)
+    s[kinds == 0] = base[kinds == 0]
+    z[kinds == 0] = (-8 * base * sign)[kinds == 0]
+    s[kinds == 1] = (base * 64)[kinds == 1]                         # |z| far below s
+    z[kinds == 1] = (base * 64 / gap * sign)[kinds == 1]
+    s[kinds == 2] = (base / 64)[kinds == 2]                         # |z| far above s
+    z[kinds == 2] = (base / 64 * gap * sign)[kinds == 2]
+    sb, zb = s.view(np.uint16), z.view(np.uint16)
+    sub = kinds == 3                                                # subnormal scale / zero
+    sb[sub] = rng.integers(1, 0x400, int(sub.sum())).astype(np.uint16)
+    zb[sub] = (rng.integers(1, 0x400, int(sub.sum())) | (rng.integers(0, 2, int(sub.sum())) << 15)).astype(np.uint16)
+    s[kinds == 4] = base[kinds == 4]                                # zero offset
+    z[kinds == 4] = 0
+    s[kinds == 5] = 0                                               # zero scale
+    z[kinds == 5] = (base * sign)[kinds == 5]
+    return sb.copy(), zb.copy()
+
+
+@pytest.mark.parametrize("storage", [0, 1])
+@pytest.mark.parametrize("M", [64, 128])
+def test_gemm_dequant_bit_exact_via_one_hot(ctx, storage, M):
+    """Row m of X is one-hot at column k_m, so y[m, n] = deq(W)[n, k_m] exactly (a single
+    1*w product in fp32): the GEMM's in-register dequantization must reproduce the oracle's
+    RNE16(fl32(q*s + z)) bit for bit, including the fallback taken when q*s + z is not exact in
+    fp32.  M=64 runs the weight-streaming kernel, M=128 the tiled GEMM."""
+    rng = np.random.default_rng(40 + storage + M)
+    N, K = 384, 1024
+    groups = K // 64
+    sb, zb = _one_hot_params(rng, N, groups)
+    if storage == 0:
+        packed = quant.pack_w4(rng.integers(0, 16, (N, K)).astype(np.uint8))
+        stride = K // 2
+    else:
+        packed = rng.integers(0, 256, (N, K)).astype(np.uint8)
+        stride = K
+    w = _wdict(storage, packed, sb, zb, N, K, stride)
+    ks = rng.choice(K, M, replace=False)
+    x = np.zeros((M, K), np.float16)
+    x[np.arange(M), ks] = 1.0
+    qw, keep = device_weight(w)
+    y = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+    LinearExecutor(ctx).execute(dev(torch.from_numpy(x)), qw, y, M)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    want = quant.dequant_to_half(storage, packed, sb, zb, N, K, stride).view(np.float16)[:, ks].T
+    finite = np.isfinite(want)
+    mism = np.argwhere(finite & (got != want))
+    for m, n in mism[:8]:
+        g = n * groups + ks[m] // 64
+        print(f"MISMATCH m={m} n={n} k={ks[m]} got={got[m, n]!r} want={want[m, n]!r} "
+              f"scale={sb.reshape(-1)[g]:#06x} zero={zb.reshape(-1)[g]:#06x}", flush=True)
+    assert len(mism) == 0
+    assert finite.mean() > 0.99

@@ -314,3 +314,46 @@ def test_w4_nibble_order_padded_rows_linear_case():
     want = x.astype(np.float64) @ deq.T
     got = _linear_oracle(x, Q.STORAGE_W4, packed, s, z, n, k, stride)
     assert np.max(np.abs(got - want)) == 0.0
+
+
+# --- the exactness condition the GEMM kernels use to round once -----------------------
+
+def _unit_exp(bits):
+    e = (bits.astype(np.int32) >> 10) & 31
+    return np.maximum(e, 1)
+
+
+@pytest.mark.parametrize("qbits", [4, 8])
+def test_one_rounding_condition_implies_fp32_exact(qbits):
+    """The GEMMs round q*s + z once (straight to fp16) when the fp16 unit exponents of s and z
+    differ by d with -12 <= d <= 12 - qbits (or s or z is zero).  Under that condition q*s + z
+    must be exactly representable in fp32 for every code q, so one rounding equals the
+    reference's fp32-then-fp16 rounding.  Checked on 400k random finite (s, z) pairs plus the
+    boundary exponents."""
+    rng = np.random.default_rng(qbits)
+    n = 400_000
+    sb = rng.integers(0, 0x10000, n).astype(np.uint16)
+    zb = rng.integers(0, 0x10000, n).astype(np.uint16)
+    # add pairs exactly at and just outside the boundary
+    es = rng.integers(1, 31, 20000)
+    for d in (-13, -12, 12 - qbits, 13 - qbits):
+        ez = es - d
+        ok = (ez >= 1) & (ez <= 30)
+        m1 = rng.integers(0, 1024, int(ok.sum()))
+        m2 = rng.integers(0, 1024, int(ok.sum()))
+        sb = np.concatenate([sb, ((es[ok] << 10) | m1).astype(np.uint16)])
+        zb = np.concatenate([zb, ((ez[ok] << 10) | m2 | (rng.integers(0, 2, int(ok.sum())) << 15)).astype(np.uint16)])
+    finite = ((sb & 0x7C00) != 0x7C00) & ((zb & 0x7C00) != 0x7C00)
+    sb, zb = sb[finite], zb[finite]
+    d = _unit_exp(sb) - _unit_exp(zb)
+    zero = ((sb & 0x7FFF) == 0) | ((zb & 0x7FFF) == 0)
+    cond = zero | ((d >= -12) & (d <= 12 - qbits))
+    s = sb.view(np.float16).astype(np.float64)
+    z = zb.view(np.float16).astype(np.float64)
+    inexact_seen = False
+    for q in (0, 1, 2, 3, 7, 15) + ((100, 255) if qbits == 8 else ()):
+        exact = q * s + z                       # exact in fp64 (< 53 bits)
+        rep = exact.astype(np.float32).astype(np.float64) == exact
+        assert np.all(rep[cond]), (qbits, q)
+        inexact_seen |= bool(np.any(~rep[~cond]))
+    assert inexact_seen                          # the condition is not vacuous
