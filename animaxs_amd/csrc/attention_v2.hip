@@ -18,8 +18,8 @@
 //     fragments of the next half, runs the next half's QK MFMAs interleaved with
 //     this half's softmax VALU, then reads this half's V^T fragments and runs the
 //     PV MFMAs.  Exps use the running max; if any row's max grew by more than 2^8
-//     a side path rescales O and redoes the exps.  Three LDS stages: tile j+2
-//     loads while tiles j and j+1 are read.
+//     a side path rescales O and redoes the exps.  Four LDS stages: tiles j+2
+//     and j+3 load while tiles j and j+1 are read.
 //   * Everything (Q, O accumulators, scores) lives in the 256 VGPRs a wave gets
 //     at 2 waves/SIMD; row sums use v_dot2_f32_f16 on the fp16 P that feeds the
 //     PV MFMA.
@@ -32,13 +32,36 @@ namespace anima {
 constexpr int F2_WAVES = 8;
 constexpr int F2_NT = 64 * F2_WAVES;
 constexpr int F2_BN = 64;
-constexpr int F2_STAGES = 3;
+constexpr int F2_STAGES = 4;
 constexpr float F2_RESCALE_THRESHOLD = 8.0f;
 static_assert(FLASH_V2_ROWS == 32 * F2_WAVES, "one 32-row block per wave");
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 #define F2_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 #define F2_LDS4(p) ((__attribute__((address_space(3))) short4v*)(p))
+
+// s_waitcnt vmcnt(n) alone (expcnt / lgkmcnt unconstrained), n wave-uniform in [0, 15].
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_imm() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  switch (n) {
+    case 0: wait_vmcnt_imm<0>(); break;
+    case 1: wait_vmcnt_imm<1>(); break;
+    case 2: wait_vmcnt_imm<2>(); break;
+    case 3: wait_vmcnt_imm<3>(); break;
+    case 4: wait_vmcnt_imm<4>(); break;
+    case 5: wait_vmcnt_imm<5>(); break;
+    case 6: wait_vmcnt_imm<6>(); break;
+    case 7: wait_vmcnt_imm<7>(); break;
+    case 8: wait_vmcnt_imm<8>(); break;
+    case 9: wait_vmcnt_imm<9>(); break;
+    case 10: wait_vmcnt_imm<10>(); break;
+    case 11: wait_vmcnt_imm<11>(); break;
+    default: wait_vmcnt_imm<12>(); break;
+  }
+}
 
 __device__ __forceinline__ float xlane32_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -110,8 +133,26 @@ __global__ __launch_bounds__(F2_NT, 1) void flash_attention_v2_kernel(FlashParam
   constexpr int KTILE = F2_BN * KROW, VTILE = F2_BN * VROW;   // halfs; whole 1 KiB segments
   static_assert(KTILE % 512 == 0 && VTILE % 512 == 0, "tile must be whole 1 KiB segments");
 
-  __shared__ __attribute__((aligned(1024))) half_t Ks[F2_STAGES][KTILE];
-  __shared__ __attribute__((aligned(1024))) half_t Vs[F2_STAGES][VTILE];
+  // One LDS object per stage: every access names its stage at compile time, so the
+  // compiler can tell an in-flight global->LDS copy into one stage from reads of
+  // another and does not make the reads wait for the copy.
+  __shared__ __attribute__((aligned(1024))) half_t K0[KTILE], K1[KTILE], K2[KTILE], K3[KTILE];
+  __shared__ __attribute__((aligned(1024))) half_t V0[VTILE], V1[VTILE], V2[VTILE], V3[VTILE];
+  static_assert(F2_STAGES == 4, "four stage objects");
+  auto kstage = [&](auto st) __attribute__((always_inline)) -> half_t* {
+    constexpr int S = decltype(st)::value % F2_STAGES;
+    if constexpr (S == 0) return K0;
+    else if constexpr (S == 1) return K1;
+    else if constexpr (S == 2) return K2;
+    else return K3;
+  };
+  auto vstage = [&](auto st) __attribute__((always_inline)) -> half_t* {
+    constexpr int S = decltype(st)::value % F2_STAGES;
+    if constexpr (S == 0) return V0;
+    else if constexpr (S == 1) return V1;
+    else if constexpr (S == 2) return V2;
+    else return V3;
+  };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -144,42 +185,52 @@ __global__ __launch_bounds__(F2_NT, 1) void flash_attention_v2_kernel(FlashParam
 
   // Direct global -> LDS copy of tile j: segment sg of a padded tile holds linear
   // 16-byte slots sg*64 .. sg*64+63; slot -> (row, chunk) of the padded layout.
-  // Wave w copies segments w, w+8, w+16.  Offsets are 32-bit byte offsets from
-  // the tile's first key row (the host checks that 64 key rows fit in 2^31 bytes),
-  // so the copies use the scalar-base + vector-offset address form; they are
-  // recomputed per tile (a few VALU) instead of being held in registers.  Rows
-  // past the last key re-read the last key row (masked in the softmax).
-  constexpr int KR = (KRCH + F2_WAVES - 1) / F2_WAVES;
-  constexpr int VR = (VRCH + F2_WAVES - 1) / F2_WAVES;
-  auto seg_offset = [&](int sg, int rch, int64_t tok, int rmax, int ln) -> uint32_t {
-    const int pos = sg * 64 + ln;
+  // The K segments (0 .. KRCH-1) and V segments (KRCH .. NSEG-1) of a tile are
+  // dealt round-robin: wave w copies combined segments w, w+8, w+16, ...  Every
+  // wave issues exactly SPW copies per tile (slots past NSEG, and every slot of a
+  // tile past the last one, copy a harmless 1 KiB into a scratch LDS object), so
+  // "all but the newest tile landed" is always the single wait vmcnt(SPW).
+  // Offsets are 32-bit byte offsets from the tile's first key row (the host checks
+  // that 64 key rows fit in 2^31 bytes), so the copies use the scalar-base +
+  // vector-offset address form; they are the same for every full tile (computed
+  // once); a tile running past the last key clamps its rows to the last key row
+  // (masked in the softmax).
+  constexpr int NSEG = KRCH + VRCH;
+  constexpr int SPW = (NSEG + F2_WAVES - 1) / F2_WAVES;
+  __shared__ __attribute__((aligned(1024))) half_t Dummy[512];
+  auto seg_offset = [&](int sg, int rmax, int ln) __attribute__((always_inline)) -> uint32_t {
+    const bool isk = sg < KRCH;
+    const int rch = isk ? KRCH : VRCH;
+    const int64_t tok = isk ? p.k_tok : p.v_tok;
+    const int pos = (isk ? sg : sg - KRCH) * 64 + ln;
     const int ch = pos % rch;
     const int row = min(pos / rch, rmax);
     return ((uint32_t)(row * tok) + (uint32_t)((ch < DCH ? ch : 0) * 8)) * 2u;
   };
-  auto issue_tile = [&](int j) {
+  uint32_t soff[SPW];
+#pragma unroll
+  for (int r = 0; r < SPW; ++r) soff[r] = seg_offset(min(wave + F2_WAVES * r, NSEG - 1), F2_BN - 1, lane);
+
+  auto issue_tile = [&](int j, auto st) __attribute__((always_inline)) {
     const int k0 = j * F2_BN;
-    half_t* kd = Ks[j % F2_STAGES];
-    half_t* vd = Vs[j % F2_STAGES];
-    const half_t* kt = kbase + (int64_t)k0 * p.k_tok;
-    const half_t* vt = vbase + (int64_t)k0 * p.v_tok;
+    half_t* kd = kstage(st);
+    half_t* vd = vstage(st);
+    const bool live = j < ntiles;
+    const char* kt = reinterpret_cast<const char*>(kbase + (int64_t)k0 * p.k_tok);
+    const char* vt = reinterpret_cast<const char*>(vbase + (int64_t)k0 * p.v_tok);
     const int rmax = min(p.Sk - 1 - k0, F2_BN - 1);
-    int ln = lane;
-    asm volatile("" : "+v"(ln));   // recompute the offsets per tile rather than keep them live
+    const bool full = rmax == F2_BN - 1;
 #pragma unroll
-    for (int r = 0; r < KR; ++r) {
+    for (int r = 0; r < SPW; ++r) {
       const int sg = wave + F2_WAVES * r;
-      if (sg < KRCH) {
-        const uint32_t o = seg_offset(sg, KRCH, p.k_tok, rmax, ln);
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(kt) + o, F2_LDS(kd + sg * 512), 16, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < VR; ++r) {
-      const int sg = wave + F2_WAVES * r;
-      if (sg < VRCH) {
-        const uint32_t o = seg_offset(sg, VRCH, p.v_tok, rmax, ln);
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(vt) + o, F2_LDS(vd + sg * 512), 16, 0, 0);
+      if (live && sg < KRCH) {
+        const uint32_t o = full ? soff[r] : seg_offset(sg, rmax, lane);
+        __builtin_amdgcn_global_load_lds(kt + o, F2_LDS(kd + sg * 512), 16, 0, 0);
+      } else if (live && sg < NSEG) {
+        const uint32_t o = full ? soff[r] : seg_offset(sg, rmax, lane);
+        __builtin_amdgcn_global_load_lds(vt + o, F2_LDS(vd + (sg - KRCH) * 512), 16, 0, 0);
+      } else {
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(kbase) + 16 * lane, F2_LDS(Dummy), 16, 0, 0);
       }
     }
   };
@@ -194,27 +245,30 @@ __global__ __launch_bounds__(F2_NT, 1) void flash_attention_v2_kernel(FlashParam
   float l_run = 0.f;
   const float c2 = p.scale_log2;
 
+  typedef __attribute__((address_space(3))) short4v lds_short4v;
+
   // Per-lane fragment bases (halfs); everything else is an immediate offset.
   const int kfrag = c32 * KROW + hh * 8;
   const int vfrag = (4 * hh + (jj >> 2)) * VROW + 16 * (gg & 1) + 4 * (jj & 3);
 
   // K fragment s of half hf: lane holds K[32hf + c32][16s + 8h .. +7].
-  auto load_kfrags = [&](int j, int hf, half8v (&kf)[QS]) {
-    const half_t* ks = Ks[j % F2_STAGES] + kfrag + hf * 32 * KROW;
+  auto load_kfrags = [&](auto st, int hf, half8v (&kf)[QS]) {
+    const half_t* ks = kstage(st) + kfrag + hf * 32 * KROW;
 #pragma unroll
     for (int s = 0; s < QS; ++s) kf[s] = *reinterpret_cast<const half8v*>(ks + 16 * s);
   };
   // V^T fragment (c, uu) of half hf: lane (d, h) holds V[key(u, h, 0..7)][32c + d]
   // with key(u, h, i) = 16u + 8(i/4) + 4h + i%4, the key order of the S^T C layout.
-  auto load_vfrags = [&](int j, int hf, half8v (&vf)[OB][2]) {
-    const half_t* vs = Vs[j % F2_STAGES] + vfrag;
+  // Reads through an LDS-space pointer formed from the shared array itself, so
+  // every read is "lane base + immediate" (no per-read address arithmetic).
+  auto load_vfrags = [&](auto st, int hf, half8v (&vf)[OB][2]) {
+    lds_short4v* vs = (lds_short4v*)vstage(st) + (vfrag + 32 * hf * VROW) / 4;
 #pragma unroll
     for (int c = 0; c < OB; ++c)
 #pragma unroll
       for (int uu = 0; uu < 2; ++uu) {
-        const int u = 2 * hf + uu;
-        const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(F2_LDS4(vs + 16 * u * VROW + 32 * c));
-        const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(F2_LDS4(vs + (16 * u + 8) * VROW + 32 * c));
+        const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vs + (16 * uu * VROW + 32 * c) / 4);
+        const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vs + ((16 * uu + 8) * VROW + 32 * c) / 4);
         const half4v lo_h = __builtin_bit_cast(half4v, lo);
         const half4v hi_h = __builtin_bit_cast(half4v, hi);
         vf[c][uu] = half8v{lo_h[0], lo_h[1], lo_h[2], lo_h[3], hi_h[0], hi_h[1], hi_h[2], hi_h[3]};
@@ -285,7 +339,7 @@ __global__ __launch_bounds__(F2_NT, 1) void flash_attention_v2_kernel(FlashParam
     l_run = s;
   };
 
-  auto half_masked = [&](int j, int hf) {
+  auto half_masked = [&](int j, int hf) __attribute__((always_inline)) {
     const int k0 = j * F2_BN + 32 * hf;
     return (k0 + 32 > kv_len) || (p.causal && k0 + 31 > wq0);
   };
@@ -293,66 +347,89 @@ __global__ __launch_bounds__(F2_NT, 1) void flash_attention_v2_kernel(FlashParam
   floatx16 SA, SB;
   half8v P[2];
 
-  // One half-step, in phases separated by scheduling fences:
-  //   A  K fragment reads for the next QK;
+  // Scores of keys past the sequence (or above the diagonal) -> -inf, in place.
+  auto mask_scores = [&](int j, int hf, floatx16& S) __attribute__((always_inline)) {
+    const int k0 = j * F2_BN + 32 * hf;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int kidx = k0 + (e >> 2) * 8 + 4 * hh + (e & 3);
+      if (kidx >= kv_len || (p.causal && kidx > qi)) S[e] = -INFINITY;
+    }
+  };
+
+  // One half-step (32 keys), a single code path for every half-step so the O
+  // accumulators never move between registers:
+  //   A  K fragment reads for the next half's QK (past the last tile they re-read
+  //      the current stage and the scores are discarded);
   //   B  QK(next) MFMAs interleaved with this half's softmax VALU;
   //   C  V^T fragment reads, the rare rescale, the row sum and the PV MFMAs.
-  auto half_step = [&](int j, int hf, floatx16& Scur, floatx16& Snext, auto has_next_c, auto masked_c) {
-    constexpr bool HAS_NEXT = decltype(has_next_c)::value;
-    constexpr bool MASKED = decltype(masked_c)::value;
-    const int nj = hf ? j + 1 : j;
-    const int nhf = hf ^ 1;
+  // Masking is a wave-uniform in-place fix-up of the current scores.
+  // st: stage of tile j; the next half's K comes from the same stage (hf = 0) or
+  // the next one (hf = 1; past the last tile that stage holds stale keys and the
+  // scores are discarded).
+  auto half_step = [&](int j, int hf, floatx16& Scur, floatx16& Snext, auto st) __attribute__((always_inline)) {
+    constexpr int ST = decltype(st)::value;
     half8v kf[QS];
-    half8v vf[OB][2];
-    if (HAS_NEXT) load_kfrags(nj, nhf, kf);
+    if (hf == 0)
+      load_kfrags(st, 1, kf);
+    else
+      load_kfrags(std::integral_constant<int, (ST + 1) % F2_STAGES>{}, 0, kf);
+    if (half_masked(j, hf)) mask_scores(j, hf, Scur);
     __builtin_amdgcn_sched_barrier(0);
-    if (HAS_NEXT) qk_mfma(kf, Snext);
-    const bool need = softmax(j, hf, Scur, P, MASKED);
-    if (HAS_NEXT) {
+    qk_mfma(kf, Snext);
+    const bool need = softmax(j, hf, Scur, P, false);
 #pragma unroll
-      for (int i = 0; i < QS; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // six VALU
-      }
+    for (int i = 0; i < QS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // six VALU
     }
     __builtin_amdgcn_sched_barrier(0);
-    load_vfrags(j, hf, vf);
+    half8v vf[OB][2];
+    load_vfrags(st, hf, vf);
     if (__any(need)) rescale(Scur, P);
     rowsum(P);
     pv_mfma(vf, P);
   };
 
-  auto run_half = [&](int j, int hf, floatx16& Scur, floatx16& Snext) {
-    using T = std::integral_constant<bool, true>;
-    using F = std::integral_constant<bool, false>;
-    const bool has_next = (hf ? j + 1 : j) < ntiles;
-    const bool masked = half_masked(j, hf);
-    if (has_next) {
-      if (masked) half_step(j, hf, Scur, Snext, T{}, T{});
-      else half_step(j, hf, Scur, Snext, T{}, F{});
-    } else {
-      if (masked) half_step(j, hf, Scur, Snext, F{}, T{});
-      else half_step(j, hf, Scur, Snext, F{}, F{});
-    }
+  // Four stages, two tiles of prefetch: iteration j reads tiles j and j+1 (the
+  // second half-step starts the next tile's QK), tile j+2 is in flight and tile
+  // j+3 is issued into the stage tile j-1 used.  Loads retire in order and every
+  // tile is SPW copies per wave, so "tiles <= j+1 landed" is vmcnt(SPW).  The
+  // barrier is written out (s_barrier after lgkmcnt(0)) so that the compiler does
+  // not turn it into a wait for every copy in flight.
+  auto lds_barrier = [&]() __attribute__((always_inline)) {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   };
-
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
   if (ntiles > 0) {
-    issue_tile(0);
-    if (ntiles > 1) issue_tile(1);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    issue_tile(0, S0{});
+    issue_tile(1, S1{});
+    issue_tile(2, S2{});
+    wait_vmcnt_imm<2 * SPW>();   // tile 0 landed
+    lds_barrier();
     half8v kf[QS];
-    load_kfrags(0, 0, kf);
+    load_kfrags(S0{}, 0, kf);
     qk_mfma(kf, SA);
   }
-  for (int j = 0; j < ntiles; ++j) {
-    // Tile j (and j+1) are resident once every wave's copies have landed; the
-    // barrier also retires all reads of stage (j+2)%3 = (j-1)%3 from step j-1.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (j + 2 < ntiles) issue_tile(j + 2);
-    run_half(j, 0, SA, SB);
-    run_half(j, 1, SB, SA);
+  // Tile j uses stage j % 4; the loop is unrolled by four so every stage is static.
+  auto tile_iter = [&](int j, auto st) __attribute__((always_inline)) {
+    constexpr int ST = decltype(st)::value;
+    // Tiles j, j+1 resident for every wave; the barrier also retires all reads of
+    // stage (j+3)%4 = (j-1)%4 from iteration j-1 before it is overwritten.
+    wait_vmcnt_imm<SPW>();
+    lds_barrier();
+    issue_tile(j + 3, std::integral_constant<int, (ST + 3) % F2_STAGES>{});
+    half_step(j, 0, SA, SB, st);
+    half_step(j, 1, SB, SA, st);
+  };
+  for (int j = 0; j < ntiles; j += F2_STAGES) {
+    tile_iter(j, S0{});
+    if (j + 1 < ntiles) tile_iter(j + 1, S1{});
+    if (j + 2 < ntiles) tile_iter(j + 2, S2{});
+    if (j + 3 < ntiles) tile_iter(j + 3, S3{});
   }
 
   const float l_tot = xlane32_sum(l_run);
