@@ -74,13 +74,21 @@ __global__ __launch_bounds__(G_NT, 1) void gemm_kernel(GemmParams p, int vec_sto
   const int m0 = tm * G_BM, n0 = tn * G_BN;
   const int nk = (p.K + G_BK - 1) / G_BK;
 
-  half8v xr[XL];
-  u32x4 wr[WL];
-  float ws_s[WL], ws_z[WL];
+  // One K block's global data in registers.  The fast path keeps two of these so the
+  // loads of block kb+2 are in flight while block kb+1 is written to LDS.
+  struct Regs {
+    half8v xr[XL];
+    u32x4 wr[WL];
+    float ws_s[WL], ws_z[WL];
+  };
   const half8v zero8 = {};
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
-  auto load_global = [&](int kb) {
+  auto load_global = [&](int kb, Regs& rg) __attribute__((always_inline)) {
+    half8v (&xr)[XL] = rg.xr;
+    u32x4 (&wr)[WL] = rg.wr;
+    float (&ws_s)[WL] = rg.ws_s;
+    float (&ws_z)[WL] = rg.ws_z;
     const int kbase = kb * G_BK;
 #pragma unroll
     for (int r = 0; r < XL; ++r) {
@@ -88,7 +96,8 @@ __global__ __launch_bounds__(G_NT, 1) void gemm_kernel(GemmParams p, int vec_sto
       const int row = c >> 3, ch = c & 7;
       const int m = m0 + row;
       if (FAST) {
-        xr[r] = m < p.M ? *reinterpret_cast<const half8v*>(p.x + (int64_t)m * p.K + kbase + ch * 8) : zero8;
+        // Rows past M are clamped, not masked: they only feed output rows never stored.
+        xr[r] = *reinterpret_cast<const half8v*>(p.x + (int64_t)min(m, p.M - 1) * p.K + kbase + ch * 8);
       } else {
         half8v v;
 #pragma unroll
@@ -106,17 +115,23 @@ __global__ __launch_bounds__(G_NT, 1) void gemm_kernel(GemmParams p, int vec_sto
       if (STORAGE == ANIMA_STORAGE_W4) { row = c >> 1; part = c & 1; }
       else if (STORAGE == ANIMA_STORAGE_W8) { row = c >> 2; part = c & 3; }
       else { row = c >> 3; part = c & 7; }
-      const int n = n0 + row;
+      // Rows past N are clamped in the fast path: they only feed columns never stored.
+      const int n = FAST ? min(n0 + row, p.N - 1) : n0 + row;
       if (STORAGE != ANIMA_STORAGE_FP16) {
-        ws_s[r] = n < p.N ? (float)p.scale[(int64_t)n * p.groups + kb] : 0.f;
-        ws_z[r] = n < p.N ? (float)p.zero[(int64_t)n * p.groups + kb] : 0.f;
+        if (FAST) {
+          ws_s[r] = (float)p.scale[(int64_t)n * p.groups + kb];
+          ws_z[r] = (float)p.zero[(int64_t)n * p.groups + kb];
+        } else {
+          ws_s[r] = n < p.N ? (float)p.scale[(int64_t)n * p.groups + kb] : 0.f;
+          ws_z[r] = n < p.N ? (float)p.zero[(int64_t)n * p.groups + kb] : 0.f;
+        }
       }
       if (FAST) {
         const uint8_t* src;
         if (STORAGE == ANIMA_STORAGE_W4) src = p.w + (int64_t)n * p.row_stride + kb * 32 + part * 16;
         else if (STORAGE == ANIMA_STORAGE_W8) src = p.w + (int64_t)n * p.row_stride + kbase + part * 16;
         else src = p.w + ((int64_t)n * p.row_stride + kbase + part * 8) * 2;
-        wr[r] = n < p.N ? *reinterpret_cast<const u32x4*>(src) : zero4;
+        wr[r] = *reinterpret_cast<const u32x4*>(src);
       } else {
         // byte-granular path: any row stride / offset / K tail
         uint32_t bytes[4] = {0u, 0u, 0u, 0u};
@@ -153,7 +168,11 @@ __global__ __launch_bounds__(G_NT, 1) void gemm_kernel(GemmParams p, int vec_sto
     }
   };
 
-  auto store_tile = [&](int st, int kb) {
+  auto store_tile = [&](int st, int kb, const Regs& rg) __attribute__((always_inline)) {
+    const half8v (&xr)[XL] = rg.xr;
+    const u32x4 (&wr)[WL] = rg.wr;
+    const float (&ws_s)[WL] = rg.ws_s;
+    const float (&ws_z)[WL] = rg.ws_z;
     const int kbase = kb * G_BK;
 #pragma unroll
     for (int r = 0; r < XL; ++r) {
@@ -205,14 +224,7 @@ __global__ __launch_bounds__(G_NT, 1) void gemm_kernel(GemmParams p, int vec_sto
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = floatx16{};
 
-  if (nk > 0) {
-    load_global(0);
-    store_tile(0, 0);
-  }
-  __syncthreads();
-  for (int kb = 0; kb < nk; ++kb) {
-    const int st = kb & 1;
-    if (kb + 1 < nk) load_global(kb + 1);
+  auto mfma_block = [&](int st) __attribute__((always_inline)) {
 #pragma unroll
     for (int s = 0; s < G_BK / 16; ++s) {
       half8v wf[2], xf[4];
@@ -231,8 +243,44 @@ __global__ __launch_bounds__(G_NT, 1) void gemm_kernel(GemmParams p, int vec_sto
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc[a][b] = mfma32(wf[a], xf[b], acc[a][b]);
     }
-    if (kb + 1 < nk) store_tile(st ^ 1, kb + 1);
+  };
+
+  if (FAST) {
+    // Register double buffer, loads two K blocks ahead, every load unconditional (the
+    // prefetch past the last block re-reads it) so each wait covers exactly the
+    // older block.  Unrolled by two so both register sets stay static.
+    Regs ra, rb;
+    if (nk > 0) {
+      load_global(0, ra);
+      load_global(min(1, nk - 1), rb);
+      store_tile(0, 0, ra);
+    }
     __syncthreads();
+    for (int kb = 0; kb < nk; kb += 2) {
+      load_global(min(kb + 2, nk - 1), ra);
+      mfma_block(0);
+      if (kb + 1 < nk) store_tile(1, kb + 1, rb);
+      __syncthreads();
+      if (kb + 1 >= nk) break;
+      load_global(min(kb + 3, nk - 1), rb);
+      mfma_block(1);
+      if (kb + 2 < nk) store_tile(0, kb + 2, ra);
+      __syncthreads();
+    }
+  } else {
+    Regs ra;
+    if (nk > 0) {
+      load_global(0, ra);
+      store_tile(0, 0, ra);
+    }
+    __syncthreads();
+    for (int kb = 0; kb < nk; ++kb) {
+      const int st = kb & 1;
+      if (kb + 1 < nk) load_global(kb + 1, ra);
+      mfma_block(st);
+      if (kb + 1 < nk) store_tile(st ^ 1, kb + 1, ra);
+      __syncthreads();
+    }
   }
 
 #pragma unroll

@@ -40,6 +40,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-block", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the per-workload table")
+    ap.add_argument("--profile-block", action="store_true",
+                    help="only run the S=4096 DiT block (--block-steps times), for a rocprofv3 kernel trace")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="only launch the dominant flash kernel (--warmup + --steps times) and a 256 MiB "
                          "calibration copy, for rocprofv3 counter passes; prints no JSON")
@@ -129,6 +131,11 @@ def main():
     stream = torch.cuda.current_stream()
     ctx = A.Context(0, stream)
     print(f"# device {dev_name}", file=sys.stderr, flush=True)
+
+    if args.profile_block:
+        ms = time_block(torch, A, ctx, stream, args)
+        print(f"# profile-block: DiT block S4096 {ms:.3f} ms", file=sys.stderr)
+        return
 
     # ---------------- headline: S=4096 self-attention with fused norm+RoPE ----------------
     sets, qw, kw = gen_attention_inputs(torch, 4)
