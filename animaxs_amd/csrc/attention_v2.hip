@@ -361,8 +361,9 @@ __global__ __launch_bounds__(F2_NT, 1) void flash_attention_v2_kernel(FlashParam
   // accumulators never move between registers:
   //   A  K fragment reads for the next half's QK (past the last tile they re-read
   //      the current stage and the scores are discarded);
-  //   B  QK(next) MFMAs interleaved with this half's softmax VALU;
-  //   C  V^T fragment reads, the rare rescale, the row sum and the PV MFMAs.
+  //   B  QK(next) MFMAs interleaved with this half's softmax VALU and the V^T
+  //      fragment reads;
+  //   C  the rare rescale, the row sum and the PV MFMAs.
   // Masking is a wave-uniform in-place fix-up of the current scores.
   // st: stage of tile j; the next half's K comes from the same stage (hf = 0) or
   // the next one (hf = 1; past the last tile that stage holds stale keys and the
@@ -378,14 +379,18 @@ __global__ __launch_bounds__(F2_NT, 1) void flash_attention_v2_kernel(FlashParam
     __builtin_amdgcn_sched_barrier(0);
     qk_mfma(kf, Snext);
     const bool need = softmax(j, hf, Scur, P, false);
+    // P is used here, above the rescale branch: otherwise the compiler sinks the
+    // exponentials below it (into both paths) and they no longer overlap the MFMAs.
+    asm volatile("" ::"v"(P[0]), "v"(P[1]));
+    half8v vf[OB][2];
+    load_vfrags(st, hf, vf);
 #pragma unroll
     for (int i = 0; i < QS; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // two V^T fragment reads
       __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // six VALU
     }
     __builtin_amdgcn_sched_barrier(0);
-    half8v vf[OB][2];
-    load_vfrags(st, hf, vf);
     if (__any(need)) rescale(Scur, P);
     rowsum(P);
     pv_mfma(vf, P);
