@@ -2,27 +2,38 @@
 //
 // Same maths and numerics as the 128-row kernel in attention.hip (S^T = K Q^T on
 // v_mfma_f32_32x32x16_f16, fp32 online softmax in base 2, fp16 P, O^T += V^T P^T,
-// Q RMSNorm + split-half RoPE fused into the Q fragment load), re-organised for
-// MFMA throughput:
+// Q RMSNorm + split-half RoPE fused into the Q fragment load), organised so that
+// the matrix cores and the vector ALUs of every SIMD stay busy at the same time:
 //   * 8 waves x 32 query rows share one K/V tile stream (1 workgroup per CU,
-//     2 waves per SIMD so the hardware interleaves two instruction streams).
-//   * K and V tiles (64 keys) go global -> LDS with global_load_lds_dwordx4 (no
-//     staging registers).  Rows are padded (K: +16 B, V: +64 B) so the fragment
-//     reads below hit distinct LDS banks (64 banks x 4 B); lanes whose linear slot
-//     falls in a pad load a harmless duplicate chunk.  Padding instead of an XOR
-//     swizzle keeps every fragment address "per-lane base + immediate".
-//   * V^T fragments come straight from the row-major V tile with
-//     ds_read_b64_tr_b16: within each 16-lane group, lane i receives column i of
-//     the 4 rows the group's lanes point at (4 consecutive keys for one d).
-//   * The pipeline steps over 32-key halves.  Each half-step reads the K
-//     fragments of the next half, runs the next half's QK MFMAs interleaved with
-//     this half's softmax VALU, then reads this half's V^T fragments and runs the
-//     PV MFMAs.  Exps use the running max; if any row's max grew by more than 2^8
-//     a side path rescales O and redoes the exps.  Four LDS stages: tiles j+2
-//     and j+3 load while tiles j and j+1 are read.
-//   * Everything (Q, O accumulators, scores) lives in the 256 VGPRs a wave gets
-//     at 2 waves/SIMD; row sums use v_dot2_f32_f16 on the fp16 P that feeds the
-//     PV MFMA.
+//     2 waves per SIMD).  The waves form two groups, one wave of each group per
+//     SIMD (waves w and w+4 share a SIMD).  Work per key tile j is split into two
+//     phases:
+//       G(j)  MFMA phase: QK^T of tile j, PV of tile j-1 and the row sums of tile
+//             j-1 on the matrix cores (lsum += ones x P^T), as one fixed sequence
+//             of MFMAs whose LDS fragment reads run a few MFMAs ahead;
+//       X(j)  VALU phase: the tile copies (below), masking, row max, the (rare)
+//             O rescale, exp2 and fp16 P of tile j.
+//     Phases are separated by workgroup barriers, and group 1 runs one phase
+//     behind group 0 (one extra barrier at the start, group 0 one at the end), so
+//     in every barrier interval one wave of each SIMD issues MFMAs while the
+//     other issues VALU work ("ping-pong").  A single wave issues VALU work at
+//     about half the SIMD's VALU rate, so the two streams overlap instead of both
+//     waves waiting on the same unit.
+//   * K and V tiles (64 keys) are copied global -> VGPR -> LDS: during X(j) a wave
+//     stores its staged segments of tile j+2 (ds_write_b128) and issues the
+//     buffer loads of tile j+3, so a full tile period hides the load latency and
+//     the LDS writes never queue ahead of the same wave's fragment reads.  Buffer
+//     descriptors bound every tile by the last key row in use: rows past it read
+//     as zeros without touching memory.
+//   * Rows are padded in LDS (K: +16 B, V: +64 B) so the fragment reads hit
+//     distinct banks (64 banks x 4 B); padding instead of an XOR swizzle keeps
+//     every fragment address "per-lane base + immediate".  V^T fragments come
+//     straight from the row-major V tile with ds_read_b64_tr_b16.
+//   * Exps use the running max; a row max that grows by more than 2^8 rescales O
+//     and the row sums first (wave-uniform branch).  Four LDS stages: tile j is
+//     read by QK while tile j-1 is read by PV and tile j+2 is written.
+//   * Everything (Q, O accumulators, scores, row sums) lives in the 256 VGPRs a
+//     wave gets at 2 waves/SIMD.
 #include <type_traits>
 
 #include "attention.hpp"
@@ -34,33 +45,29 @@ constexpr int F2_NT = 64 * F2_WAVES;
 constexpr int F2_BN = 64;
 constexpr int F2_STAGES = 4;
 constexpr float F2_RESCALE_THRESHOLD = 8.0f;
+constexpr int F2_READ_AHEAD = 4;    // MFMA operand fragments read from LDS ahead of their MFMA
 static_assert(FLASH_V2_ROWS == 32 * F2_WAVES, "one 32-row block per wave");
 
 typedef short short4v __attribute__((ext_vector_type(4)));
-#define F2_LDS(p) ((__attribute__((address_space(3))) void*)(p))
-#define F2_LDS4(p) ((__attribute__((address_space(3))) short4v*)(p))
 
-// s_waitcnt vmcnt(n) alone (expcnt / lgkmcnt unconstrained), n wave-uniform in [0, 15].
+// s_waitcnt vmcnt(n) alone (expcnt / lgkmcnt unconstrained), n in [0, 15].
 template <int N>
 __device__ __forceinline__ void wait_vmcnt_imm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8));
 }
-__device__ __forceinline__ void wait_vmcnt(int n) {
-  switch (n) {
-    case 0: wait_vmcnt_imm<0>(); break;
-    case 1: wait_vmcnt_imm<1>(); break;
-    case 2: wait_vmcnt_imm<2>(); break;
-    case 3: wait_vmcnt_imm<3>(); break;
-    case 4: wait_vmcnt_imm<4>(); break;
-    case 5: wait_vmcnt_imm<5>(); break;
-    case 6: wait_vmcnt_imm<6>(); break;
-    case 7: wait_vmcnt_imm<7>(); break;
-    case 8: wait_vmcnt_imm<8>(); break;
-    case 9: wait_vmcnt_imm<9>(); break;
-    case 10: wait_vmcnt_imm<10>(); break;
-    case 11: wait_vmcnt_imm<11>(); break;
-    default: wait_vmcnt_imm<12>(); break;
-  }
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte load through a raw buffer descriptor of n bytes at base: offsets at or
+// past n read zeros without touching memory.  (The descriptor type exists in the
+// device pass only.)
+__device__ __forceinline__ u32x4 load16_bounded(const void* base, int n, uint32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
+#else
+  return u32x4{};
+#endif
 }
 
 __device__ __forceinline__ float xlane32_max(float x) {
@@ -123,7 +130,7 @@ __device__ __forceinline__ void load_q_fragment(const FlashParams& p, int b, int
 }
 
 template <int D>
-__global__ __launch_bounds__(F2_NT, 1) void flash_attention_v2_kernel(FlashParams p) {
+__global__ __launch_bounds__(F2_NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_attention_v2_kernel(FlashParams p) {
   constexpr int DCH = D / 8;             // 16-byte data chunks per row
   constexpr int QS = D / 16;
   constexpr int OB = D / 32;
@@ -132,6 +139,8 @@ __global__ __launch_bounds__(F2_NT, 1) void flash_attention_v2_kernel(FlashParam
   constexpr int KRCH = KROW / 8, VRCH = VROW / 8;
   constexpr int KTILE = F2_BN * KROW, VTILE = F2_BN * VROW;   // halfs; whole 1 KiB segments
   static_assert(KTILE % 512 == 0 && VTILE % 512 == 0, "tile must be whole 1 KiB segments");
+  constexpr int NSEG = KRCH + VRCH;                            // 1 KiB copies per tile
+  constexpr int SPW = (NSEG + F2_WAVES - 1) / F2_WAVES;        // copies per wave (at most)
 
   // One LDS object per stage: every access names its stage at compile time, so the
   // compiler can tell an in-flight global->LDS copy into one stage from reads of
@@ -155,9 +164,12 @@ __global__ __launch_bounds__(F2_NT, 1) void flash_attention_v2_kernel(FlashParam
   };
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c32 = lane & 31, hh = lane >> 5;
   const int jj = lane & 15, gg = lane >> 4;
+  // Waves w and w+4 share a SIMD; one of them is in each group.
+  const int group = wave >> 2;
 
   int lb = xcd_logical_block(blockIdx.x, gridDim.x);
   const int qt = lb % p.q_tiles;
@@ -183,55 +195,73 @@ __global__ __launch_bounds__(F2_NT, 1) void flash_attention_v2_kernel(FlashParam
   const half_t* kbase = p.k + (int64_t)b * p.k_batch + (int64_t)kvh * p.k_head;
   const half_t* vbase = p.v + (int64_t)b * p.v_batch + (int64_t)kvh * p.v_head;
 
-  // Direct global -> LDS copy of tile j: segment sg of a padded tile holds linear
-  // 16-byte slots sg*64 .. sg*64+63; slot -> (row, chunk) of the padded layout.
-  // The K segments (0 .. KRCH-1) and V segments (KRCH .. NSEG-1) of a tile are
-  // dealt round-robin: wave w copies combined segments w, w+8, w+16, ...  Every
-  // wave issues exactly SPW copies per tile (slots past NSEG, and every slot of a
-  // tile past the last one, copy a harmless 1 KiB into a scratch LDS object), so
-  // "all but the newest tile landed" is always the single wait vmcnt(SPW).
-  // Offsets are 32-bit byte offsets from the tile's first key row (the host checks
-  // that 64 key rows fit in 2^31 bytes), so the copies use the scalar-base +
-  // vector-offset address form; they are the same for every full tile (computed
-  // once); a tile running past the last key clamps its rows to the last key row
-  // (masked in the softmax).
-  constexpr int NSEG = KRCH + VRCH;
-  constexpr int SPW = (NSEG + F2_WAVES - 1) / F2_WAVES;
-  __shared__ __attribute__((aligned(1024))) half_t Dummy[512];
-  auto seg_offset = [&](int sg, int rmax, int ln) __attribute__((always_inline)) -> uint32_t {
+  // Segment sg of a padded tile holds linear 16-byte slots sg*64 .. sg*64+63;
+  // slot -> (row, chunk) of the padded layout.  The K segments (0 .. KRCH-1) and
+  // V segments (KRCH .. NSEG-1) of a tile are dealt round-robin: wave w copies
+  // combined segments w, w+8, w+16, ...  Each tile is read through a buffer
+  // descriptor whose base is its first key row and whose size ends at the last
+  // key row this workgroup uses (kend): rows past it, and every row of a tile past
+  // the last one, read as zeros without touching memory.  The per-lane offsets are
+  // therefore the same for every tile (computed once; 64 key rows fit in 2^31
+  // bytes, checked on the host).  Pad slots load a duplicate of the row's first
+  // chunk.
+  uint32_t soff[SPW];
+#pragma unroll
+  for (int r = 0; r < SPW; ++r) {
+    const int sg = min(wave + F2_WAVES * r, NSEG - 1);
     const bool isk = sg < KRCH;
     const int rch = isk ? KRCH : VRCH;
     const int64_t tok = isk ? p.k_tok : p.v_tok;
-    const int pos = (isk ? sg : sg - KRCH) * 64 + ln;
+    const int pos = (isk ? sg : sg - KRCH) * 64 + lane;
     const int ch = pos % rch;
-    const int row = min(pos / rch, rmax);
-    return ((uint32_t)(row * tok) + (uint32_t)((ch < DCH ? ch : 0) * 8)) * 2u;
+    soff[r] = ((uint32_t)((pos / rch) * tok) + (uint32_t)((ch < DCH ? ch : 0) * 8)) * 2u;
+  }
+  const int64_t ktile_bytes = (int64_t)F2_BN * p.k_tok * 2;
+  const int64_t vtile_bytes = (int64_t)F2_BN * p.v_tok * 2;
+  const int64_t k_end = kend > 0 ? ((int64_t)(kend - 1) * p.k_tok + D) * 2 : 0;   // bytes from kbase
+  const int64_t v_end = kend > 0 ? ((int64_t)(kend - 1) * p.v_tok + D) * 2 : 0;
+  struct TileSpan { const char* base; int n; };
+  auto tile_span = [&](const half_t* base, int64_t tile_bytes, int64_t end, int j)
+      __attribute__((always_inline)) -> TileSpan {
+    const int64_t off = (int64_t)j * tile_bytes;
+    const int64_t rem = end - off;
+    return {reinterpret_cast<const char*>(base) + off, rem <= 0 ? 0 : (int)min(rem, (int64_t)0x7fffffff)};
   };
-  uint32_t soff[SPW];
-#pragma unroll
-  for (int r = 0; r < SPW; ++r) soff[r] = seg_offset(min(wave + F2_WAVES * r, NSEG - 1), F2_BN - 1, lane);
 
-  auto issue_tile = [&](int j, auto st) __attribute__((always_inline)) {
-    const int k0 = j * F2_BN;
-    half_t* kd = kstage(st);
-    half_t* vd = vstage(st);
-    const bool live = j < ntiles;
-    const char* kt = reinterpret_cast<const char*>(kbase + (int64_t)k0 * p.k_tok);
-    const char* vt = reinterpret_cast<const char*>(vbase + (int64_t)k0 * p.v_tok);
-    const int rmax = min(p.Sk - 1 - k0, F2_BN - 1);
-    const bool full = rmax == F2_BN - 1;
+  // Tile copies go global -> VGPR -> LDS.  load_tile(j) fetches this wave's
+  // segments of tile j into 16-byte staging registers; store_tile writes them
+  // into a stage with ds_write_b128 one MFMA phase later, so a full tile period
+  // of load latency is hidden behind the MFMAs.
+  u32x4 stg[SPW];
+  auto load_tile = [&](int j) __attribute__((always_inline)) {
+    const TileSpan rk = tile_span(kbase, ktile_bytes, k_end, j);
+    const TileSpan rv = tile_span(vbase, vtile_bytes, v_end, j);
 #pragma unroll
     for (int r = 0; r < SPW; ++r) {
       const int sg = wave + F2_WAVES * r;
-      if (live && sg < KRCH) {
-        const uint32_t o = full ? soff[r] : seg_offset(sg, rmax, lane);
-        __builtin_amdgcn_global_load_lds(kt + o, F2_LDS(kd + sg * 512), 16, 0, 0);
-      } else if (live && sg < NSEG) {
-        const uint32_t o = full ? soff[r] : seg_offset(sg, rmax, lane);
-        __builtin_amdgcn_global_load_lds(vt + o, F2_LDS(vd + (sg - KRCH) * 512), 16, 0, 0);
-      } else {
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(kbase) + 16 * lane, F2_LDS(Dummy), 16, 0, 0);
-      }
+      if (r == SPW - 1 && sg >= NSEG) break;
+      stg[r] = sg < KRCH ? load16_bounded(rk.base, rk.n, soff[r]) : load16_bounded(rv.base, rv.n, soff[r]);
+    }
+  };
+  auto load_seg = [&](int r, int j) __attribute__((always_inline)) {
+    const int sg = wave + F2_WAVES * r;
+    if (r == SPW - 1 && sg >= NSEG) return;
+    const TileSpan sp = sg < KRCH ? tile_span(kbase, ktile_bytes, k_end, j) : tile_span(vbase, vtile_bytes, v_end, j);
+    stg[r] = load16_bounded(sp.base, sp.n, soff[r]);
+  };
+  auto store_seg = [&](int r, auto st) __attribute__((always_inline)) {
+    const int sg = wave + F2_WAVES * r;
+    if (r == SPW - 1 && sg >= NSEG) return;
+    half_t* dst = sg < KRCH ? kstage(st) + sg * 512 : vstage(st) + (sg - KRCH) * 512;
+    *reinterpret_cast<u32x4*>(dst + lane * 8) = stg[r];
+  };
+  auto store_tile = [&](auto st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < SPW; ++r) {
+      const int sg = wave + F2_WAVES * r;
+      if (r == SPW - 1 && sg >= NSEG) break;
+      half_t* dst = sg < KRCH ? kstage(st) + sg * 512 : vstage(st) + (sg - KRCH) * 512;
+      *reinterpret_cast<u32x4*>(dst + lane * 8) = stg[r];
     }
   };
 
@@ -242,202 +272,193 @@ __global__ __launch_bounds__(F2_NT, 1) void flash_attention_v2_kernel(FlashParam
 #pragma unroll
   for (int c = 0; c < OB; ++c) acc[c] = floatx16{};
   float m_run = -INFINITY;
-  float l_run = 0.f;
+  // Row sums on the matrix cores: lsum += ones(32x16) x P^T gives, in every lane,
+  // the sum of its query's fp16 probabilities (fp32 accumulation).
+  floatx16 lsum = floatx16{};
+  const half8v ones = {(half_t)1.f, (half_t)1.f, (half_t)1.f, (half_t)1.f,
+                       (half_t)1.f, (half_t)1.f, (half_t)1.f, (half_t)1.f};
   const float c2 = p.scale_log2;
 
+  typedef __attribute__((address_space(3))) half8v lds_half8v;
   typedef __attribute__((address_space(3))) short4v lds_short4v;
 
   // Per-lane fragment bases (halfs); everything else is an immediate offset.
   const int kfrag = c32 * KROW + hh * 8;
   const int vfrag = (4 * hh + (jj >> 2)) * VROW + 16 * (gg & 1) + 4 * (jj & 3);
 
-  // K fragment s of half hf: lane holds K[32hf + c32][16s + 8h .. +7].
-  auto load_kfrags = [&](auto st, int hf, half8v (&kf)[QS]) {
-    const half_t* ks = kstage(st) + kfrag + hf * 32 * KROW;
+  floatx16 S[2];     // scores of the current tile: keys 0..31, 32..63
+  half8v P[2][2];    // fp16 probabilities of the previous tile (keys 32h + 16u + ...)
+  // G(0) runs the PV step of a tile "-1" in stage 3: P = 0 and V = 0 make it add
+  // exact zeros (stage 3 is first filled in G(1), after two barriers).
 #pragma unroll
-    for (int s = 0; s < QS; ++s) kf[s] = *reinterpret_cast<const half8v*>(ks + 16 * s);
-  };
-  // V^T fragment (c, uu) of half hf: lane (d, h) holds V[key(u, h, 0..7)][32c + d]
-  // with key(u, h, i) = 16u + 8(i/4) + 4h + i%4, the key order of the S^T C layout.
-  // Reads through an LDS-space pointer formed from the shared array itself, so
-  // every read is "lane base + immediate" (no per-read address arithmetic).
-  auto load_vfrags = [&](auto st, int hf, half8v (&vf)[OB][2]) {
-    lds_short4v* vs = (lds_short4v*)vstage(st) + (vfrag + 32 * hf * VROW) / 4;
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int c = 0; c < OB; ++c)
-#pragma unroll
-      for (int uu = 0; uu < 2; ++uu) {
-        const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vs + (16 * uu * VROW + 32 * c) / 4);
-        const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vs + ((16 * uu + 8) * VROW + 32 * c) / 4);
-        const half4v lo_h = __builtin_bit_cast(half4v, lo);
-        const half4v hi_h = __builtin_bit_cast(half4v, hi);
-        vf[c][uu] = half8v{lo_h[0], lo_h[1], lo_h[2], lo_h[3], hi_h[0], hi_h[1], hi_h[2], hi_h[3]};
-      }
-  };
+    for (int u = 0; u < 2; ++u) P[h][u] = half8v{};
+  for (int i = tid; i < VTILE / 8; i += F2_NT) reinterpret_cast<half8v*>(V3)[i] = half8v{};
 
-  auto qk_mfma = [&](const half8v (&kf)[QS], floatx16& S) {
-    S = floatx16{};
-#pragma unroll
-    for (int s = 0; s < QS; ++s) S = mfma32(kf[s], qf[s], S);
+  // V^T fragment (c, u) of key half h: lane (d, hh) holds V[key(u, hh, 0..7)][32c + d]
+  // with key(u, hh, i) = 32h + 16u + 8(i/4) + 4hh + i%4, the key order of the
+  // S^T C layout, read through an LDS-space pointer ("lane base + immediate").
+  auto vfrag_read = [&](auto st, int h, int u, int c) __attribute__((always_inline)) -> half8v {
+    lds_short4v* vs = (lds_short4v*)vstage(st) + vfrag / 4;
+    const int off = (32 * h + 16 * u) * VROW + 32 * c;
+    const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vs + off / 4);
+    const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vs + (off + 8 * VROW) / 4);
+    const half4v lo_h = __builtin_bit_cast(half4v, lo);
+    const half4v hi_h = __builtin_bit_cast(half4v, hi);
+    return half8v{lo_h[0], lo_h[1], lo_h[2], lo_h[3], hi_h[0], hi_h[1], hi_h[2], hi_h[3]};
   };
 
-  auto pv_mfma = [&](const half8v (&vf)[OB][2], const half8v (&P)[2]) {
-#pragma unroll
-    for (int uu = 0; uu < 2; ++uu)
-#pragma unroll
-      for (int c = 0; c < OB; ++c) acc[c] = mfma32(vf[c][uu], P[uu], acc[c]);
+  // fp16 probability of one score with the running max msub of the latest X phase.
+  float msub = 0.f;
+  auto exp_p = [&](float sc) __attribute__((always_inline)) -> half_t {
+    return (half_t)fast_exp2(fmaf(sc, c2, -msub));
   };
 
-  // P = fp16(exp2(S*c - m)) with the running max; returns whether any row of the
-  // wave must raise its max (S is kept intact for that path).
-  auto softmax = [&](int j, int hf, floatx16& S, half8v (&P)[2], bool masked) -> bool {
-    if (masked) {
-      const int k0 = j * F2_BN + 32 * hf;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int kidx = k0 + (e >> 2) * 8 + 4 * hh + (e & 3);
-        if (kidx >= kv_len || (p.causal && kidx > qi)) S[e] = -INFINITY;
-      }
-    }
-    float mloc = S[0];
-#pragma unroll
-    for (int e = 1; e < 16; ++e) mloc = fmaxf(mloc, S[e]);
-    mloc = xlane32_max(mloc);
-    const bool need = mloc * c2 > m_run + F2_RESCALE_THRESHOLD;
-    const float msub = (m_run == -INFINITY) ? 0.f : m_run;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) P[e >> 3][e & 7] = (half_t)fast_exp2(fmaf(S[e], c2, -msub));
-    return need;
-  };
-
-  auto rescale = [&](floatx16& S, half8v (&P)[2]) {
-    float mloc = S[0];
-#pragma unroll
-    for (int e = 1; e < 16; ++e) mloc = fmaxf(mloc, S[e]);
-    mloc = xlane32_max(mloc);
-    const float mnew = fmaxf(m_run, mloc * c2);
-    const float alpha = (mnew == -INFINITY) ? 1.f : fast_exp2(m_run - mnew);
-    l_run *= alpha;
-#pragma unroll
-    for (int c = 0; c < OB; ++c) acc[c] *= alpha;
-    m_run = mnew;
-    const float msub = (mnew == -INFINITY) ? 0.f : mnew;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) P[e >> 3][e & 7] = (half_t)fast_exp2(fmaf(S[e], c2, -msub));
-  };
-
-  auto rowsum = [&](const half8v (&P)[2]) {
-    const half2v one = {(half_t)1.f, (half_t)1.f};
-    float s = l_run;
-#pragma unroll
-    for (int uu = 0; uu < 2; ++uu)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const half2v pr = {P[uu][2 * e], P[uu][2 * e + 1]};
-        s = __builtin_amdgcn_fdot2(pr, one, s, false);
-      }
-    l_run = s;
-  };
-
-  auto half_masked = [&](int j, int hf) __attribute__((always_inline)) {
-    const int k0 = j * F2_BN + 32 * hf;
-    return (k0 + 32 > kv_len) || (p.causal && k0 + 31 > wq0);
-  };
-
-  floatx16 SA, SB;
-  half8v P[2];
-
-  // Scores of keys past the sequence (or above the diagonal) -> -inf, in place.
-  auto mask_scores = [&](int j, int hf, floatx16& S) __attribute__((always_inline)) {
-    const int k0 = j * F2_BN + 32 * hf;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int kidx = k0 + (e >> 2) * 8 + 4 * hh + (e & 3);
-      if (kidx >= kv_len || (p.causal && kidx > qi)) S[e] = -INFINITY;
-    }
-  };
-
-  // One half-step (32 keys), a single code path for every half-step so the O
-  // accumulators never move between registers:
-  //   A  K fragment reads for the next half's QK (past the last tile they re-read
-  //      the current stage and the scores are discarded);
-  //   B  QK(next) MFMAs interleaved with this half's softmax VALU and the V^T
-  //      fragment reads;
-  //   C  the rare rescale, the row sum and the PV MFMAs.
-  // Masking is a wave-uniform in-place fix-up of the current scores.
-  // st: stage of tile j; the next half's K comes from the same stage (hf = 0) or
-  // the next one (hf = 1; past the last tile that stage holds stale keys and the
-  // scores are discarded).
-  auto half_step = [&](int j, int hf, floatx16& Scur, floatx16& Snext, auto st) __attribute__((always_inline)) {
+  // G(j): S = K_j Q^T, O += V_{j-1}^T P_{j-1}; the probabilities of keys 32..63 of
+  // tile j-1 are computed under the first (key half 0) QK MFMAs, before QK
+  // overwrites those scores.
+  auto g_phase = [&](int j, auto st) __attribute__((always_inline)) {
     constexpr int ST = decltype(st)::value;
-    half8v kf[QS];
-    if (hf == 0)
-      load_kfrags(st, 1, kf);
-    else
-      load_kfrags(std::integral_constant<int, (ST + 1) % F2_STAGES>{}, 0, kf);
-    if (half_masked(j, hf)) mask_scores(j, hf, Scur);
-    __builtin_amdgcn_sched_barrier(0);
-    qk_mfma(kf, Snext);
-    const bool need = softmax(j, hf, Scur, P, false);
-    // P is used here, above the rescale branch: otherwise the compiler sinks the
-    // exponentials below it (into both paths) and they no longer overlap the MFMAs.
-    asm volatile("" ::"v"(P[0]), "v"(P[1]));
-    half8v vf[OB][2];
-    load_vfrags(st, hf, vf);
+    using SPREV = std::integral_constant<int, (ST + 3) % F2_STAGES>;
+    const lds_half8v* ks = (const lds_half8v*)(kstage(st) + kfrag);
+    // Anchor the keys-32..63 exponentials in this phase (the compiler would hoist
+    // them above the barrier into the VALU phase).
+    // The phase is a fixed sequence of NOPS MFMAs: QK (op i < 2*QS: key half i/QS,
+    // d-step i%QS), PV (op 2*QS + k: key half k/(4*OB), 16-key block k/OB % 2, d
+    // block k%OB) and the four row-sum MFMAs.  Operand fragments come from LDS
+    // F2_READ_AHEAD ops ahead of their MFMA through a small register ring; the
+    // sched_barriers pin that order (the scheduler would otherwise trade the
+    // read-ahead for registers).
+    constexpr int NQK = 2 * QS, NPV = 4 * OB, NOPS = NQK + NPV + 4;
+    constexpr int RING = F2_READ_AHEAD + 1;
+    half8v ring[RING];
+    auto read_op = [&](int i) __attribute__((always_inline)) -> half8v {
+      if (i < NQK) return ks[(i / QS) * (32 * KROW / 8) + 2 * (i % QS)];
+      const int k = i - NQK;
+      return vfrag_read(SPREV{}, k / (2 * OB), (k / OB) & 1, k % OB);
+    };
 #pragma unroll
-    for (int i = 0; i < QS; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // two V^T fragment reads
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // six VALU
+    for (int i = 0; i < F2_READ_AHEAD; ++i) ring[i % RING] = read_op(i);
+#pragma unroll
+    for (int i = 0; i < NOPS; ++i) {
+      if (i + F2_READ_AHEAD < NQK + NPV) ring[(i + F2_READ_AHEAD) % RING] = read_op(i + F2_READ_AHEAD);
+      if (i < NQK) {
+        const int h = i / QS;
+        S[h] = mfma32(ring[i % RING], qf[i % QS], i % QS == 0 ? floatx16{} : S[h]);
+      } else if (i < NQK + NPV) {
+        const int k = i - NQK;
+        acc[k % OB] = mfma32(ring[i % RING], P[k / (2 * OB)][(k / OB) & 1], acc[k % OB]);
+      } else {
+        const int r = i - NQK - NPV;
+        lsum = mfma32(ones, P[r >> 1][r & 1], lsum);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    if (__any(need)) rescale(Scur, P);
-    rowsum(P);
-    pv_mfma(vf, P);
+    asm volatile("" ::"v"(S[0]), "v"(S[1]));
   };
 
-  // Four stages, two tiles of prefetch: iteration j reads tiles j and j+1 (the
-  // second half-step starts the next tile's QK), tile j+2 is in flight and tile
-  // j+3 is issued into the stage tile j-1 used.  Loads retire in order and every
-  // tile is SPW copies per wave, so "tiles <= j+1 landed" is vmcnt(SPW).  The
-  // barrier is written out (s_barrier after lgkmcnt(0)) so that the compiler does
-  // not turn it into a wait for every copy in flight.
-  auto lds_barrier = [&]() __attribute__((always_inline)) {
+  // Final PV of the last tile (stage st).
+  auto pv_last = [&](auto st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int c = 0; c < OB; ++c) acc[c] = mfma32(vfrag_read(st, h, u, c), P[h][u], acc[c]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) lsum = mfma32(ones, P[h][u], lsum);
+  };
+
+  // X(j): the tile copies (tile j+2, staged in registers during X(j-1), goes to
+  // LDS; the loads of tile j+3 start), then P = fp16(exp2(S*c - m)) with the
+  // running max m, rescaling O first when a row's max grew by more than 2^8.  The
+  // copies sit in the VALU phase so that their LDS writes never queue ahead of
+  // the fragment reads of this wave's MFMA phase.
+  auto x_phase = [&](int j, auto st) __attribute__((always_inline)) {
+    using SW = std::integral_constant<int, (decltype(st)::value + 2) % F2_STAGES>;
+#pragma unroll
+    for (int r = 0; r < SPW; ++r) {
+      store_seg(r, SW{});      // tile j+2
+      load_seg(r, j + 3);      // all zeros past the last tile
+    }
+    const int k0 = j * F2_BN;
+    if ((k0 + F2_BN > kv_len) || (p.causal && k0 + F2_BN - 1 > wq0)) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int kidx = k0 + 32 * h + (e >> 2) * 8 + 4 * hh + (e & 3);
+          if (kidx >= kv_len || (p.causal && kidx > qi)) S[h][e] = -INFINITY;
+        }
+    }
+    // NaN-propagating maximum (v_maximum3_f32, no operand canonicalisation) as a
+    // shallow tree: 32 scores -> 8 partial maxima -> 1.
+    auto mx = [](float a, float b) __attribute__((always_inline)) { return __builtin_elementwise_maximum(a, b); };
+    float part[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) part[i] = mx(mx(S[i >> 2][4 * (i & 3)], S[i >> 2][4 * (i & 3) + 1]),
+                                            mx(S[i >> 2][4 * (i & 3) + 2], S[i >> 2][4 * (i & 3) + 3]));
+    float mloc = mx(mx(mx(part[0], part[1]), mx(part[2], part[3])), mx(mx(part[4], part[5]), mx(part[6], part[7])));
+    mloc = xlane32_max(mloc) * c2;
+    if (__any(mloc > m_run + F2_RESCALE_THRESHOLD)) {
+      const float mnew = fmaxf(m_run, mloc);
+      const float alpha = (mnew == -INFINITY) ? 1.f : fast_exp2(m_run - mnew);
+      lsum *= alpha;
+#pragma unroll
+      for (int c = 0; c < OB; ++c) acc[c] *= alpha;
+      m_run = mnew;
+    }
+    msub = (m_run == -INFINITY) ? 0.f : m_run;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) P[0][e >> 3][e & 7] = exp_p(S[0][e]);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) P[1][e >> 3][e & 7] = exp_p(S[1][e]);
+    asm volatile("" ::"v"(P[0][0]), "v"(P[0][1]), "v"(P[1][0]), "v"(P[1][1]));
+  };
+
+  // The barrier is written out (s_barrier after lgkmcnt(0)) so that the compiler
+  // does not turn it into a wait for every copy in flight.
+  auto barrier = [&]() __attribute__((always_inline)) {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   };
+
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
   using S2 = std::integral_constant<int, 2>;
   using S3 = std::integral_constant<int, 3>;
-  if (ntiles > 0) {
-    issue_tile(0, S0{});
-    issue_tile(1, S1{});
-    issue_tile(2, S2{});
-    wait_vmcnt_imm<2 * SPW>();   // tile 0 landed
-    lds_barrier();
-    half8v kf[QS];
-    load_kfrags(S0{}, 0, kf);
-    qk_mfma(kf, SA);
-  }
+  load_tile(0);
+  store_tile(S0{});
+  load_tile(1);
+  store_tile(S1{});
+  load_tile(2);
+#pragma unroll
+  for (int e = 0; e < 16; ++e) S[1][e] = -INFINITY;   // G(0) derives P[1] of tile "-1": zeros
+  barrier();                      // tiles 0 and 1 resident
+  if (group == 1) barrier();      // group 1 runs one phase behind
   // Tile j uses stage j % 4; the loop is unrolled by four so every stage is static.
-  auto tile_iter = [&](int j, auto st) __attribute__((always_inline)) {
-    constexpr int ST = decltype(st)::value;
-    // Tiles j, j+1 resident for every wave; the barrier also retires all reads of
-    // stage (j+3)%4 = (j-1)%4 from iteration j-1 before it is overwritten.
-    wait_vmcnt_imm<SPW>();
-    lds_barrier();
-    issue_tile(j + 3, std::integral_constant<int, (ST + 3) % F2_STAGES>{});
-    half_step(j, 0, SA, SB, st);
-    half_step(j, 1, SB, SA, st);
+  // Stage (j+2)%4, written in X(j), last held tile j-2, whose V was read by
+  // G(j-1) of both groups (at least one barrier back for either group); tile j+2
+  // is first read by G(j+2), two or more barriers later.
+  auto step = [&](int j, auto st) __attribute__((always_inline)) {
+    g_phase(j, st);
+    barrier();
+    x_phase(j, st);
+    barrier();
+    if (j == ntiles - 1) pv_last(st);
   };
   for (int j = 0; j < ntiles; j += F2_STAGES) {
-    tile_iter(j, S0{});
-    if (j + 1 < ntiles) tile_iter(j + 1, S1{});
-    if (j + 2 < ntiles) tile_iter(j + 2, S2{});
-    if (j + 3 < ntiles) tile_iter(j + 3, S3{});
+    step(j, S0{});
+    if (j + 1 < ntiles) step(j + 1, S1{});
+    if (j + 2 < ntiles) step(j + 2, S2{});
+    if (j + 3 < ntiles) step(j + 3, S3{});
   }
+  if (group == 0) barrier();      // same barrier count for both groups
+  wait_vmcnt_imm<0>();            // loads of tiles past the end (no memory traffic)
 
-  const float l_tot = xlane32_sum(l_run);
+  const float l_tot = lsum[0];
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (qi < p.Sq) {
     half_t* op = p.o + (int64_t)b * p.o_batch + (int64_t)head * p.o_head + (int64_t)qi * p.o_tok;
