@@ -130,17 +130,14 @@ __device__ __forceinline__ void load_q_fragment(const FlashParams& p, int b, int
 }
 
 template <int D>
-__global__ __launch_bounds__(F2_NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_attention_v2_kernel(FlashParams p) {
+__global__ __launch_bounds__(F2_NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void flash_attention_v2_kernel(FlashParams p) {
   constexpr int DCH = D / 8;             // 16-byte data chunks per row
   constexpr int QS = D / 16;
   constexpr int OB = D / 32;
   constexpr int KROW = D + 8;            // padded K row (halfs)
   constexpr int VROW = D + 32;           // padded V row (halfs)
-  constexpr int KRCH = KROW / 8, VRCH = VROW / 8;
-  constexpr int KTILE = F2_BN * KROW, VTILE = F2_BN * VROW;   // halfs; whole 1 KiB segments
-  static_assert(KTILE % 512 == 0 && VTILE % 512 == 0, "tile must be whole 1 KiB segments");
-  constexpr int NSEG = KRCH + VRCH;                            // 1 KiB copies per tile
-  constexpr int SPW = (NSEG + F2_WAVES - 1) / F2_WAVES;        // copies per wave (at most)
+  constexpr int KTILE = F2_BN * KROW, VTILE = F2_BN * VROW;   // halfs
 
   // One LDS object per stage: every access names its stage at compile time, so the
   // compiler can tell an in-flight global->LDS copy into one stage from reads of
@@ -195,74 +192,51 @@ __global__ __launch_bounds__(F2_NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))
   const half_t* kbase = p.k + (int64_t)b * p.k_batch + (int64_t)kvh * p.k_head;
   const half_t* vbase = p.v + (int64_t)b * p.v_batch + (int64_t)kvh * p.v_head;
 
-  // Segment sg of a padded tile holds linear 16-byte slots sg*64 .. sg*64+63;
-  // slot -> (row, chunk) of the padded layout.  The K segments (0 .. KRCH-1) and
-  // V segments (KRCH .. NSEG-1) of a tile are dealt round-robin: wave w copies
-  // combined segments w, w+8, w+16, ...  Each tile is read through a buffer
-  // descriptor whose base is its first key row and whose size ends at the last
-  // key row this workgroup uses (kend): rows past it, and every row of a tile past
-  // the last one, read as zeros without touching memory.  The per-lane offsets are
-  // therefore the same for every tile (computed once; 64 key rows fit in 2^31
-  // bytes, checked on the host).  Pad slots load a duplicate of the row's first
-  // chunk.
-  uint32_t soff[SPW];
-#pragma unroll
-  for (int r = 0; r < SPW; ++r) {
-    const int sg = min(wave + F2_WAVES * r, NSEG - 1);
-    const bool isk = sg < KRCH;
-    const int rch = isk ? KRCH : VRCH;
-    const int64_t tok = isk ? p.k_tok : p.v_tok;
-    const int pos = (isk ? sg : sg - KRCH) * 64 + lane;
-    const int ch = pos % rch;
-    soff[r] = ((uint32_t)((pos / rch) * tok) + (uint32_t)((ch < DCH ? ch : 0) * 8)) * 2u;
-  }
-  const int64_t ktile_bytes = (int64_t)F2_BN * p.k_tok * 2;
-  const int64_t vtile_bytes = (int64_t)F2_BN * p.v_tok * 2;
+  // Tile copies: thread t moves the 16-byte chunks t + F2_NT*r (r < CPT) of the K
+  // tile and of the V tile (chunk -> row, column: 16-lane coalesced rows in
+  // memory, padded rows in LDS), so only the tile's own bytes move.  Chunk r sits
+  // RSTEP*r rows below chunk 0: one per-lane offset per tensor, the row step goes
+  // into the (scalar) descriptor base and the LDS immediate.  Each copy reads
+  // through a buffer descriptor whose size ends at the last key row this
+  // workgroup uses (kend): rows past it, and every row of a tile past the last
+  // one, read as zeros without touching memory (64 key rows fit in 2^31 bytes,
+  // checked on the host).
+  constexpr int CPT = F2_BN * DCH / F2_NT;   // chunks per thread per tensor per tile
+  constexpr int RSTEP = F2_NT / DCH;
+  constexpr int NCP = 2 * CPT;               // copies per thread per tile: K chunks, then V chunks
+  static_assert(CPT * F2_NT == F2_BN * DCH && F2_NT % DCH == 0, "tile splits evenly over the threads");
+  const int crow = tid / DCH, cch = tid % DCH;
+  const uint32_t goff_k = ((uint32_t)(crow * p.k_tok) + (uint32_t)(cch * 8)) * 2u;
+  const uint32_t goff_v = ((uint32_t)(crow * p.v_tok) + (uint32_t)(cch * 8)) * 2u;
+  const uint32_t loff_k = (uint32_t)(crow * KROW + cch * 8) * 2u;
+  const uint32_t loff_v = (uint32_t)(crow * VROW + cch * 8) * 2u;
   const int64_t k_end = kend > 0 ? ((int64_t)(kend - 1) * p.k_tok + D) * 2 : 0;   // bytes from kbase
   const int64_t v_end = kend > 0 ? ((int64_t)(kend - 1) * p.v_tok + D) * 2 : 0;
-  struct TileSpan { const char* base; int n; };
-  auto tile_span = [&](const half_t* base, int64_t tile_bytes, int64_t end, int j)
-      __attribute__((always_inline)) -> TileSpan {
-    const int64_t off = (int64_t)j * tile_bytes;
-    const int64_t rem = end - off;
-    return {reinterpret_cast<const char*>(base) + off, rem <= 0 ? 0 : (int)min(rem, (int64_t)0x7fffffff)};
-  };
 
-  // Tile copies go global -> VGPR -> LDS.  load_tile(j) fetches this wave's
-  // segments of tile j into 16-byte staging registers; store_tile writes them
-  // into a stage with ds_write_b128 one MFMA phase later, so a full tile period
-  // of load latency is hidden behind the MFMAs.
-  u32x4 stg[SPW];
-  auto load_tile = [&](int j) __attribute__((always_inline)) {
-    const TileSpan rk = tile_span(kbase, ktile_bytes, k_end, j);
-    const TileSpan rv = tile_span(vbase, vtile_bytes, v_end, j);
-#pragma unroll
-    for (int r = 0; r < SPW; ++r) {
-      const int sg = wave + F2_WAVES * r;
-      if (r == SPW - 1 && sg >= NSEG) break;
-      stg[r] = sg < KRCH ? load16_bounded(rk.base, rk.n, soff[r]) : load16_bounded(rv.base, rv.n, soff[r]);
-    }
-  };
+  // Copies go global -> VGPR -> LDS: load_seg fetches copy r of tile j into a
+  // staging register, store_seg writes it into a stage one tile period later.
+  u32x4 stg[NCP];
   auto load_seg = [&](int r, int j) __attribute__((always_inline)) {
-    const int sg = wave + F2_WAVES * r;
-    if (r == SPW - 1 && sg >= NSEG) return;
-    const TileSpan sp = sg < KRCH ? tile_span(kbase, ktile_bytes, k_end, j) : tile_span(vbase, vtile_bytes, v_end, j);
-    stg[r] = load16_bounded(sp.base, sp.n, soff[r]);
+    const bool is_v = r >= CPT;
+    const int64_t tok_bytes = (is_v ? p.v_tok : p.k_tok) * 2;
+    const int64_t off = ((int64_t)j * F2_BN + RSTEP * (is_v ? r - CPT : r)) * tok_bytes;
+    const int64_t rem = (is_v ? v_end : k_end) - off;
+    const int n = rem <= 0 ? 0 : (int)min(rem, (int64_t)0x7fffffff);
+    stg[r] = load16_bounded(reinterpret_cast<const char*>(is_v ? vbase : kbase) + off, n, is_v ? goff_v : goff_k);
   };
   auto store_seg = [&](int r, auto st) __attribute__((always_inline)) {
-    const int sg = wave + F2_WAVES * r;
-    if (r == SPW - 1 && sg >= NSEG) return;
-    half_t* dst = sg < KRCH ? kstage(st) + sg * 512 : vstage(st) + (sg - KRCH) * 512;
-    *reinterpret_cast<u32x4*>(dst + lane * 8) = stg[r];
+    if (r < CPT)
+      *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(kstage(st)) + loff_k + RSTEP * r * KROW * 2) = stg[r];
+    else
+      *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(vstage(st)) + loff_v + RSTEP * (r - CPT) * VROW * 2) = stg[r];
+  };
+  auto load_tile = [&](int j) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < NCP; ++r) load_seg(r, j);
   };
   auto store_tile = [&](auto st) __attribute__((always_inline)) {
 #pragma unroll
-    for (int r = 0; r < SPW; ++r) {
-      const int sg = wave + F2_WAVES * r;
-      if (r == SPW - 1 && sg >= NSEG) break;
-      half_t* dst = sg < KRCH ? kstage(st) + sg * 512 : vstage(st) + (sg - KRCH) * 512;
-      *reinterpret_cast<u32x4*>(dst + lane * 8) = stg[r];
-    }
+    for (int r = 0; r < NCP; ++r) store_seg(r, st);
   };
 
   half8v qf[QS];
@@ -380,7 +354,7 @@ __global__ __launch_bounds__(F2_NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))
   auto x_phase = [&](int j, auto st) __attribute__((always_inline)) {
     using SW = std::integral_constant<int, (decltype(st)::value + 2) % F2_STAGES>;
 #pragma unroll
-    for (int r = 0; r < SPW; ++r) {
+    for (int r = 0; r < NCP; ++r) {
       store_seg(r, SW{});      // tile j+2
       load_seg(r, j + 3);      // all zeros past the last tile
     }
