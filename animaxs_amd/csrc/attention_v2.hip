@@ -195,44 +195,49 @@ void flash_attention_v2_kernel(FlashParams p) {
   // Tile copies: thread t moves the 16-byte chunks t + F2_NT*r (r < CPT) of the K
   // tile and of the V tile (chunk -> row, column: 16-lane coalesced rows in
   // memory, padded rows in LDS), so only the tile's own bytes move.  Chunk r sits
-  // RSTEP*r rows below chunk 0: one per-lane offset per tensor, the row step goes
-  // into the (scalar) descriptor base and the LDS immediate.  Each copy reads
-  // through a buffer descriptor whose size ends at the last key row this
-  // workgroup uses (kend): rows past it, and every row of a tile past the last
-  // one, read as zeros without touching memory (64 key rows fit in 2^31 bytes,
-  // checked on the host).
+  // RSTEP*r rows below chunk 0.  A tile is read through one buffer descriptor per
+  // tensor whose size ends at the last key row this workgroup uses (kend): rows
+  // past it, and every row of a tile past the last one, read as zeros without
+  // touching memory.  64 key rows fit in 2^31 bytes (checked on the host), so the
+  // per-lane offsets and sizes are 32-bit.
   constexpr int CPT = F2_BN * DCH / F2_NT;   // chunks per thread per tensor per tile
   constexpr int RSTEP = F2_NT / DCH;
   constexpr int NCP = 2 * CPT;               // copies per thread per tile: K chunks, then V chunks
   static_assert(CPT * F2_NT == F2_BN * DCH && F2_NT % DCH == 0, "tile splits evenly over the threads");
   const int crow = tid / DCH, cch = tid % DCH;
-  const uint32_t goff_k = ((uint32_t)(crow * p.k_tok) + (uint32_t)(cch * 8)) * 2u;
-  const uint32_t goff_v = ((uint32_t)(crow * p.v_tok) + (uint32_t)(cch * 8)) * 2u;
+  const uint32_t ktok2 = (uint32_t)p.k_tok * 2u, vtok2 = (uint32_t)p.v_tok * 2u;
+  uint32_t goff_k[CPT], goff_v[CPT];
+#pragma unroll
+  for (int r = 0; r < CPT; ++r) {
+    goff_k[r] = (uint32_t)(crow + RSTEP * r) * ktok2 + (uint32_t)cch * 16u;
+    goff_v[r] = (uint32_t)(crow + RSTEP * r) * vtok2 + (uint32_t)cch * 16u;
+  }
   const uint32_t loff_k = (uint32_t)(crow * KROW + cch * 8) * 2u;
   const uint32_t loff_v = (uint32_t)(crow * VROW + cch * 8) * 2u;
-  const int64_t k_end = kend > 0 ? ((int64_t)(kend - 1) * p.k_tok + D) * 2 : 0;   // bytes from kbase
-  const int64_t v_end = kend > 0 ? ((int64_t)(kend - 1) * p.v_tok + D) * 2 : 0;
+  // Valid bytes of tile j from its first row (the last valid row ends at column D).
+  auto tile_bytes = [&](int j, uint32_t tok2) __attribute__((always_inline)) -> int {
+    const int rows = kend - j * F2_BN;
+    return rows <= 0 ? 0 : rows >= F2_BN ? (int)(F2_BN * tok2) : (int)((uint32_t)(rows - 1) * tok2 + D * 2);
+  };
 
-  // Copies go global -> VGPR -> LDS: load_seg fetches copy r of tile j into a
-  // staging register, store_seg writes it into a stage one tile period later.
+  // Copies go global -> VGPR -> LDS: load_tile fetches this thread's chunks of tile
+  // j into staging registers, store_seg writes copy r into a stage one tile period
+  // later.
   u32x4 stg[NCP];
-  auto load_seg = [&](int r, int j) __attribute__((always_inline)) {
-    const bool is_v = r >= CPT;
-    const int64_t tok_bytes = (is_v ? p.v_tok : p.k_tok) * 2;
-    const int64_t off = ((int64_t)j * F2_BN + RSTEP * (is_v ? r - CPT : r)) * tok_bytes;
-    const int64_t rem = (is_v ? v_end : k_end) - off;
-    const int n = rem <= 0 ? 0 : (int)min(rem, (int64_t)0x7fffffff);
-    stg[r] = load16_bounded(reinterpret_cast<const char*>(is_v ? vbase : kbase) + off, n, is_v ? goff_v : goff_k);
+  auto load_tile = [&](int j) __attribute__((always_inline)) {
+    const char* kt = reinterpret_cast<const char*>(kbase) + (int64_t)j * F2_BN * ktok2;
+    const char* vt = reinterpret_cast<const char*>(vbase) + (int64_t)j * F2_BN * vtok2;
+    const int nk = tile_bytes(j, ktok2), nv = tile_bytes(j, vtok2);
+#pragma unroll
+    for (int r = 0; r < CPT; ++r) stg[r] = load16_bounded(kt, nk, goff_k[r]);
+#pragma unroll
+    for (int r = 0; r < CPT; ++r) stg[CPT + r] = load16_bounded(vt, nv, goff_v[r]);
   };
   auto store_seg = [&](int r, auto st) __attribute__((always_inline)) {
     if (r < CPT)
       *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(kstage(st)) + loff_k + RSTEP * r * KROW * 2) = stg[r];
     else
       *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(vstage(st)) + loff_v + RSTEP * (r - CPT) * VROW * 2) = stg[r];
-  };
-  auto load_tile = [&](int j) __attribute__((always_inline)) {
-#pragma unroll
-    for (int r = 0; r < NCP; ++r) load_seg(r, j);
   };
   auto store_tile = [&](auto st) __attribute__((always_inline)) {
 #pragma unroll
@@ -353,11 +358,8 @@ void flash_attention_v2_kernel(FlashParams p) {
   // the fragment reads of this wave's MFMA phase.
   auto x_phase = [&](int j, auto st) __attribute__((always_inline)) {
     using SW = std::integral_constant<int, (decltype(st)::value + 2) % F2_STAGES>;
-#pragma unroll
-    for (int r = 0; r < NCP; ++r) {
-      store_seg(r, SW{});      // tile j+2
-      load_seg(r, j + 3);      // all zeros past the last tile
-    }
+    store_tile(SW{});        // tile j+2
+    load_tile(j + 3);        // all zeros past the last tile
     const int k0 = j * F2_BN;
     if ((k0 + F2_BN > kv_len) || (p.causal && k0 + F2_BN - 1 > wq0)) {
 #pragma unroll
