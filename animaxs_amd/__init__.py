@@ -8,11 +8,11 @@ reference's Swift operator surface in Python over that ABI (``executors``).
 from ._abi import AnimaError, LIB_PATH, load  # noqa: F401
 from .executors import (  # noqa: F401
     AttentionExecutor, BlockOps, Context, DiTBlockExecutor, DitRoPE, LinearExecutor, QKPrologue,
-    QuantDecoders, QuantizedLinearWeightBuffers, as_buffer, qwen_rope,
+    QuantDecoders, QuantizedLinearWeightBuffers, QwenLayerExecutor, as_buffer, qwen_rope,
 )
 
 __all__ = [
     "AnimaError", "LIB_PATH", "load", "AttentionExecutor", "BlockOps", "Context", "DiTBlockExecutor",
     "DitRoPE", "LinearExecutor", "QKPrologue", "QuantDecoders", "QuantizedLinearWeightBuffers",
-    "as_buffer", "qwen_rope",
+    "QwenLayerExecutor", "as_buffer", "qwen_rope",
 ]

@@ -63,6 +63,7 @@ class AttentionArgs(C.Structure):
         ("causal", C.c_int32), ("layout", C.c_int32), ("token_stride", C.c_int64),
         ("batch", C.c_int64), ("key_lengths", C.c_void_p), ("key_lengths_on_device", C.c_int32),
         ("scale", C.c_float), ("prologue", C.POINTER(QKPrologue)),
+        ("kv_token_stride", C.c_int64),
     ]
 
 
@@ -93,6 +94,19 @@ class DitBlockArgs(C.Structure):
                 ("rope", C.c_void_p), ("tokens", C.c_int64), ("dim", C.c_int64), ("heads", C.c_int64),
                 ("head_dim", C.c_int64), ("context_tokens", C.c_int64), ("context_dim", C.c_int64),
                 ("mlp_hidden", C.c_int64), ("eps", C.c_float)]
+
+
+class QwenLayerWeights(C.Structure):
+    _fields_ = [(n, QWeight) for n in ("q", "k", "v", "o", "gate", "up", "down")] + [
+        ("input_norm", C.c_void_p), ("post_attention_norm", C.c_void_p),
+        ("q_norm", C.c_void_p), ("k_norm", C.c_void_p)]
+
+
+class QwenLayerArgs(C.Structure):
+    _fields_ = [("residual", Buffer), ("rope", C.c_void_p), ("key_lengths", C.c_void_p),
+                ("batch", C.c_int64), ("tokens", C.c_int64), ("hidden", C.c_int64), ("heads", C.c_int64),
+                ("kv_heads", C.c_int64), ("head_dim", C.c_int64), ("intermediate", C.c_int64),
+                ("eps", C.c_float)]
 
 
 # name -> (restype, argtypes)
@@ -132,6 +146,12 @@ SIGNATURES = {
     "anima_gelu_half_inplace_encode": (_S, [_P, Buffer, _I64]),
     "anima_silu_f32_encode": (_S, [_P, Buffer, Buffer, _I64]),
     "anima_add_f32_encode": (_S, [_P, Buffer, Buffer, _I64]),
+    "anima_rmsnorm_f32_to_half_encode": (_S, [_P, Buffer, Buffer, Buffer, _I64, _I64, C.c_float]),
+    "anima_gated_silu_half_encode": (_S, [_P, Buffer, Buffer, Buffer, _I64]),
+    "anima_add_half_into_float_encode": (_S, [_P, Buffer, Buffer, _I64]),
+    "anima_qwen_layer_create": (_S, [_P, _PP]),
+    "anima_qwen_layer_destroy": (_S, [_P]),
+    "anima_qwen_layer_encode": (_S, [_P, C.POINTER(QwenLayerWeights), C.POINTER(QwenLayerArgs)]),
     "anima_dit_block_create": (_S, [_P, _PP]),
     "anima_dit_block_destroy": (_S, [_P]),
     "anima_dit_block_encode": (_S, [_P, C.POINTER(DitBlockWeights), C.POINTER(DitBlockArgs)]),

@@ -222,6 +222,67 @@ anima_status anima_add_f32_encode(anima_ctx* ctx, anima_buffer destination, anim
   });
 }
 
+anima_status anima_rmsnorm_f32_to_half_encode(anima_ctx* ctx, anima_buffer input, anima_buffer weight,
+                                              anima_buffer output, int64_t n, int64_t rows, float eps) {
+  return guarded([&] {
+    require(ctx, "context");
+    if (n <= 0 || rows <= 0) fail(ANIMA_E_INVALID_SHAPE, "invalid rmsnorm shape");
+    if (!(eps >= 0.f && std::isfinite(eps))) fail(ANIMA_E_INVALID_ARGUMENT, "rmsnorm epsilon must be finite");
+    check_elementwise(input, checked_product({rows, n}, "rmsnorm"), 4, "rmsnorm input");
+    check_elementwise(weight, n, 2, "rmsnorm weight");
+    check_elementwise(output, checked_product({rows, n}, "rmsnorm"), 2, "rmsnorm output");
+    DeviceGuard g(ctx);
+    launch_rmsnorm_half(static_cast<const float*>(input.ptr), static_cast<const half_t*>(weight.ptr),
+                        static_cast<half_t*>(output.ptr), n, rows, eps, ctx->stream);
+  });
+}
+
+anima_status anima_gated_silu_half_encode(anima_ctx* ctx, anima_buffer gate, anima_buffer up, anima_buffer output,
+                                          int64_t count) {
+  return guarded([&] {
+    require(ctx, "context");
+    check_elementwise(gate, count, 2, "gated_silu gate");
+    check_elementwise(up, count, 2, "gated_silu up");
+    check_elementwise(output, count, 2, "gated_silu output");
+    if (count == 0) return;
+    DeviceGuard g(ctx);
+    launch_gated_silu(static_cast<const half_t*>(gate.ptr), static_cast<const half_t*>(up.ptr),
+                      static_cast<half_t*>(output.ptr), count, ctx->stream);
+  });
+}
+
+anima_status anima_add_half_into_float_encode(anima_ctx* ctx, anima_buffer residual, anima_buffer branch,
+                                              int64_t count) {
+  return guarded([&] {
+    require(ctx, "context");
+    check_elementwise(residual, count, 4, "add_half residual");
+    check_elementwise(branch, count, 2, "add_half branch");
+    if (count == 0) return;
+    DeviceGuard g(ctx);
+    launch_add_half(static_cast<float*>(residual.ptr), static_cast<const half_t*>(branch.ptr), count, ctx->stream);
+  });
+}
+
+// ---------------------------------------------------------------- Qwen layer
+anima_status anima_qwen_layer_create(anima_ctx* ctx, anima_qwen_layer** out) {
+  return guarded([&] {
+    require(out, "layer output");
+    *out = nullptr;
+    *out = new anima_qwen_layer(require(ctx, "context"));
+  });
+}
+
+anima_status anima_qwen_layer_destroy(anima_qwen_layer* layer) {
+  return guarded([&] { delete layer; });
+}
+
+anima_status anima_qwen_layer_encode(anima_qwen_layer* layer, const anima_qwen_layer_weights* w,
+                                     const anima_qwen_layer_args* args) {
+  return guarded([&] {
+    require(layer, "layer")->impl.encode(*require(w, "layer weights"), *require(args, "layer args"));
+  });
+}
+
 // ---------------------------------------------------------------- DiT block
 anima_status anima_dit_block_create(anima_ctx* ctx, anima_dit_block** out) {
   return guarded([&] {

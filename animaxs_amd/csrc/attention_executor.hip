@@ -39,6 +39,9 @@ void AttentionExecutor::encode(const anima_attention_args& a) {
   const int64_t H = a.heads, Sq = a.query_count, Sk = a.key_count, D = a.head_dim;
   const int64_t kvh = a.key_value_heads == 0 ? H : a.key_value_heads;
   const int64_t B = a.batch == 0 ? 1 : a.batch;
+  // K/V row stride: the reference contract shares token_stride; the extension
+  // kv_token_stride = kv_heads * head_dim admits grouped-query heads.
+  const int64_t kts = token_major ? (a.kv_token_stride > 0 ? a.kv_token_stride : ts) : 0;
 
   // ---- AttentionExecutor.validate (:778-825) ----
   if (!(H > 0 && Sq > 0 && Sk > 0 && D > 0 && kvh > 0 && H % kvh == 0 && a.query_offset >= 0 &&
@@ -46,16 +49,24 @@ void AttentionExecutor::encode(const anima_attention_args& a) {
         B > 0))
     fail(ANIMA_E_INVALID_SHAPE, "invalid attention shape, offset, or causal dimensions");
   if (token_major) {
-    if (!(ts > 0 && D <= ts && ts % D == 0 && H * D == ts && kvh == H))
+    if (a.kv_token_stride < 0) fail(ANIMA_E_INVALID_SHAPE, "kv_token_stride must be >= 0");
+    if (a.kv_token_stride == 0) {
+      if (!(ts > 0 && D <= ts && ts % D == 0 && H * D == ts && kvh == H))
+        fail(ANIMA_E_INVALID_SHAPE,
+             "P4 token-major attention requires tokenStride == heads * headDim and keyValueHeads == heads");
+    } else if (!(ts > 0 && H * D == ts && kvh * D == kts)) {
       fail(ANIMA_E_INVALID_SHAPE,
-           "P4 token-major attention requires tokenStride == heads * headDim and keyValueHeads == heads");
-    if (a.query_offset % 16 || a.key_offset % 16 || a.value_offset % 16 || a.output_offset % 16 || (ts * 2) % 16)
+           "grouped token-major attention requires tokenStride == heads * headDim and "
+           "kvTokenStride == keyValueHeads * headDim");
+    }
+    if (a.query_offset % 16 || a.key_offset % 16 || a.value_offset % 16 || a.output_offset % 16 || (ts * 2) % 16 ||
+        (kts * 2) % 16)
       fail(ANIMA_E_MISALIGNED, "P4 token-major attention requires 16-byte-aligned offsets and row stride");
   }
   int64_t q_bytes, k_bytes;
   if (token_major) {
     q_bytes = checked_product({B, Sq, ts, 2}, "attention");
-    k_bytes = checked_product({B, Sk, ts, 2}, "attention");
+    k_bytes = checked_product({B, Sk, kts, 2}, "attention");
   } else {
     q_bytes = checked_product({B, H, Sq, D, 2}, "attention");
     k_bytes = checked_product({B, kvh, Sk, D, 2}, "attention");
@@ -126,7 +137,7 @@ void AttentionExecutor::encode(const anima_attention_args& a) {
   int64_t q_tok, q_head, q_batch, k_tok, k_head, k_batch;
   if (token_major) {
     q_tok = ts; q_head = D; q_batch = Sq * ts;
-    k_tok = ts; k_head = D; k_batch = Sk * ts;
+    k_tok = kts; k_head = D; k_batch = Sk * kts;
   } else {
     q_tok = D; q_head = Sq * D; q_batch = H * Sq * D;
     k_tok = D; k_head = Sk * D; k_batch = kvh * Sk * D;
@@ -185,7 +196,7 @@ void AttentionExecutor::encode(const anima_attention_args& a) {
   p.q_tok = q_tok; p.q_head = q_head; p.q_batch = q_batch;
   p.k_tok = k_tok; p.k_head = k_head; p.k_batch = k_batch;
   if (token_major) {
-    p.v_tok = ts; p.v_head = D; p.v_batch = Sk * ts;
+    p.v_tok = kts; p.v_head = D; p.v_batch = Sk * kts;
     p.o_tok = ts; p.o_head = D; p.o_batch = Sq * ts;
   } else {
     p.v_tok = D; p.v_head = Sk * D; p.v_batch = kvh * Sk * D;

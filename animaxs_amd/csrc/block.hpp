@@ -1,5 +1,6 @@
 // DiT block support kernels and DiTBlockExecutor analog
-// (AnimaXS/Runtime/Metal/DiTBlockExecutor.swift:49-1319).
+// (AnimaXS/Runtime/Metal/DiTBlockExecutor.swift:49-1319); QwenLayerExecutor analog
+// (AnimaXS/Runtime/Metal/QwenEncoderMetal.swift:202-304).
 #pragma once
 
 #include "attention.hpp"
@@ -14,6 +15,10 @@ void launch_gate_add(float* residual, const half_t* branch, const float* gate, i
 void launch_gelu(half_t* values, int64_t count, hipStream_t stream);
 void launch_silu(const float* in, float* out, int64_t count, hipStream_t stream);
 void launch_add(float* dst, const float* src, int64_t count, hipStream_t stream);
+void launch_rmsnorm_half(const float* in, const half_t* w, half_t* out, int64_t n, int64_t rows, float eps,
+                         hipStream_t stream);
+void launch_gated_silu(const half_t* gate, const half_t* up, half_t* out, int64_t count, hipStream_t stream);
+void launch_add_half(float* residual, const half_t* branch, int64_t count, hipStream_t stream);
 
 class DitBlockExecutor {
  public:
@@ -27,7 +32,24 @@ class DitBlockExecutor {
   Workspace ws_;
 };
 
+class QwenLayerExecutor {
+ public:
+  explicit QwenLayerExecutor(anima_ctx* ctx);
+  void encode(const anima_qwen_layer_weights& w, const anima_qwen_layer_args& a);
+
+ private:
+  anima_ctx* ctx_;
+  AttentionExecutor attention_;
+  LinearExecutor linear_;
+  Workspace ws_;
+};
+
 }  // namespace anima
+
+struct anima_qwen_layer {
+  anima::QwenLayerExecutor impl;
+  explicit anima_qwen_layer(anima_ctx* c) : impl(c) {}
+};
 
 struct anima_dit_block {
   anima::DitBlockExecutor impl;

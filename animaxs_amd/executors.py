@@ -151,7 +151,7 @@ class AttentionExecutor:
     def _args(self, query, key, value, output, heads, query_count, key_count, head_dim,
               query_offset=0, key_offset=0, value_offset=0, output_offset=0, key_value_heads=None,
               causal=False, layout=None, batch=1, key_lengths=None, key_lengths_on_device=False,
-              scale=0.0, prologue: Optional[QKPrologue] = None):
+              scale=0.0, prologue: Optional[QKPrologue] = None, kv_token_stride: int = 0):
         lay, ts = self._layout(layout)
         keep = []
         kl = None
@@ -172,7 +172,7 @@ class AttentionExecutor:
             as_buffer(value), int(value_offset), as_buffer(output), int(output_offset),
             int(heads), int(query_count), int(key_count), int(head_dim),
             int(key_value_heads or 0), int(bool(causal)), lay, ts, int(batch), kl,
-            int(bool(key_lengths_on_device)), float(scale), pro)
+            int(bool(key_lengths_on_device)), float(scale), pro, int(kv_token_stride))
         return a, keep
 
     def encode(self, **kw) -> None:
@@ -366,6 +366,21 @@ class BlockOps:
     def silu(self, input, output, count: int) -> None:
         call("anima_silu_f32_encode", self.context.handle, as_buffer(input), as_buffer(output), int(count))
 
+    def rmsnorm_f32_to_half(self, input, weight, output, n: int, rows: int, eps: float = 1e-6) -> None:
+        """rmsnorm_f32_to_f32 + float_to_half (AnimaKernels.metal:172-204, :81-88)."""
+        call("anima_rmsnorm_f32_to_half_encode", self.context.handle, as_buffer(input), as_buffer(weight),
+             as_buffer(output), int(n), int(rows), float(eps))
+
+    def gated_silu_half(self, gate, up, output, count: int) -> None:
+        """gated_silu_half (AnimaKernels.metal:401-411)."""
+        call("anima_gated_silu_half_encode", self.context.handle, as_buffer(gate), as_buffer(up),
+             as_buffer(output), int(count))
+
+    def add_half_into_float(self, residual, branch, count: int) -> None:
+        """add_half_into_float (AnimaKernels.metal:639-647)."""
+        call("anima_add_half_into_float_encode", self.context.handle, as_buffer(residual), as_buffer(branch),
+             int(count))
+
     def add_f32(self, destination, source, count: int) -> None:
         call("anima_add_f32_encode", self.context.handle, as_buffer(destination), as_buffer(source), int(count))
 
@@ -398,6 +413,48 @@ class DiTBlockExecutor:
     def close(self):
         if self._h:
             call("anima_dit_block_destroy", self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class QwenLayerExecutor:
+    """QwenLayerExecutor.execute (QwenEncoderMetal.swift:232-304) for a batch of right-padded
+    sequences; the fp32 residual ``[batch, tokens, hidden]`` is updated in place."""
+
+    NAMES = ("q", "k", "v", "o", "gate", "up", "down")
+
+    def __init__(self, context: Context):
+        h = C.c_void_p()
+        call("anima_qwen_layer_create", context.handle, C.byref(h))
+        self._h = h
+        self.context = context
+
+    def encode(self, weights: dict, norms: dict, residual, rope, batch: int, tokens: int,
+               key_lengths=None, hidden: int = 1024, heads: int = 16, kv_heads: int = 8, head_dim: int = 128,
+               intermediate: int = 3072, eps: float = 1e-6) -> None:
+        w = _abi.QwenLayerWeights()
+        for n in self.NAMES:
+            setattr(w, n, weights[n].to_c())
+        for n in ("input_norm", "post_attention_norm", "q_norm", "k_norm"):
+            setattr(w, n, _ptr(norms[n]))
+        keep = None
+        kl = None
+        if key_lengths is not None:
+            keep = np.ascontiguousarray(np.asarray(key_lengths, dtype=np.int32))
+            kl = C.c_void_p(keep.ctypes.data)
+        a = _abi.QwenLayerArgs(as_buffer(residual), _ptr(rope), kl, int(batch), int(tokens), int(hidden),
+                               int(heads), int(kv_heads), int(head_dim), int(intermediate), float(eps))
+        call("anima_qwen_layer_encode", self._h, C.byref(w), C.byref(a))
+        del keep
+
+    def close(self):
+        if self._h:
+            call("anima_qwen_layer_destroy", self._h)
             self._h = C.c_void_p()
 
     def __del__(self):

@@ -205,6 +205,9 @@ def main():
     if not args.no_block:
         block_ms = time_block(torch, A, ctx, stream, args)
         print(f"# DiT block S4096: {block_ms:.3f} ms", file=sys.stderr, flush=True)
+        qwen = time_qwen_layer(torch, A, ctx, stream, args)
+        extra["qwen_layer_b4_s512"] = qwen
+        print(f"# Qwen layer B4 S512: {qwen}", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -373,6 +376,44 @@ def time_block(torch, A, ctx, stream, args):
         blk.encode(weights, norms, residual, emb, adaln, ctxt, rope, tokens=S)
 
     return time_region(torch, stream, step, args.block_steps, 2)
+
+
+def time_qwen_layer(torch, A, ctx, stream, args):
+    """ms per Qwen encoder layer (workload 4 shape: B=4 right-padded sequences of 512
+    tokens, hidden 1024, 16/8 heads, MLP 3072, all seven linears W8 symmetric, group 64)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1004)
+    B, S, hidden, H, Hkv, D, inter = 4, 512, 1024, 16, 8, 128, 3072
+    keep = []
+
+    def w8(n, k):
+        p = torch.randint(0, 256, (n, k), device="cuda", generator=g, dtype=torch.uint8)
+        sc = (1e-4 + 2e-4 * torch.rand(n, k // 64, device="cuda", generator=g)).half()
+        z = (-128 * sc.float()).half()
+        keep.extend([p, sc, z])
+        return A.QuantizedLinearWeightBuffers(1, p, sc, z, n, k, k)
+
+    shapes = {"q": (H * D, hidden), "k": (Hkv * D, hidden), "v": (Hkv * D, hidden), "o": (hidden, H * D),
+              "gate": (inter, hidden), "up": (inter, hidden), "down": (hidden, inter)}
+    weights = {n: w8(*s) for n, s in shapes.items()}
+    norms = {"input_norm": (0.8 + 0.4 * torch.rand(hidden, device="cuda", generator=g)).half(),
+             "post_attention_norm": (0.8 + 0.4 * torch.rand(hidden, device="cuda", generator=g)).half(),
+             "q_norm": (0.8 + 0.4 * torch.rand(D, device="cuda", generator=g)).half(),
+             "k_norm": (0.8 + 0.4 * torch.rand(D, device="cuda", generator=g)).half()}
+    residual = torch.randn(B, S, hidden, device="cuda", generator=g)
+    rope = torch.from_numpy(A.qwen_rope(S)).cuda()
+    lengths = [115, 165, 240, 509]
+    layer = A.QwenLayerExecutor(ctx)
+
+    def step(i):
+        layer.encode(weights, norms, residual, rope, batch=B, tokens=S, key_lengths=lengths)
+
+    ms = time_region(torch, stream, step, args.block_steps, 2)
+    rows = B * S
+    lin = 2 * rows * sum(n * k for n, k in shapes.values())
+    att = sum(2 * D * L * (L + 1) for L in lengths) * H
+    return {"ms": round(ms, 5), "tflops": round((lin + att) / ms / 1e9, 2), "gflop": round((lin + att) / 1e9, 2),
+            "key_lengths": lengths}
 
 
 def cpu_baseline():

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ANIMA_HIP_ABI_VERSION 1
+#define ANIMA_HIP_ABI_VERSION 2
 
 /* Status codes.  The reference throws AnimapkError.validation(String)
  * (Runtime/Animapk/MappedFile.swift:14) for every failure; the codes split that
@@ -164,6 +164,11 @@ typedef struct anima_attention_args {
                                     array, clamped to [1, key_count] by the kernel */
   float scale;                 /* 0 -> 1/sqrt(head_dim) (AttentionExecutor.swift:153) */
   const anima_qk_prologue* prologue; /* NULL -> none */
+  int64_t kv_token_stride;     /* TOKEN_MAJOR K/V row stride in halfs: 0 -> the reference contract
+                                  (K/V share token_stride, key_value_heads == heads); otherwise
+                                  key_value_heads * head_dim, which admits grouped-query heads
+                                  with token-major [rows, heads*D] Q/O and [rows, kv_heads*D] K/V
+                                  (the Qwen projections' natural layout, no transposes). */
 } anima_attention_args;
 
 anima_status anima_attention_encode(anima_attention* attn, const anima_attention_args* args);
@@ -334,6 +339,44 @@ anima_status anima_dit_block_create(anima_ctx* ctx, anima_dit_block** out);
 anima_status anima_dit_block_destroy(anima_dit_block* blk);
 anima_status anima_dit_block_encode(anima_dit_block* blk, const anima_dit_block_weights* w,
                                     const anima_dit_block_args* args);
+
+/* ------------------------------------------------------------------------- */
+/* Qwen encoder layer: QwenLayerExecutor.execute (QwenEncoderMetal.swift:232-304)  */
+/* for a batch of right-padded sequences, fp32 residual updated in place.        */
+/* ------------------------------------------------------------------------- */
+/* rmsnorm_f32_to_f32 (AnimaKernels.metal:172-204) followed by float_to_half
+ * (:81-88), fused: out[r][i] = half(in[r][i] * rsqrt(mean(in[r]^2) + eps) * w[i]). */
+anima_status anima_rmsnorm_f32_to_half_encode(anima_ctx* ctx, anima_buffer input,
+                                              anima_buffer weight, anima_buffer output,
+                                              int64_t n, int64_t rows, float eps);
+/* gated_silu_half (AnimaKernels.metal:401-411): out = half(silu(gate) * up), fp32 maths. */
+anima_status anima_gated_silu_half_encode(anima_ctx* ctx, anima_buffer gate, anima_buffer up,
+                                          anima_buffer output, int64_t count);
+/* add_half_into_float (AnimaKernels.metal:639-647): residual[i] += float(branch[i]). */
+anima_status anima_add_half_into_float_encode(anima_ctx* ctx, anima_buffer residual,
+                                              anima_buffer branch, int64_t count);
+
+typedef struct anima_qwen_layer_weights {
+  anima_qweight q, k, v, o, gate, up, down;  /* W8 in the reference; W4/W8/FP16 accepted */
+  const void* input_norm;            /* fp16 [hidden] */
+  const void* post_attention_norm;   /* fp16 [hidden] */
+  const void* q_norm;                /* fp16 [head_dim] */
+  const void* k_norm;                /* fp16 [head_dim] */
+} anima_qwen_layer_weights;
+
+typedef struct anima_qwen_layer_args {
+  anima_buffer residual;        /* fp32 [batch][tokens][hidden], updated in place */
+  const float* rope;            /* device fp32 [tokens][head_dim/2][2][2] (anima_rope_neox) */
+  const int32_t* key_lengths;   /* host, per sequence, 1..tokens; NULL = every token valid */
+  int64_t batch, tokens, hidden, heads, kv_heads, head_dim, intermediate;
+  float eps;
+} anima_qwen_layer_args;
+
+typedef struct anima_qwen_layer anima_qwen_layer;
+anima_status anima_qwen_layer_create(anima_ctx* ctx, anima_qwen_layer** out);
+anima_status anima_qwen_layer_destroy(anima_qwen_layer* layer);
+anima_status anima_qwen_layer_encode(anima_qwen_layer* layer, const anima_qwen_layer_weights* w,
+                                     const anima_qwen_layer_args* args);
 
 #ifdef __cplusplus
 }

@@ -1,4 +1,4 @@
-"""DiT block composition oracle (torch-CPU fp32, optional fp16 boundaries).
+"""DiT block and Qwen layer composition oracles (torch-CPU fp32, optional fp16 boundaries).
 
 Restates ``scripts/dit_block0_oracle.py:327-391`` (the MiniTrainDIT block of
 ComfyUI predict2.py as transcribed there):
@@ -24,7 +24,7 @@ from __future__ import annotations
 import torch
 
 from . import attention as attn
-from .norms import gelu_erf, layer_norm_modulated, silu
+from .norms import gelu_erf, layer_norm_modulated, rms_norm, silu
 from .quant import dequant_matrix_f32
 
 
@@ -116,3 +116,45 @@ def block_flops(S: int = 4096, ctx_tokens: int = 512, dim: int = 2048, ctx_dim: 
     lin += 2 * S * dim * hidden * 2                  # mlp1, mlp2
     att = 4 * heads * hd * S * S + 4 * heads * hd * S * ctx_tokens
     return float(lin + att)
+
+
+def qwen_layer(d: dict, boundary: str = "fp16", weights: dict | None = None,
+               return_intermediates: bool = False):
+    """One Qwen encoder layer on ``d`` (``oracle.inputs.qwen_layer``) -> fp32 residual [B, S, hidden].
+
+    Restates QwenLayerExecutor.execute (QwenEncoderMetal.swift:244-303) and the layer of
+    scripts/qwen_comfy_oracle.py:268-300: RMSNorm(input_layernorm) -> fp16 -> q/k/v
+    projections -> per-head RMSNorm + split-half RoPE on q,k -> causal GQA attention with
+    the right-padding key mask -> o projection -> x += o -> RMSNorm(post_attention_layernorm)
+    -> fp16 -> gate/up -> SiLU(gate)*up (fp32, one rounding, gated_silu_half
+    AnimaKernels.metal:401-411) -> down -> x += down.  The residual is fp32; with
+    ``boundary="fp16"`` every activation the reference stores as fp16 is rounded there."""
+    W = weights if weights is not None else dequant_weights(d)
+    x = d["x"].float()
+    B, S, hidden = x.shape
+    H, Hkv, hd = d["heads"], d["kv_heads"], 128
+    eps = d["eps"]
+    lengths = d.get("key_lengths")
+    inter = {}
+
+    def proj(a, name):
+        return _bq(a @ W[name].T, boundary)
+
+    n = _bq(rms_norm(x, d["input_norm"], eps), boundary)
+    q = proj(n, "q").reshape(B, S, H, hd)
+    k = proj(n, "k").reshape(B, S, Hkv, hd)
+    v = proj(n, "v").reshape(B, S, Hkv, hd)
+    q = _bq(attn.qk_prologue(q, d["q_norm"], eps, d["rope"]), boundary)
+    k = _bq(attn.qk_prologue(k, d["k_norm"], eps, d["rope"]), boundary)
+    a = _bq(attn.sdpa(q, k, v, causal=True, key_lengths=lengths).reshape(B, S, H * hd), boundary)
+    inter["attention"] = a.clone()
+    x = x + proj(a, "o")
+    inter["x1"] = x.clone()
+    n = _bq(rms_norm(x, d["post_attention_norm"], eps), boundary)
+    g = proj(n, "gate")
+    u = proj(n, "up")
+    h = _bq(silu(g) * u, boundary)
+    x = x + proj(h, "down")
+    if return_intermediates:
+        return x, inter
+    return x

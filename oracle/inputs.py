@@ -168,6 +168,47 @@ def dit_block(S: int = 4096, ctx_tokens: int = 512, ctx_dim: int = 1024,
     return d
 
 
+def symmetric_w8(g: torch.Generator, rows: int, cols: int, lo: float = 1e-4, hi: float = 3e-4) -> dict:
+    """Symmetric int8 weight in the reference's affine W8 layout: q ~U{0..255},
+    scale ~U(lo, hi) stored as fp16 per (row, 64-wide group), zero = -128 * scale
+    (exact in fp16)."""
+    q = torch.randint(0, 256, (rows, cols), generator=g, dtype=torch.int64).numpy().astype(np.uint8)
+    groups = (cols + 63) // 64
+    scale = _uniform(g, lo, hi, rows, groups).half()
+    zero = (scale.float() * -128.0).half()
+    assert torch.equal(zero.float(), scale.float() * -128.0)
+    return {
+        "storage": 1, "rows": rows, "cols": cols, "row_stride": cols,
+        "packed": q.reshape(-1), "scale_bits": scale.numpy().view(np.uint16),
+        "zero_bits": zero.numpy().view(np.uint16),
+    }
+
+
+QWEN_LINEARS = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+def qwen_layer(B: int = 4, S: int = 512, hidden: int = 1024, heads: int = 16, kv_heads: int = 8,
+               intermediate: int = 3072) -> dict:
+    """One Qwen3-0.6B-shaped encoder layer (QwenEncoderMetal.swift:202-304): W8 projections,
+    fp16 norm weights, fp32 residual [B, S, hidden], right padding with L_b ~U{min(8,S)..S}."""
+    g = _gen(4)
+    qdim, kvdim = heads * HEAD_DIM, kv_heads * HEAD_DIM
+    shapes = {"q": (qdim, hidden), "k": (kvdim, hidden), "v": (kvdim, hidden), "o": (hidden, qdim),
+              "gate": (intermediate, hidden), "up": (intermediate, hidden), "down": (hidden, intermediate)}
+    d = {
+        "x": torch.randn(B, S, hidden, generator=g, dtype=torch.float32),
+        "key_lengths": torch.randint(min(8, S), S + 1, (B,), generator=g, dtype=torch.int32),
+        "input_norm": _uniform(g, 0.8, 1.2, hidden).half(),
+        "post_attention_norm": _uniform(g, 0.8, 1.2, hidden).half(),
+        "q_norm": _uniform(g, 0.8, 1.2, HEAD_DIM).half(),
+        "k_norm": _uniform(g, 0.8, 1.2, HEAD_DIM).half(),
+        "rope": rope_mod.neox_rope_table(S, 1.0e6),
+        "eps": 1e-6, "heads": heads, "kv_heads": kv_heads,
+    }
+    d["w"] = {name: symmetric_w8(g, *shapes[name]) for name in QWEN_LINEARS}
+    return d
+
+
 def small_m_gemm(M: int, N: int, K: int, seed: int = 1006) -> dict:
     """Small-M W4 GEMM sweep inputs: X ~N(0,1) fp16 [M,K], symmetric W4 [N,K]."""
     g = torch.Generator(device="cpu")

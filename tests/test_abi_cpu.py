@@ -171,14 +171,59 @@ def test_w8_stride_uses_full_columns(ctx):
 
 
 def test_last_error_is_thread_local_and_set():
-    lib = _abi.load()
-    st = lib.anima_rope_dit3d(0, 1, 1, None)
-    assert st != 0
-    msg = lib.anima_last_error()
-    assert msg and len(msg) > 0
-    # a successful call on another thread does not clear this thread's message
+    import gc
     import threading
-    t = threading.Thread(target=lambda: lib.anima_fp16_to_float32(None, 0, None))
-    t.start()
-    t.join()
-    assert lib.anima_last_error() == msg
+    lib = _abi.load()
+    # Any successful call on this thread clears its message, including the destroy calls
+    # that finalizers of earlier tests' executors make: collect them first, then keep the
+    # collector off while the message must survive.
+    gc.collect()
+    gc.disable()
+    try:
+        st = lib.anima_rope_dit3d(0, 1, 1, None)
+        assert st != 0
+        msg = lib.anima_last_error()
+        assert msg and len(msg) > 0
+        # a successful call on another thread does not clear this thread's message
+        t = threading.Thread(target=lambda: lib.anima_fp16_to_float32(None, 0, None))
+        t.start()
+        t.join()
+        assert lib.anima_last_error() == msg
+    finally:
+        gc.enable()
+
+
+def test_grouped_token_major_contract(ctx):
+    """kv_token_stride (extension): token-major Q/O rows of heads*D with K/V rows of
+    kv_heads*D; any other K/V stride is refused before launch."""
+    ex = animaxs_amd.AttentionExecutor(ctx)
+    expect(lambda: ex.encode(**attn_kw(layout=("tokenMajor", 128), key_value_heads=1, kv_token_stride=32)),
+           _abi.E_INVALID_SHAPE, "kvTokenStride == keyValueHeads * headDim")
+    expect(lambda: ex.encode(**attn_kw(layout=("tokenMajor", 128), key_value_heads=1, kv_token_stride=-64)),
+           _abi.E_INVALID_SHAPE, "kv_token_stride must be >= 0")
+    # K/V ranges use the K/V stride: [4 tokens x 64] halfs is 512 bytes, one short fails.
+    expect(lambda: ex.encode(**attn_kw(layout=("tokenMajor", 128), key_value_heads=1, kv_token_stride=64,
+                                       key=buf(4 * 64 * 2 - 2))),
+           _abi.E_OUT_OF_BOUNDS, "attention buffer range is out of bounds")
+
+
+def _qwen_weights(hidden=64, qdim=128, kvdim=64, inter=96, bad=None):
+    shapes = {"q": (qdim, hidden), "k": (kvdim, hidden), "v": (kvdim, hidden), "o": (hidden, qdim),
+              "gate": (inter, hidden), "up": (inter, hidden), "down": (hidden, inter)}
+    if bad:
+        shapes[bad] = (shapes[bad][0] + 1, shapes[bad][1])
+    return {n: w4(rows=r, cols=c, storage=1, stride=c) for n, (r, c) in shapes.items()}
+
+
+def test_qwen_layer_validation(ctx):
+    layer = animaxs_amd.QwenLayerExecutor(ctx)
+    norms_ = {n: FAKE for n in ("input_norm", "post_attention_norm", "q_norm", "k_norm")}
+    kw = dict(batch=2, tokens=4, hidden=64, heads=2, kv_heads=1, head_dim=64, intermediate=96)
+    expect(lambda: layer.encode(_qwen_weights(), norms_, buf(2 * 4 * 64 * 4 - 4), FAKE, **kw),
+           _abi.E_OUT_OF_BOUNDS, "invalid Qwen layer input buffers")
+    expect(lambda: layer.encode(_qwen_weights(bad="down"), norms_, buf(2 * 4 * 64 * 4), FAKE, **kw),
+           _abi.E_INVALID_SHAPE, "invalid Qwen matrix down")
+    expect(lambda: layer.encode(_qwen_weights(), norms_, buf(2 * 4 * 64 * 4), FAKE, **dict(kw, kv_heads=3)),
+           _abi.E_INVALID_SHAPE, "invalid Qwen layer shape")
+    expect(lambda: layer.encode(_qwen_weights(), norms_, buf(2 * 4 * 64 * 4), None, **kw),
+           _abi.E_INVALID_ARGUMENT, "requires a RoPE table")

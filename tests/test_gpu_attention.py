@@ -100,6 +100,22 @@ def test_workload4_qwen_causal_gqa(ctx):
     assert_attention_close(o.permute(0, 2, 1, 3), ref, label="workload4 qwen causal gqa")
 
 
+@pytest.mark.parametrize("flash_rows", [128, 256])
+def test_workload4_token_major_grouped_kv_stride(ctx, flash_rows):
+    """Workload 4 on the projections' own token-major rows: Q/O [B, S, 16*128], K/V
+    [B, S, 8*128] (kv_token_stride extension), both flash variants."""
+    d = inputs.qwen_attention()
+    L = d["key_lengths"]
+    pro = QKPrologue(dev(d["q_norm_w"]), dev(d["k_norm_w"]), d["eps"], dev(d["rope"]), 512, True, True)
+    o = _run(ctx, dev(d["q"]), dev(d["k"]), dev(d["v"]), layout=("tokenMajor", 2048), heads=16, Sq=512, Sk=512,
+             D=128, out_shape=(4, 512, 16, 128), backend="flash", flash_rows=flash_rows, batch=4,
+             key_value_heads=8, kv_token_stride=1024, causal=True, key_lengths=L.numpy(), prologue=pro)
+    qq = oatt.qk_prologue(d["q"], d["q_norm_w"], d["eps"], d["rope"])
+    kk = oatt.qk_prologue(d["k"], d["k_norm_w"], d["eps"], d["rope"])
+    ref = oatt.sdpa(qq, kk, d["v"], causal=True, key_lengths=L.tolist())
+    assert_attention_close(o, ref, label=f"workload4 token-major grouped flash{flash_rows}")
+
+
 # ---------------------------------------------------------------------------
 # Reference special cases (AnimaXSTests/AttentionExecutorTests.swift)
 # ---------------------------------------------------------------------------

@@ -89,3 +89,61 @@ def test_layernorm_modulate_gelu_gate_add(ctx):
     ops.add_f32(a, so, 2048)
     torch.cuda.synchronize()
     assert torch.allclose(a.cpu(), 1 + norms.silu(e), atol=1e-6, rtol=1e-5)
+
+
+@pytest.mark.parametrize("B,S", [(2, 64), (4, 512)])
+def test_qwen_layer_matches_oracle(ctx, B, S):
+    """QwenLayerExecutor.execute (QwenEncoderMetal.swift:232-304) on right-padded sequences
+    against the oracle layer with fp16 boundaries."""
+    from animaxs_amd import QwenLayerExecutor
+    d = inputs.qwen_layer(B=B, S=S)
+    keep = []
+    weights = {}
+    for name, w in d["w"].items():
+        qw, k = device_weight(w)
+        weights[name] = qw
+        keep.append(k)
+    norms_d = {n: dev(d[n]) for n in ("input_norm", "post_attention_norm", "q_norm", "k_norm")}
+    residual = dev(d["x"].clone())
+    layer = QwenLayerExecutor(ctx)
+    layer.encode(weights, norms_d, residual, dev(d["rope"]), batch=B, tokens=S,
+                 key_lengths=d["key_lengths"].numpy())
+    torch.cuda.synchronize()
+    ref = blocks.qwen_layer(d, boundary="fp16")
+    y = residual.cpu()
+    assert torch.isfinite(y).all()
+    ma, mr = max_abs(y, ref), mean_rel(y, ref)
+    print(f"PARITY qwen_layer B{B} S{S}: max_abs={ma:.3e} mean_rel={mr:.3e} max_ref={float(ref.abs().max()):.3e}",
+          flush=True)
+    assert mr <= BLOCK_MEAN_REL
+    assert ma <= 5e-3 * float(ref.abs().max())
+
+
+def test_rmsnorm_gated_silu_add_half(ctx):
+    """rmsnorm_f32_to_f32 + float_to_half / gated_silu_half / add_half_into_float
+    (AnimaKernels.metal:172-204, 81-88, 401-411, 639-647)."""
+    g = torch.Generator().manual_seed(4)
+    rows, n = 29, 1024
+    x = torch.randn(rows, n, generator=g) * 2 + 0.25
+    w = (torch.rand(n, generator=g) * 0.4 + 0.8).half()
+    ops = BlockOps(ctx)
+    out = torch.zeros(rows, n, dtype=torch.float16, device="cuda")
+    ops.rmsnorm_f32_to_half(dev(x), dev(w), out, n, rows, 1e-6)
+    torch.cuda.synchronize()
+    ref = norms.rms_norm(x, w, 1e-6).half()
+    assert float((out.cpu().float() - ref.float()).abs().max()) <= 2 ** -10 * float(ref.float().abs().max())
+
+    gt = (torch.randn(5001, generator=g) * 4).half()
+    up = torch.randn(5001, generator=g).half()
+    o = torch.zeros(5001, dtype=torch.float16, device="cuda")
+    ops.gated_silu_half(dev(gt), dev(up), o, 5001)
+    torch.cuda.synchronize()
+    sref = (norms.silu(gt.float()) * up.float()).half()
+    assert float((o.cpu().float() - sref.float()).abs().max()) <= 2 ** -10 * max(1.0, float(sref.float().abs().max()))
+
+    res = torch.randn(rows, n, generator=g)
+    br = torch.randn(rows, n, generator=g).half()
+    rd = dev(res.clone())
+    ops.add_half_into_float(rd, dev(br), rows * n)
+    torch.cuda.synchronize()
+    assert torch.equal(rd.cpu(), res + br.float())
