@@ -50,26 +50,6 @@ static_assert(FLASH_V2_ROWS == 32 * F2_WAVES, "one 32-row block per wave");
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 
-// s_waitcnt vmcnt(n) alone (expcnt / lgkmcnt unconstrained), n in [0, 15].
-template <int N>
-__device__ __forceinline__ void wait_vmcnt_imm() {
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8));
-}
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// 16-byte load through a raw buffer descriptor of n bytes at base: offsets at or
-// past n read zeros without touching memory.  (The descriptor type exists in the
-// device pass only.)
-__device__ __forceinline__ u32x4 load16_bounded(const void* base, int n, uint32_t voff) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
-  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
-#else
-  return u32x4{};
-#endif
-}
-
 __device__ __forceinline__ float xlane32_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));

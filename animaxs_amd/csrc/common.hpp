@@ -76,6 +76,35 @@ __device__ __forceinline__ half_t f32_to_f16(float v) {
   return (half_t)v;
 }
 
+// s_waitcnt vmcnt(n) alone (expcnt / lgkmcnt unconstrained), n in [0, 15].
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_imm() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8));
+}
+
+// 16-byte load through a raw buffer descriptor of n bytes at base: offsets at or
+// past n read zeros without touching memory.  (The descriptor type exists in the
+// device pass only.)
+// soff is a wave-uniform byte offset added to every lane's voff.
+__device__ __forceinline__ u32x4 load16_bounded(const void* base, int n, uint32_t voff, int soff = 0) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+#else
+  return u32x4{};
+#endif
+}
+
+// 2-byte variant of load16_bounded (zero-extended).
+__device__ __forceinline__ uint32_t load2_bounded(const void* base, int n, uint32_t voff, int soff = 0) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+#else
+  return 0u;
+#endif
+}
+
 // Workgroup id remapped so that consecutive logical ids share an XCD: the
 // dispatcher places workgroup i on XCD i % 8, so logical id L is given to
 // physical id (L % per) * 8 + L / per when the grid is a multiple of 8.

@@ -379,6 +379,11 @@ static void launch_gemm_t(const GemmParams& p, bool fast, int vec, dim3 grid, hi
 }
 
 void launch_gemm(const GemmParams& p, int storage, hipStream_t stream) {
+  if (p.M <= 0 || p.N <= 0) return;
+  if (pingpong_supported(p, storage)) {
+    launch_pingpong(p, storage, stream);
+    return;
+  }
   const int64_t tiles = (int64_t)((p.M + G_BM - 1) / G_BM) * ((p.N + G_BN - 1) / G_BN);
   if (tiles <= 0) return;
   if (tiles > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "GEMM grid too large");

@@ -35,6 +35,25 @@ struct DequantParams {
   int N, K, groups, storage;
 };
 
+// Exponent of the unit in the last place of an fp16 value, as a biased field (1..31).
+__device__ __forceinline__ int fp16_unit_exponent(half_t v) {
+  const int e = (__builtin_bit_cast(uint16_t, v) >> 10) & 31;
+  return e < 1 ? 1 : e;
+}
+
+// True when q*s + z is exactly representable in fp32 for every code q < 2^QBITS.
+// q*s is an integer of at most QBITS+11 bits times s's unit, z one of at most 11
+// bits times its own unit; their sum spans at most 24 bits exactly when the unit
+// exponents differ by d = u(s) - u(z) with -12 <= d <= 12 - QBITS (or when s or z
+// is zero).
+// Written without short-circuits so that it compiles to straight-line code.
+template <int QBITS>
+__device__ __forceinline__ bool one_rounding_exact(half_t s, half_t z) {
+  const bool zero = ((__builtin_bit_cast(uint16_t, s) & 0x7fff) == 0) | ((__builtin_bit_cast(uint16_t, z) & 0x7fff) == 0);
+  const int d = fp16_unit_exponent(s) - fp16_unit_exponent(z);
+  return zero | ((d >= -12) & (d <= 12 - QBITS));
+}
+
 // Validated, resolved view of an anima_qweight.
 struct QWeightView {
   int storage;
@@ -49,6 +68,11 @@ struct QWeightView {
 QWeightView validate_weight(const anima_qweight& w, const char* who);
 
 void launch_gemm(const GemmParams& p, int storage, hipStream_t stream);
+
+// Ping-pong W4/W8 GEMM (linear_pingpong.hip): K a multiple of 64, 16-byte aligned X
+// and weight rows, buffers below 2 GiB.  launch_gemm routes to it when it applies.
+bool pingpong_supported(const GemmParams& p, int storage);
+void launch_pingpong(const GemmParams& p, int storage, hipStream_t stream);
 
 // Weight-streaming GEMM for M <= SMALLM_MAX_ROWS (linear_smallm.hip); requires K a
 // multiple of 128 and 16-byte aligned X and weight rows.

@@ -1,0 +1,446 @@
+// Quantized GEMM for M > 64 on gfx950: Y[M,N] = X[M,K] deq(W)[N,K]^T for W4/W8
+// weights, computed as C^T = W X^T on v_mfma_f32_32x32x16_f16.
+//
+// Replaces the qgemm_w4/w8 path of LinearExecutor.encodeQGEMM
+// (AnimaXS/Runtime/Metal/LinearExecutor.swift:304-361; kernels at
+// AnimaXS/Shaders/AnimaKernels.metal:955-1047).  Organisation:
+//   * Workgroup tile 128 (M) x 256 (N), 8 waves in two groups of 4.  Wave w of a
+//     group owns output columns 64w .. 64w+63 and all 128 rows (2 x 4 MFMA
+//     tiles); waves w and w+4 share a SIMD and the same output tile.  Group 0
+//     takes the first half of the K blocks (64 = one quantisation group), group 1
+//     the second; the two partial sums meet in LDS at the end (fp32, fixed order).
+//   * Each K block j of a group is two phases per wave, separated by workgroup
+//     barriers:
+//       M  the 32 MFMAs of block j, X fragments read from LDS a few MFMAs ahead,
+//          with the dequantisation of block j+1 interleaved (half a fragment per
+//          MFMA pair, into the registers the MFMAs have finished with);
+//       V  scale/zero of block j+2 from the LDS window, the X tile of block j+1 to
+//          LDS, and the loads of X(j+2) and of the weights of block j+3.
+//     Group 1 runs one phase behind group 0, so in every barrier interval one
+//     wave of each SIMD issues MFMAs while the other issues the memory work.
+//   * Weights never touch LDS: each lane loads its own rows' packed bytes (16 B
+//     per row per block for W4, two blocks in flight) and dequantises them in
+//     registers.  X is shared through LDS (one stage per group); scale/zero pairs
+//     are read 8 groups at a time per row into an LDS window when the rows allow.
+//   * Dequantisation is bit-identical to the reference decoder's
+//     half(fl32(q*scale + zero)).  When q*scale + zero is exact in fp32 for every
+//     code (one_rounding_exact), packed fp16 arithmetic gives the same bits with
+//     one rounding: q is rebuilt exactly from the fp16 pattern 0x6400|q
+//     (= 1024 + q) and v_pk_fma_f16(q, s, z) rounds once.  The MFMA phase always
+//     runs that form, branch-free; a wave whose block fails the test redoes it
+//     with the fp32 FMA and separate RNE conversion (a rare, wave-uniform branch
+//     after the MFMAs).
+//   * W4 pairs come out as (k, k+4) from the nibble layout, so the A fragment
+//     holds k in the order 0,4,1,5,2,6,3,7 of each 8; the X tile is written to LDS
+//     in the same order (v_perm) and the MFMA's sum over k is unchanged.
+//   * Buffer descriptors bound X, W and the scales by the tile's first row: rows
+//     past M or N read as zeros without touching memory.  Every global load in the
+//     loop is unconditional, so the compiler's in-order wait counts stay exact.
+#include <type_traits>
+
+#include "dequant.hpp"
+
+namespace anima {
+
+constexpr int PG_BM = 128;                  // output rows (M) per workgroup
+constexpr int PG_BN = 256;                  // output columns (N) per workgroup: 4 waves x 64
+constexpr int PG_BK = 64;                   // K per block: one quantisation group
+constexpr int PG_NT = 512;                  // two groups of 4 waves
+constexpr int PG_XROW = PG_BK + 8;          // padded X row in LDS (halfs)
+constexpr int PG_XSTAGE = PG_BM * PG_XROW * 2;   // bytes per X stage (one per group)
+constexpr int PG_RED = 16384;               // bytes per wave for the final K-split sum
+constexpr int PG_SMEM = 8 * PG_RED;         // reduction area, overlaying the two X stages
+constexpr int PG_WIN = 8;                   // K blocks per scale/zero window
+constexpr int PG_WINBUF = PG_BN * PG_WIN * 2 * 2;    // one window: scale and zero of 256 rows (8 KiB)
+constexpr int PG_WINOFF = 2 * PG_XSTAGE;    // windows: [group][buffer] after the X stages
+static_assert(PG_WINOFF + 4 * PG_WINBUF <= PG_SMEM, "X stages and windows fit in the reduction area");
+
+typedef __attribute__((address_space(3))) half8v lds_half8v;
+
+// ---------------------------------------------------------------------------
+// Dequantisation of one lane's packed weights into A fragments.
+// ---------------------------------------------------------------------------
+
+// ---------------------------------------------------------------------------
+// The kernel.
+// ---------------------------------------------------------------------------
+// SWIN: the scale/zero rows are 16-byte aligned runs of 8 groups (groups % 8 == 0),
+// read 8 groups at a time per row into an LDS window instead of one 2-byte load per
+// row and block.
+template <int STORAGE, bool SWIN>
+__global__ __launch_bounds__(PG_NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void pingpong_gemm_kernel(GemmParams p, int vec_store) {
+  constexpr bool W4 = STORAGE == ANIMA_STORAGE_W4;
+  constexpr int QBITS = W4 ? 4 : 8;
+  constexpr int WCH = W4 ? 1 : 2;           // 16-byte weight chunks per lane per row per block
+  constexpr int XCH = PG_BM * PG_BK / 8 / 256;   // X chunks per thread of a group (4)
+  // X fragments read ahead of their MFMAs (W8's two weight blocks in flight leave
+  // fewer registers).
+  constexpr int PG_READ_AHEAD = W4 ? 3 : 2;
+  __shared__ __attribute__((aligned(1024))) char smem[PG_SMEM];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int group = wave >> 2, wg = wave & 3;
+  const int c32 = lane & 31, hh = lane >> 5;
+  const int ntn = (p.N + PG_BN - 1) / PG_BN;
+  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int tn = lb % ntn, tm = lb / ntn;
+  const int m0 = tm * PG_BM, n0 = tn * PG_BN;
+  const int nk = p.K / PG_BK;
+  // Group 0 takes K blocks [0, half), group 1 [half, nk); with windows, half is a
+  // multiple of the window so every window is aligned.
+  int half = SWIN ? PG_WIN * ((nk + 2 * PG_WIN - 1) / (2 * PG_WIN)) : (nk + 1) / 2;
+  half = half < nk ? half : nk;
+  const int kb0 = group == 0 ? 0 : half;
+  const int nown = group == 0 ? half : nk - half;
+
+  // Tile-relative buffers (sizes fit in 31 bits; checked on the host).
+  const half_t* xb = p.x + (int64_t)m0 * p.K;
+  const int xbytes = (p.M - m0) * p.K * 2;
+  const uint8_t* wb = p.w + (int64_t)n0 * p.row_stride;
+  const int wbytes = (int)((int64_t)(p.N - n0) * p.row_stride);
+  const half_t* sb = p.scale + (int64_t)n0 * p.groups;
+  const half_t* zb = p.zero + (int64_t)n0 * p.groups;
+  const int sbytes = (p.N - n0) * p.groups * 2;
+
+  // X copies: thread t of a group moves chunks t + 256r (r < 4) of its group's
+  // block: row t/8 + 32r, 16-byte column t%8 (8 lanes read one 128-byte row).
+  const int tg = tid & 255;
+  const int xrow = tg >> 3, xch = tg & 7;
+  uint32_t goff_x[XCH];
+#pragma unroll
+  for (int r = 0; r < XCH; ++r) goff_x[r] = (uint32_t)(xrow + 32 * r) * (uint32_t)p.K * 2u + (uint32_t)xch * 16u;
+  char* const xstage = smem + group * PG_XSTAGE;
+  const int loff_x = (xrow * PG_XROW + xch * 8) * 2;
+
+  // Weights: lane (c32, hh) of wave wg holds rows 64wg + 32t + c32 (t = 0, 1),
+  // k = 32hh .. 32hh+31 of each block.
+  uint32_t goff_w[2], goff_s[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const uint32_t row = (uint32_t)(64 * wg + 32 * t + c32);
+    goff_w[t] = row * (uint32_t)p.row_stride + (uint32_t)hh * 16u * WCH;
+    goff_s[t] = row * (uint32_t)p.groups * 2u;
+  }
+
+  u32x4 xs[XCH];           // staged X chunks of the group's next block
+  u32x4 wr[2][2][WCH];     // packed weights, two blocks in flight: [buffer][row tile][chunk]
+  uint32_t sr[2], zr[2];   // scale / zero bits of the block after next (without windows)
+  u32x4 swin[2];           // staged scale / zero window chunk of row tg (with windows)
+  char* const winbase = smem + PG_WINOFF + group * 2 * PG_WINBUF;
+  half8v wf[2][4];         // dequantised A fragments (row tile, k step) of the current block
+  floatx16 acc[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc[t][m] = floatx16{};
+
+  auto load_x = [&](int kb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < XCH; ++r) xs[r] = load16_bounded(xb, xbytes, goff_x[r], kb * PG_BK * 2);
+  };
+  auto load_w = [&](int kb, auto buf_c) __attribute__((always_inline)) {
+    constexpr int B = decltype(buf_c)::value;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int c = 0; c < WCH; ++c) wr[B][t][c] = load16_bounded(wb, wbytes, goff_w[t] + 16u * c, kb * 32 * WCH);
+  };
+  // Scale / zero of one block, without windows: one 2-byte load per row.
+  auto load_sz = [&](int kb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      sr[t] = load2_bounded(sb, sbytes, goff_s[t], kb * 2);
+      zr[t] = load2_bounded(zb, sbytes, goff_s[t], kb * 2);
+    }
+  };
+  // Window of K blocks kw .. kw+7: thread tg of the group fetches row tg's 16-byte
+  // scale and zero runs; the window lands in LDS buffer (kw - kb0) / 8 % 2 as
+  // [scale | zero][row][8 groups].
+  const uint32_t goff_win = (uint32_t)tg * (uint32_t)p.groups * 2u;
+  // A window load with real == false reads nothing (an empty descriptor) and
+  // returns zeros.
+  auto load_win = [&](int kw, bool real) __attribute__((always_inline)) {
+    const int n = real ? sbytes : 0;
+    swin[0] = load16_bounded(sb, n, goff_win, kw * 2);
+    swin[1] = load16_bounded(zb, n, goff_win, kw * 2);
+  };
+  auto store_win = [&](int buf) __attribute__((always_inline)) {
+    *reinterpret_cast<u32x4*>(winbase + buf * PG_WINBUF + tg * 16) = swin[0];
+    *reinterpret_cast<u32x4*>(winbase + buf * PG_WINBUF + PG_WINBUF / 2 + tg * 16) = swin[1];
+  };
+
+  auto store_x = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < XCH; ++r) {
+      const u32x4 v = W4 ? interleave_w4_order(xs[r]) : xs[r];
+      *reinterpret_cast<u32x4*>(xstage + loff_x + r * 32 * PG_XROW * 2) = v;
+    }
+  };
+
+  uint32_t w4k[3] = {0x000F000Fu, 0x00F000F0u, 0x64006400u};
+#pragma unroll
+  for (int i = 0; i < 3; ++i) asm volatile("" : "+v"(w4k[i]));
+
+  // Scale and zero of the block the next M phase dequantises (local block j), and
+  // whether every lane of the wave may take the one-rounding dequantisation.
+  half_t sh[2], zh[2];
+  auto fetch_sz = [&](int j) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if constexpr (SWIN) {
+        const half_t* w = reinterpret_cast<const half_t*>(winbase + ((j / PG_WIN) & 1) * PG_WINBUF);
+        const int e = (64 * wg + 32 * t + c32) * PG_WIN + j % PG_WIN;
+        sh[t] = w[e];
+        zh[t] = w[PG_WINBUF / 4 + e];
+      } else {
+        sh[t] = __builtin_bit_cast(half_t, (uint16_t)sr[t]);
+        zh[t] = __builtin_bit_cast(half_t, (uint16_t)zr[t]);
+      }
+    }
+    return (bool)__all(one_rounding_exact<QBITS>(sh[0], zh[0]) & one_rounding_exact<QBITS>(sh[1], zh[1]));
+  };
+  // Step s of row tile t of the block in weight buffer B -> wf[t][s].
+  // Half (part 0: elements 0-3, part 1: elements 4-7) of step s of row tile t,
+  // one rounding.
+  auto dq_half = [&](auto buf_c, int t, int s, int part) __attribute__((always_inline)) {
+    constexpr int B = decltype(buf_c)::value;
+    const half2v s2 = {sh[t], sh[t]}, z2 = {zh[t], zh[t]};
+    half4v h;
+    if constexpr (W4) {
+      const uint32_t x = wr[B][t][0][s];
+      h = w4_half_one_rounding(part ? x >> 8 : x, s2, z2, w4k);
+    } else {
+      h = w8_half_one_rounding(wr[B][t][s >> 1][2 * (s & 1) + part], s2, z2);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wf[t][s][4 * part + e] = h[e];
+  };
+  auto dq_step = [&](auto fast_c, auto buf_c, int t, int s) __attribute__((always_inline)) {
+    constexpr bool F = decltype(fast_c)::value;
+    constexpr int B = decltype(buf_c)::value;
+    if constexpr (F) {
+      dq_half(buf_c, t, s, 0);
+      dq_half(buf_c, t, s, 1);
+    } else {
+      const float sf = (float)sh[t], zf = (float)zh[t];
+      if constexpr (W4)
+        wf[t][s] = w4_frag_exact(wr[B][t][0][s], sf, zf);
+      else
+        wf[t][s] = w8_frag_exact(wr[B][t][s >> 1][2 * (s & 1)], wr[B][t][s >> 1][2 * (s & 1) + 1], sf, zf);
+    }
+  };
+
+  // M phase: op i reads X fragment (k step i/4, row tile i%4) -- lane (c32, hh)
+  // reads row 32(i%4) + c32, k = 32hh + 8(i/4) .. +7 -- and issues the MFMAs of
+  // both weight row tiles with it.  Fragments come PG_READ_AHEAD ops ahead through
+  // a register ring; the sched_barriers pin that order.  The wave also dequantises
+  // the next block (weight buffer B) into the fragments the MFMAs have finished
+  // with, spread over the ops of the following steps (step 3 after the last op),
+  // so the vector work of the next block runs under this block's MFMAs.
+  const lds_half8v* xfrag = (const lds_half8v*)(xstage + (c32 * PG_XROW + 32 * hh) * 2);
+  // The M phase always runs the one-rounding dequantisation of the next block,
+  // branch-free (a branch costs about as much as a whole word's dequantisation, and
+  // two copies of the MFMA sequence would not keep one register assignment for
+  // the accumulators).  When a lane's scale/zero pair is not exact in one rounding
+  // the wave redoes the block with the fp32 FMA after the MFMAs (next_exact).
+  auto m_phase = [&](auto buf_c) __attribute__((always_inline)) {
+    constexpr int NOPS = 16, RING = PG_READ_AHEAD + 1;
+    half8v ring[RING];
+    auto read_op = [&](int i) __attribute__((always_inline)) -> half8v {
+      return xfrag[((i & 3) * 32 * PG_XROW + (i >> 2) * 8) / 8];
+    };
+#pragma unroll
+    for (int i = 0; i < PG_READ_AHEAD; ++i) ring[i] = read_op(i);
+#pragma unroll
+    for (int i = 0; i < NOPS; ++i) {
+      if (i + PG_READ_AHEAD < NOPS) ring[(i + PG_READ_AHEAD) % RING] = read_op(i + PG_READ_AHEAD);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[t][i & 3] = mfma32(wf[t][i >> 2], ring[i % RING], acc[t][i & 3]);
+      // Steps 0-2 of the next block, one (row tile, step) every second op from op 4
+      // on: step s is last read by op 4s+3.
+      // Steps 0-2 of the next block, half a (row tile, step) per op from op 4 on:
+      // step s is last read by op 4s+3.
+      if (i >= 4) dq_half(buf_c, ((i - 4) >> 1) & 1, (i - 4) >> 2, (i - 4) & 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    dq_step(std::true_type{}, buf_c, 0, 3);
+    dq_step(std::true_type{}, buf_c, 1, 3);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) asm volatile("" ::"v"(acc[t][m]));
+  };
+
+  // The barrier is written out (s_barrier after lgkmcnt(0)) so that the compiler
+  // does not turn it into a wait for the loads in flight.
+  auto barrier = [&]() __attribute__((always_inline)) {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  using YES = std::true_type;
+  using NO = std::false_type;
+
+  // Every global load below is issued unconditionally, so that each iteration
+  // issues the same loads in the same order and the compiler's in-order wait
+  // counts stay exact (a conditional load makes it wait for everything in
+  // flight).  Loads past a group's last block read other blocks or, past the
+  // buffers, zeros from the bounded descriptors; their results are never used.
+  // Prologue: stage block 0 (X, weights, first scale window), dequantise it, and
+  // start the loads of blocks 1 and 2.
+  if constexpr (SWIN)
+    load_win(kb0, true);
+  else
+    load_sz(kb0);
+  load_w(kb0, B0{});
+  load_w(kb0 + 1, B1{});
+  load_x(kb0);
+  if constexpr (SWIN) store_win(0);
+  store_x();
+  barrier();
+  {
+    const bool fast0 = fetch_sz(0);
+    if (fast0) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) { dq_step(YES{}, B0{}, 0, s); dq_step(YES{}, B0{}, 1, s); }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) { dq_step(NO{}, B0{}, 0, s); dq_step(NO{}, B0{}, 1, s); }
+    }
+  }
+  if constexpr (!SWIN) load_sz(kb0 + 1);
+  load_x(kb0 + 1);
+  load_w(kb0 + 2, B0{});
+  barrier();
+  if (group == 1) barrier();   // group 1 runs one phase behind
+  bool fast = fetch_sz(1);
+  if constexpr (!SWIN) load_sz(kb0 + 2);
+  // Local block j: the M phase multiplies block j and dequantises block j+1 (weight
+  // buffer (j+1)%2); the V phase writes the X tile of block j+1 to LDS, fetches
+  // the scale/zero of block j+2 and starts the loads of X(j+2) and of the weights
+  // of block j+3 (into the buffer the M phase just emptied).  Scale windows: the
+  // next window is loaded in the V phase of its predecessor's fifth block, written
+  // to LDS in that of the sixth and first read two V phases later (every phase
+  // ends in a barrier).  Unrolled by two so the weight buffers are static.
+  auto step = [&](int j, auto buf_c) __attribute__((always_inline)) {
+    using BN = decltype(buf_c);   // buffer of block j+1 (and of block j+3)
+    m_phase(BN{});
+    if (!fast && j + 1 < nown) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) { dq_step(NO{}, BN{}, 0, s); dq_step(NO{}, BN{}, 1, s); }
+    }
+    barrier();
+    const int jn = j + 1;
+    const bool next_win = SWIN && (jn / PG_WIN + 1) * PG_WIN < nown;
+    if (jn < nown) {
+      // The scale/zero reads go first: LDS operations of a wave complete in order,
+      // and behind the X tile writes they would wait for all of them.
+      if (j + 2 < nown) fast = fetch_sz(j + 2);
+      store_x();
+      if constexpr (SWIN) {
+        if (jn % PG_WIN == 5 && next_win) store_win((jn / PG_WIN + 1) & 1);
+      }
+    }
+    load_x(kb0 + j + 2);
+    if constexpr (SWIN)
+      load_win(kb0 + (jn / PG_WIN + 1) * PG_WIN, jn % PG_WIN == 4 && next_win);
+    else
+      load_sz(kb0 + j + 3);
+    load_w(kb0 + j + 3, BN{});
+    barrier();
+  };
+  int j = 0;
+  for (; j + 1 < nown; j += 2) {
+    step(j, B1{});
+    step(j + 1, B0{});
+  }
+  if (j < nown) step(j, B1{});
+  wait_vmcnt_imm<0>();   // loads past the end
+  // Same barrier count for both groups: group g passes 2 + g + 2*nown(g).
+  {
+    const int bars0 = 2 + 2 * half, bars1 = 3 + 2 * (nk - half);
+    const int mine = group == 0 ? bars0 : bars1;
+    const int target = bars0 > bars1 ? bars0 : bars1;
+    for (int i = mine; i < target; ++i) barrier();
+  }
+
+  // K-split sum: group 0 finishes row tiles 0-1, group 1 row tiles 2-3; each hands
+  // the other half to its partner wave (same SIMD, same columns) through LDS.
+  auto finish = [&](auto mine_c) __attribute__((always_inline)) {
+    constexpr int MINE = decltype(mine_c)::value, GIVE = 2 - MINE;
+    char* own = smem + (group * 4 + wg) * PG_RED;
+    const char* partner = smem + ((1 - group) * 4 + wg) * PG_RED;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const floatx4 v = {acc[t][GIVE + j][4 * q], acc[t][GIVE + j][4 * q + 1], acc[t][GIVE + j][4 * q + 2],
+                             acc[t][GIVE + j][4 * q + 3]};
+          *reinterpret_cast<floatx4*>(own + (((t * 2 + j) * 4 + q) * 64 + lane) * 16) = v;
+        }
+    barrier();
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int m = m0 + 32 * (MINE + j) + c32;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const floatx4 o = *reinterpret_cast<const floatx4*>(partner + (((t * 2 + j) * 4 + q) * 64 + lane) * 16);
+          const int n = n0 + 64 * wg + 32 * t + 8 * q + 4 * hh;
+          const half4v v = {(half_t)(acc[t][MINE + j][4 * q] + o[0]), (half_t)(acc[t][MINE + j][4 * q + 1] + o[1]),
+                            (half_t)(acc[t][MINE + j][4 * q + 2] + o[2]), (half_t)(acc[t][MINE + j][4 * q + 3] + o[3])};
+          if (m < p.M) {
+            half_t* yrow = p.y + (int64_t)m * p.N;
+            if (vec_store && n + 3 < p.N) {
+              *reinterpret_cast<half4v*>(yrow + n) = v;
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (n + e < p.N) yrow[n + e] = v[e];
+            }
+          }
+        }
+      }
+  };
+  if (group == 0)
+    finish(std::integral_constant<int, 0>{});
+  else
+    finish(std::integral_constant<int, 2>{});
+}
+
+bool pingpong_supported(const GemmParams& p, int storage) {
+  if (storage != ANIMA_STORAGE_W4 && storage != ANIMA_STORAGE_W8) return false;
+  if (p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K % PG_BK != 0 || p.groups != p.K / PG_BK) return false;
+  if (!aligned16(p.x) || !aligned16(p.w) || p.row_stride % 16 != 0) return false;
+  if ((reinterpret_cast<uintptr_t>(p.scale) & 1u) || (reinterpret_cast<uintptr_t>(p.zero) & 1u)) return false;
+  const int64_t lim = 0x7fffffff;
+  return (int64_t)p.M * p.K * 2 <= lim && (int64_t)p.N * p.row_stride <= lim && (int64_t)p.N * p.groups * 2 <= lim;
+}
+
+void launch_pingpong(const GemmParams& p, int storage, hipStream_t stream) {
+  if (!pingpong_supported(p, storage)) fail(ANIMA_E_INVALID_SHAPE, "ping-pong GEMM: unsupported shape or alignment");
+  const int64_t tiles = (int64_t)((p.M + PG_BM - 1) / PG_BM) * ((p.N + PG_BN - 1) / PG_BN);
+  if (tiles > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "GEMM grid too large");
+  const int vec = ((reinterpret_cast<uintptr_t>(p.y) & 7u) == 0 && p.N % 4 == 0) ? 1 : 0;
+  const bool swin = p.groups % PG_WIN == 0 && aligned16(p.scale) && aligned16(p.zero);
+  const dim3 grid((unsigned)tiles), block(PG_NT);
+  if (storage == ANIMA_STORAGE_W4) {
+    if (swin)
+      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W4, true>), grid, block, 0, stream, p, vec);
+    else
+      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W4, false>), grid, block, 0, stream, p, vec);
+  } else {
+    if (swin)
+      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W8, true>), grid, block, 0, stream, p, vec);
+    else
+      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W8, false>), grid, block, 0, stream, p, vec);
+  }
+  ANIMA_HIP(hipGetLastError());
+}
+
+}  // namespace anima

@@ -55,24 +55,6 @@ __device__ __forceinline__ half_t dq1(uint32_t q, half_t s, half_t z) {
     return f32_to_f16(fmaf((float)q, (float)s, (float)z));
 }
 
-// Exponent of the unit in the last place of an fp16 value, as a biased field (1..31).
-__device__ __forceinline__ int fp16_unit_exponent(half_t v) {
-  const int e = (__builtin_bit_cast(uint16_t, v) >> 10) & 31;
-  return e < 1 ? 1 : e;
-}
-
-// True when q*s + z is exactly representable in fp32 for every code q < 2^QBITS.
-// q*s is an integer of at most QBITS+11 bits times s's unit, z one of at most 11
-// bits times its own unit; their sum spans at most 24 bits exactly when the unit
-// exponents differ by d = u(s) - u(z) with -12 <= d <= 12 - QBITS (or when s or z
-// is zero).
-template <int QBITS>
-__device__ __forceinline__ bool one_rounding_exact(half_t s, half_t z) {
-  if ((__builtin_bit_cast(uint16_t, s) & 0x7fff) == 0 || (__builtin_bit_cast(uint16_t, z) & 0x7fff) == 0) return true;
-  const int d = fp16_unit_exponent(s) - fp16_unit_exponent(z);
-  return d >= -12 && d <= 12 - QBITS;
-}
-
 // A fragment t (k = 32g + 8t .. +7 of the chunk) from a lane's raw weight words.
 template <int STORAGE, bool ONE_ROUNDING>
 __device__ __forceinline__ half8v dequant_frag(const uint32_t (&wv)[SmallMChunk<STORAGE>::WORDS], int t, half_t s,

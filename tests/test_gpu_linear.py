@@ -116,6 +116,38 @@ def test_w4_gemm_block_shapes(ctx, backend, M, N, K):
     _check_gemm(y, _gemm_ref(d["x"], d["w"]), f"W4 {backend} M{M} N{N} K{K}")
 
 
+@pytest.mark.parametrize("storage", [0, 1])
+@pytest.mark.parametrize("M,N,K", [(65, 256, 64), (130, 520, 320), (257, 1000, 448), (1000, 2056, 1024),
+                                   (200, 300, 512), (129, 768, 1536), (383, 520, 4608)])
+def test_tiled_gemm_ragged_shapes_and_both_dequant_roundings(ctx, storage, M, N, K):
+    """The tiled GEMM for M > 64 with K a multiple of 64: partial row and column tiles, a
+    single K block, odd block counts (the workgroup's two K halves get unequal shares), and
+    per-group scale/zero pairs chosen per 64-row block so that whole waves take the
+    one-rounding packed dequant (symmetric or zero offset) or the fp32 fallback (offset 2^-14
+    of the scale: q*s + z no longer exact in fp32)."""
+    rng = np.random.default_rng(1000 * storage + M + N + K)
+    groups = K // 64
+    scale = (rng.random((N, groups)) * 0.015 + 0.005).astype(np.float16)
+    kind = np.repeat(rng.integers(0, 3, ((N + 63) // 64, groups)), 64, axis=0)[:N]
+    sign = np.where(rng.random((N, groups)) < 0.5, -1.0, 1.0)
+    qmid = 8.0 if storage == 0 else 128.0
+    zero = np.where(kind == 0, -qmid * scale.astype(np.float64),
+                    np.where(kind == 1, scale.astype(np.float64) * 2.0 ** -14 * sign, 0.0)).astype(np.float16)
+    if storage == 0:
+        packed = quant.pack_w4(rng.integers(0, 16, (N, K)).astype(np.uint8))
+        stride = K // 2
+    else:
+        packed = rng.integers(0, 256, (N, K)).astype(np.uint8)
+        stride = K
+    w = _wdict(storage, packed, scale.view(np.uint16), zero.view(np.uint16), N, K, stride)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16))
+    qw, keep = device_weight(w)
+    y = torch.full((M, N), float("nan"), dtype=torch.float16, device="cuda")
+    LinearExecutor(ctx).execute(dev(x), qw, y, M)
+    torch.cuda.synchronize()
+    _check_gemm(y, _gemm_ref(x, w), f"tiled s{storage} M{M} N{N} K{K}")
+
+
 def test_w8_padded_stride_tail_tile_and_guards(ctx):
     """LinearExecutorTests.swift:33-103: W8, M=133 N=16 K=16, packed stride 20, byte offsets 32,
     guard bytes on both sides of the output untouched."""
