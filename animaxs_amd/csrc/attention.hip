@@ -414,42 +414,52 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(PrologueParams p) {
   }
 }
 
-// head_dim 128 fast path: 8 lanes per row, lane l holds the pairs (8l+i, 64+8l+i),
-// i < 8, as two 16-byte loads; the RoPE blocks of those pairs are eight float4
-// loads; the sum of squares needs three lane exchanges.  Same arithmetic as the
-// generic kernel (and as the fused Q path of the flash kernels).
+// head_dim 128 fast path: a group of 8 lanes takes HPT heads of one token; lane
+// sub holds the pairs (8sub+i, 64+8sub+i), i < 8, of each head as two 16-byte
+// loads, so the token's RoPE blocks (eight float4 loads per lane) and the norm
+// weights are read once per HPT heads.  The per-head sum of squares needs three
+// lane exchanges.  Same arithmetic as the generic kernel (and as the fused Q path
+// of the flash kernels).
+template <int HPT>
 __global__ __launch_bounds__(256) void qk_prologue_d128_kernel(PrologueParams p) {
   const int sub = threadIdx.x & 7;
-  const int64_t row = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
-  const int64_t total = (int64_t)p.batch * p.rows * p.heads;
-  const bool live = row < total;
-  const int64_t rr = live ? row : total - 1;   // tail lanes recompute the last row, never store
-  const int h = (int)(rr % p.heads);
-  const int64_t t = (rr / p.heads) % p.rows;
-  const int b = (int)(rr / ((int64_t)p.heads * p.rows));
-  const half_t* x = p.in + (int64_t)b * p.in_batch + t * p.in_tok + (int64_t)h * p.in_head;
-  half_t* y = p.out + (((int64_t)b * p.heads + h) * p.rows + t) * 128;
-  const half8v xa = *reinterpret_cast<const half8v*>(x + 8 * sub);
-  const half8v xc = *reinterpret_cast<const half8v*>(x + 64 + 8 * sub);
-  float a[8], c[8];
-  float ss = 0.f;
+  const int groups = p.heads / HPT;
+  const int64_t unit = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int64_t total = (int64_t)p.batch * p.rows * groups;
+  const bool live = unit < total;
+  const int64_t uu = live ? unit : total - 1;   // tail lanes recompute the last unit, never store
+  const int hg = (int)(uu % groups);
+  const int64_t t = (uu / groups) % p.rows;
+  const int b = (int)(uu / ((int64_t)groups * p.rows));
+  float a[HPT][8], c[HPT][8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    a[i] = (float)xa[i];
-    c[i] = (float)xc[i];
-    ss = fmaf(a[i], a[i], fmaf(c[i], c[i], ss));
+  for (int j = 0; j < HPT; ++j) {
+    const half_t* x = p.in + (int64_t)b * p.in_batch + t * p.in_tok + (int64_t)(hg * HPT + j) * p.in_head;
+    const half8v xa = *reinterpret_cast<const half8v*>(x + 8 * sub);
+    const half8v xc = *reinterpret_cast<const half8v*>(x + 64 + 8 * sub);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a[j][i] = (float)xa[i];
+      c[j][i] = (float)xc[i];
+    }
   }
   if (p.norm_w) {
-    ss += __shfl_xor(ss, 1, 8);
-    ss += __shfl_xor(ss, 2, 8);
-    ss += __shfl_xor(ss, 4, 8);
-    const float inv = rsqrtf(ss / 128.f + p.eps);
     const half8v wa = *reinterpret_cast<const half8v*>(p.norm_w + 8 * sub);
     const half8v wc = *reinterpret_cast<const half8v*>(p.norm_w + 64 + 8 * sub);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      a[i] = a[i] * inv * (float)wa[i];
-      c[i] = c[i] * inv * (float)wc[i];
+    for (int j = 0; j < HPT; ++j) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = fmaf(a[j][i], a[j][i], fmaf(c[j][i], c[j][i], ss));
+      ss += __shfl_xor(ss, 1, 8);
+      ss += __shfl_xor(ss, 2, 8);
+      ss += __shfl_xor(ss, 4, 8);
+      const float inv = rsqrtf(ss / 128.f + p.eps);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        a[j][i] = a[j][i] * inv * (float)wa[i];
+        c[j][i] = c[j][i] * inv * (float)wc[i];
+      }
     }
   }
   if (p.rope) {
@@ -457,21 +467,28 @@ __global__ __launch_bounds__(256) void qk_prologue_d128_kernel(PrologueParams p)
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const floatx4 r = blk[i];
-      const float ra = r[0] * a[i] + r[1] * c[i];
-      const float rc = r[2] * a[i] + r[0] * c[i];
-      a[i] = ra;
-      c[i] = rc;
+#pragma unroll
+      for (int j = 0; j < HPT; ++j) {
+        const float ra = r[0] * a[j][i] + r[1] * c[j][i];
+        const float rc = r[2] * a[j][i] + r[0] * c[j][i];
+        a[j][i] = ra;
+        c[j][i] = rc;
+      }
     }
   }
-  half8v oa, oc;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    oa[i] = f32_to_f16(a[i]);
-    oc[i] = f32_to_f16(c[i]);
-  }
   if (live) {
-    *reinterpret_cast<half8v*>(y + 8 * sub) = oa;
-    *reinterpret_cast<half8v*>(y + 64 + 8 * sub) = oc;
+#pragma unroll
+    for (int j = 0; j < HPT; ++j) {
+      half8v oa, oc;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        oa[i] = f32_to_f16(a[j][i]);
+        oc[i] = f32_to_f16(c[j][i]);
+      }
+      half_t* y = p.out + (((int64_t)b * p.heads + hg * HPT + j) * p.rows + t) * 128;
+      *reinterpret_cast<half8v*>(y + 8 * sub) = oa;
+      *reinterpret_cast<half8v*>(y + 64 + 8 * sub) = oc;
+    }
   }
 }
 
@@ -521,9 +538,15 @@ void launch_prologue(const PrologueParams& p, hipStream_t stream) {
                     p.in_batch % 8 == 0 && aligned16(p.out) && (!p.norm_w || aligned16(p.norm_w)) &&
                     (!p.rope || aligned16(p.rope));
   if (fast) {
-    const int64_t blocks = (rows + 31) / 32;
+    const int hpt = p.heads % 4 == 0 ? 4 : (p.heads % 2 == 0 ? 2 : 1);
+    const int64_t blocks = (rows / hpt + 31) / 32;
     if (blocks > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "prologue grid too large");
-    hipLaunchKernelGGL(qk_prologue_d128_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+    if (hpt == 4)
+      hipLaunchKernelGGL(qk_prologue_d128_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+    else if (hpt == 2)
+      hipLaunchKernelGGL(qk_prologue_d128_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL(qk_prologue_d128_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream, p);
     ANIMA_HIP(hipGetLastError());
     return;
   }
