@@ -127,6 +127,35 @@ anima_status anima_linear_encode(anima_linear* lin, anima_buffer input, int64_t 
   });
 }
 
+static void check_elementwise(const anima_buffer& b, int64_t count, int64_t elem, const char* what) {
+  if (count < 0) fail(ANIMA_E_INVALID_SHAPE, std::string(what) + " count must be >= 0");
+  if (checked_product({count, elem}, what) > b.length) fail(ANIMA_E_OUT_OF_BOUNDS, std::string(what) + " buffer range is out of bounds");
+  if (count > 0 && !b.ptr) fail(ANIMA_E_INVALID_ARGUMENT, std::string(what) + " buffer pointer is null");
+}
+
+anima_status anima_linear_encode_epilogue(anima_linear* lin, anima_buffer input, int64_t input_offset,
+                                          const anima_qweight* weight, anima_buffer output, int64_t output_offset,
+                                          int64_t input_rows, int32_t family, int32_t epilogue, anima_buffer residual,
+                                          anima_buffer gate) {
+  return guarded([&] {
+    require(lin, "linear");
+    const anima_qweight& w = *require(weight, "weight");
+    if (epilogue != ANIMA_LINEAR_EPILOGUE_GELU && epilogue != ANIMA_LINEAR_EPILOGUE_GATE_ADD)
+      fail(ANIMA_E_INVALID_ARGUMENT, "unknown linear epilogue");
+    float* res = nullptr;
+    const float* gt = nullptr;
+    if (epilogue == ANIMA_LINEAR_EPILOGUE_GATE_ADD) {
+      if (!(input_rows > 0 && w.rows > 0)) fail(ANIMA_E_INVALID_SHAPE, "invalid LinearExecutor shape or offset");
+      check_elementwise(residual, checked_product({input_rows, w.rows}, "linear epilogue"), 4, "linear residual");
+      check_elementwise(gate, w.rows, 4, "linear gate");
+      res = static_cast<float*>(residual.ptr);
+      gt = static_cast<const float*>(gate.ptr);
+    }
+    encode_linear_epilogue(lin->impl, input, input_offset, w, output, output_offset, input_rows, family,
+                           epilogue == ANIMA_LINEAR_EPILOGUE_GELU ? GEMM_GELU : GEMM_GATE_ADD, res, gt);
+  });
+}
+
 anima_status anima_linear_execute(anima_linear* lin, anima_buffer input, int64_t input_offset,
                                   const anima_qweight* weight, anima_buffer output, int64_t output_offset,
                                   int64_t input_rows, int32_t family) {
@@ -154,11 +183,6 @@ anima_status anima_dequant_to_half_encode(anima_ctx* ctx, const anima_qweight* w
 }
 
 // ---------------------------------------------------------------- DiT block support kernels
-static void check_elementwise(const anima_buffer& b, int64_t count, int64_t elem, const char* what) {
-  if (count < 0) fail(ANIMA_E_INVALID_SHAPE, std::string(what) + " count must be >= 0");
-  if (checked_product({count, elem}, what) > b.length) fail(ANIMA_E_OUT_OF_BOUNDS, std::string(what) + " buffer range is out of bounds");
-  if (count > 0 && !b.ptr) fail(ANIMA_E_INVALID_ARGUMENT, std::string(what) + " buffer pointer is null");
-}
 
 anima_status anima_layernorm_modulate_to_half_encode(anima_ctx* ctx, anima_buffer residual, anima_buffer modulation,
                                                      anima_buffer output, int64_t n, int64_t rows, float eps,

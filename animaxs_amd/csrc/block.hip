@@ -17,15 +17,25 @@
 namespace anima {
 
 // ---------------------------------------------------------------------------
-// LayerNorm (mean-centred, no affine) * (1 + scale) + shift -> fp16.  One
-// 256-thread workgroup per row; the row stays in registers between the mean,
-// variance and output passes (the reference re-reads memory three times).
+// Row normalisations.  Wave form: one wave per row, four rows per 256-thread
+// workgroup; lane l holds columns 4*(l + 64*e) .. +3 for e < V as float4s, so the
+// row stays in registers between the mean, variance and output passes (the
+// reference re-reads memory three times) and the sums are wave butterflies with
+// no barriers.  Rows longer than 256*V (V <= 16), not a multiple of 4 columns or
+// not 16-byte aligned take the workgroup-per-row kernels (one element per thread
+// and step, n <= 8192).
 // ---------------------------------------------------------------------------
 constexpr int LN_NT = 256;
 constexpr int LN_MAX_PER_THREAD = 32;  // n <= 8192
 
-__device__ __forceinline__ float block_sum(float v, float* red) {
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) red[wave] = v;
@@ -34,6 +44,57 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 #pragma unroll
   for (int w = 0; w < LN_NT / 64; ++w) t += red[w];
   return t;
+}
+
+// dit_layernorm_modulate_to_half (AnimaKernels.metal:477-524):
+// half(((x - mean) * rsqrt(var + eps)) * (1 + scale) + shift), var the mean of the
+// squared deviations.
+template <int V>
+__global__ __launch_bounds__(256) void layernorm_modulate_wave_kernel(const float* __restrict__ residual,
+                                                                      const float* __restrict__ mod,
+                                                                      half_t* __restrict__ out, int n, int rows,
+                                                                      float eps, int64_t mod_offset) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* x = residual + (int64_t)row * n;
+  floatx4 v[V];
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    const int c = 4 * (lane + 64 * e);
+    v[e] = c < n ? *reinterpret_cast<const floatx4*>(x + c) : floatx4{0.f, 0.f, 0.f, 0.f};
+    s += (v[e][0] + v[e][1]) + (v[e][2] + v[e][3]);
+  }
+  const float mean = wave_sum(s) / (float)n;
+  float sq = 0.f;
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    const int c = 4 * (lane + 64 * e);
+    if (c < n) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float d = v[e][u] - mean;
+        sq = fmaf(d, d, sq);
+      }
+    }
+  }
+  const float inv = rsqrtf(wave_sum(sq) / (float)n + eps);
+  const float* scale = mod + mod_offset;
+  const float* shift = mod;
+  half_t* o = out + (int64_t)row * n;
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    const int c = 4 * (lane + 64 * e);
+    if (c < n) {
+      const floatx4 sc = *reinterpret_cast<const floatx4*>(scale + c);
+      const floatx4 sh = *reinterpret_cast<const floatx4*>(shift + c);
+      half4v h;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) h[u] = f32_to_f16((v[e][u] - mean) * inv * (1.0f + sc[u]) + sh[u]);
+      *reinterpret_cast<half4v*>(o + c) = h;
+    }
+  }
 }
 
 __global__ __launch_bounds__(LN_NT) void layernorm_modulate_kernel(const float* __restrict__ residual,
@@ -67,43 +128,45 @@ __global__ __launch_bounds__(LN_NT) void layernorm_modulate_kernel(const float* 
 #pragma unroll
   for (int e = 0; e < LN_MAX_PER_THREAD; ++e) {
     const int i = threadIdx.x + e * LN_NT;
-    if (i < n) {
-      const float normalized = (v[e] - mean) * inv;
-      o[i] = f32_to_f16(normalized * (1.0f + scale[i]) + shift[i]);
-    }
+    if (i < n) o[i] = f32_to_f16((v[e] - mean) * inv * (1.0f + scale[i]) + shift[i]);
   }
-}
-
-__global__ __launch_bounds__(256) void gate_add_kernel(float* __restrict__ residual, const half_t* __restrict__ branch,
-                                                       const float* __restrict__ gate, int64_t n, int64_t count) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < count) residual[i] += (float)branch[i] * gate[i % n];
-}
-
-__global__ __launch_bounds__(256) void gelu_kernel(half_t* __restrict__ values, int64_t count) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < count) {
-    const float x = (float)values[i];
-    values[i] = f32_to_f16(0.5f * x * (1.0f + erff(x * 0.7071067811865475f)));
-  }
-}
-
-__global__ __launch_bounds__(256) void silu_kernel(const float* __restrict__ in, float* __restrict__ out, int64_t count) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < count) {
-    const float x = in[i];
-    out[i] = x / (1.0f + expf(-x));
-  }
-}
-
-__global__ __launch_bounds__(256) void add_kernel(float* __restrict__ dst, const float* __restrict__ src, int64_t count) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < count) dst[i] += src[i];
 }
 
 // RMSNorm of an fp32 row with an fp16 weight, stored as fp16: rmsnorm_f32_to_f32
 // (AnimaKernels.metal:172-204) followed by float_to_half (:81-88) in one pass.
 // out = half(x * rsqrt(mean(x^2) + eps) * w), the product in the reference's order.
+template <int V>
+__global__ __launch_bounds__(256) void rmsnorm_half_wave_kernel(const float* __restrict__ in,
+                                                                const half_t* __restrict__ w,
+                                                                half_t* __restrict__ out, int n, int rows, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* x = in + (int64_t)row * n;
+  floatx4 v[V];
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    const int c = 4 * (lane + 64 * e);
+    v[e] = c < n ? *reinterpret_cast<const floatx4*>(x + c) : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ss = fmaf(v[e][u], v[e][u], ss);
+  }
+  const float inv = rsqrtf(wave_sum(ss) / (float)n + eps);
+  half_t* o = out + (int64_t)row * n;
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    const int c = 4 * (lane + 64 * e);
+    if (c < n) {
+      const half4v wv = *reinterpret_cast<const half4v*>(w + c);
+      half4v h;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) h[u] = f32_to_f16(v[e][u] * inv * (float)wv[u]);
+      *reinterpret_cast<half4v*>(o + c) = h;
+    }
+  }
+}
+
 __global__ __launch_bounds__(LN_NT) void rmsnorm_half_kernel(const float* __restrict__ in, const half_t* __restrict__ w,
                                                              half_t* __restrict__ out, int n, float eps) {
   __shared__ float red[LN_NT / 64];
@@ -126,67 +189,230 @@ __global__ __launch_bounds__(LN_NT) void rmsnorm_half_kernel(const float* __rest
   }
 }
 
+// ---------------------------------------------------------------------------
+// Elementwise kernels.  Each thread takes a chunk of EW consecutive elements:
+// 16-byte accesses (one per 8 fp16, two per 8 fp32) when the launcher found every
+// pointer 16-byte aligned (vec != 0) and the chunk is whole, element-wise
+// accesses for the last partial chunk and for unaligned buffers.
+// ---------------------------------------------------------------------------
+constexpr int EW = 8;
+
+__device__ __forceinline__ void load8(const float* p, float (&v)[EW]) {
+  const floatx4 a = *reinterpret_cast<const floatx4*>(p), b = *reinterpret_cast<const floatx4*>(p + 4);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    v[u] = a[u];
+    v[u + 4] = b[u];
+  }
+}
+__device__ __forceinline__ void store8(float* p, const float (&v)[EW]) {
+  *reinterpret_cast<floatx4*>(p) = floatx4{v[0], v[1], v[2], v[3]};
+  *reinterpret_cast<floatx4*>(p + 4) = floatx4{v[4], v[5], v[6], v[7]};
+}
+
+// gate_add_half_f32 (AnimaKernels.metal:624-634): residual += float(branch) * gate[i % n].
+// The vector form needs n % 8 == 0 so that a chunk never wraps a row.
+__global__ __launch_bounds__(256) void gate_add_kernel(float* __restrict__ residual, const half_t* __restrict__ branch,
+                                                       const float* __restrict__ gate, int64_t n, int64_t count,
+                                                       int vec) {
+  const int64_t c0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * EW;
+  if (c0 >= count) return;
+  if (vec && c0 + EW <= count) {
+    const int64_t col = c0 % n;
+    float r[EW], g[EW];
+    load8(residual + c0, r);
+    load8(gate + col, g);
+    const half8v b = *reinterpret_cast<const half8v*>(branch + c0);
+#pragma unroll
+    for (int u = 0; u < EW; ++u) r[u] = fmaf((float)b[u], g[u], r[u]);
+    store8(residual + c0, r);
+  } else {
+    const int64_t end = c0 + EW < count ? c0 + EW : count;
+    for (int64_t i = c0; i < end; ++i) residual[i] = fmaf((float)branch[i], gate[i % n], residual[i]);
+  }
+}
+
+// dit_gelu_half_inplace (AnimaKernels.metal:312-322).
+__global__ __launch_bounds__(256) void gelu_kernel(half_t* __restrict__ values, int64_t count, int vec) {
+  const int64_t c0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * EW;
+  if (c0 >= count) return;
+  if (vec && c0 + EW <= count) {
+    half8v v = *reinterpret_cast<const half8v*>(values + c0);
+#pragma unroll
+    for (int u = 0; u < EW; ++u) v[u] = gelu_erf_half(v[u]);
+    *reinterpret_cast<half8v*>(values + c0) = v;
+  } else {
+    const int64_t end = c0 + EW < count ? c0 + EW : count;
+    for (int64_t i = c0; i < end; ++i) values[i] = gelu_erf_half(values[i]);
+  }
+}
+
+// silu (AnimaKernels.metal:388-397).
+__global__ __launch_bounds__(256) void silu_kernel(const float* __restrict__ in, float* __restrict__ out, int64_t count,
+                                                   int vec) {
+  const int64_t c0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * EW;
+  if (c0 >= count) return;
+  if (vec && c0 + EW <= count) {
+    float v[EW];
+    load8(in + c0, v);
+#pragma unroll
+    for (int u = 0; u < EW; ++u) v[u] = silu_f32(v[u]);
+    store8(out + c0, v);
+  } else {
+    const int64_t end = c0 + EW < count ? c0 + EW : count;
+    for (int64_t i = c0; i < end; ++i) out[i] = silu_f32(in[i]);
+  }
+}
+
+// add_f32 (AnimaKernels.metal:649-656).
+__global__ __launch_bounds__(256) void add_kernel(float* __restrict__ dst, const float* __restrict__ src, int64_t count,
+                                                  int vec) {
+  const int64_t c0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * EW;
+  if (c0 >= count) return;
+  if (vec && c0 + EW <= count) {
+    float d[EW], s[EW];
+    load8(dst + c0, d);
+    load8(src + c0, s);
+#pragma unroll
+    for (int u = 0; u < EW; ++u) d[u] += s[u];
+    store8(dst + c0, d);
+  } else {
+    const int64_t end = c0 + EW < count ? c0 + EW : count;
+    for (int64_t i = c0; i < end; ++i) dst[i] += src[i];
+  }
+}
+
 // gated_silu_half (AnimaKernels.metal:401-411): SiLU and product in fp32, one rounding.
 __global__ __launch_bounds__(256) void gated_silu_kernel(const half_t* __restrict__ gate, const half_t* __restrict__ up,
-                                                         half_t* __restrict__ out, int64_t count) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < count) {
-    const float x = (float)gate[i];
-    out[i] = f32_to_f16((x / (1.0f + expf(-x))) * (float)up[i]);
+                                                         half_t* __restrict__ out, int64_t count, int vec) {
+  const int64_t c0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * EW;
+  if (c0 >= count) return;
+  if (vec && c0 + EW <= count) {
+    const half8v g = *reinterpret_cast<const half8v*>(gate + c0);
+    const half8v u = *reinterpret_cast<const half8v*>(up + c0);
+    half8v o;
+#pragma unroll
+    for (int e = 0; e < EW; ++e) o[e] = f32_to_f16(silu_f32((float)g[e]) * (float)u[e]);
+    *reinterpret_cast<half8v*>(out + c0) = o;
+  } else {
+    const int64_t end = c0 + EW < count ? c0 + EW : count;
+    for (int64_t i = c0; i < end; ++i) out[i] = f32_to_f16(silu_f32((float)gate[i]) * (float)up[i]);
   }
 }
 
 // add_half_into_float (AnimaKernels.metal:639-647).
 __global__ __launch_bounds__(256) void add_half_kernel(float* __restrict__ residual, const half_t* __restrict__ branch,
-                                                       int64_t count) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < count) residual[i] += (float)branch[i];
+                                                       int64_t count, int vec) {
+  const int64_t c0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * EW;
+  if (c0 >= count) return;
+  if (vec && c0 + EW <= count) {
+    float r[EW];
+    load8(residual + c0, r);
+    const half8v b = *reinterpret_cast<const half8v*>(branch + c0);
+#pragma unroll
+    for (int u = 0; u < EW; ++u) r[u] += (float)b[u];
+    store8(residual + c0, r);
+  } else {
+    const int64_t end = c0 + EW < count ? c0 + EW : count;
+    for (int64_t i = c0; i < end; ++i) residual[i] += (float)branch[i];
+  }
 }
 
-static dim3 grid1d(int64_t count) {
-  const int64_t b = (count + 255) / 256;
+static dim3 grid_ew(int64_t count) {
+  const int64_t b = (count + 256 * EW - 1) / (256 * EW);
   if (b > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "elementwise grid too large");
   return dim3((unsigned)b);
+}
+
+// Smallest wave-kernel register depth V (float4s per lane) for a row of n, or 0.
+static int wave_depth(int64_t n) {
+  if (n % 4 != 0) return 0;
+  for (int v = 2; v <= 16; v *= 2)
+    if (n <= 256 * v) return v;
+  return 0;
 }
 
 void launch_layernorm_modulate(const float* residual, const float* mod, half_t* out, int64_t n, int64_t rows, float eps,
                                int64_t mod_offset, hipStream_t stream) {
   if (n > LN_NT * LN_MAX_PER_THREAD) fail(ANIMA_E_UNSUPPORTED, "layernorm-modulate supports rows of at most 8192");
   if (rows > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "layernorm-modulate rows exceed int32");
-  hipLaunchKernelGGL(layernorm_modulate_kernel, dim3((unsigned)rows), dim3(LN_NT), 0, stream, residual, mod, out, (int)n,
-                     eps, mod_offset);
+  if (rows <= 0 || n <= 0) return;
+  const int depth = wave_depth(n);
+  if (depth && aligned16(residual) && aligned16(mod) && mod_offset % 4 == 0 && aligned8(out)) {
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    switch (depth) {
+      case 2: hipLaunchKernelGGL(layernorm_modulate_wave_kernel<2>, grid, dim3(256), 0, stream, residual, mod, out,
+                                 (int)n, (int)rows, eps, mod_offset); break;
+      case 4: hipLaunchKernelGGL(layernorm_modulate_wave_kernel<4>, grid, dim3(256), 0, stream, residual, mod, out,
+                                 (int)n, (int)rows, eps, mod_offset); break;
+      case 8: hipLaunchKernelGGL(layernorm_modulate_wave_kernel<8>, grid, dim3(256), 0, stream, residual, mod, out,
+                                 (int)n, (int)rows, eps, mod_offset); break;
+      default: hipLaunchKernelGGL(layernorm_modulate_wave_kernel<16>, grid, dim3(256), 0, stream, residual, mod, out,
+                                  (int)n, (int)rows, eps, mod_offset); break;
+    }
+  } else {
+    hipLaunchKernelGGL(layernorm_modulate_kernel, dim3((unsigned)rows), dim3(LN_NT), 0, stream, residual, mod, out,
+                       (int)n, eps, mod_offset);
+  }
   ANIMA_HIP(hipGetLastError());
 }
 void launch_gate_add(float* residual, const half_t* branch, const float* gate, int64_t n, int64_t count,
                      hipStream_t stream) {
-  hipLaunchKernelGGL(gate_add_kernel, grid1d(count), dim3(256), 0, stream, residual, branch, gate, n, count);
+  if (count <= 0) return;
+  const int vec = aligned16(residual) && aligned16(branch) && aligned16(gate) && n % EW == 0;
+  hipLaunchKernelGGL(gate_add_kernel, grid_ew(count), dim3(256), 0, stream, residual, branch, gate, n, count, vec);
   ANIMA_HIP(hipGetLastError());
 }
 void launch_gelu(half_t* values, int64_t count, hipStream_t stream) {
-  hipLaunchKernelGGL(gelu_kernel, grid1d(count), dim3(256), 0, stream, values, count);
+  if (count <= 0) return;
+  hipLaunchKernelGGL(gelu_kernel, grid_ew(count), dim3(256), 0, stream, values, count, aligned16(values) ? 1 : 0);
   ANIMA_HIP(hipGetLastError());
 }
 void launch_silu(const float* in, float* out, int64_t count, hipStream_t stream) {
-  hipLaunchKernelGGL(silu_kernel, grid1d(count), dim3(256), 0, stream, in, out, count);
+  if (count <= 0) return;
+  const int vec = aligned16(in) && aligned16(out);
+  hipLaunchKernelGGL(silu_kernel, grid_ew(count), dim3(256), 0, stream, in, out, count, vec);
   ANIMA_HIP(hipGetLastError());
 }
 void launch_add(float* dst, const float* src, int64_t count, hipStream_t stream) {
-  hipLaunchKernelGGL(add_kernel, grid1d(count), dim3(256), 0, stream, dst, src, count);
+  if (count <= 0) return;
+  const int vec = aligned16(dst) && aligned16(src);
+  hipLaunchKernelGGL(add_kernel, grid_ew(count), dim3(256), 0, stream, dst, src, count, vec);
   ANIMA_HIP(hipGetLastError());
 }
 void launch_rmsnorm_half(const float* in, const half_t* w, half_t* out, int64_t n, int64_t rows, float eps,
                          hipStream_t stream) {
   if (n > LN_NT * LN_MAX_PER_THREAD) fail(ANIMA_E_UNSUPPORTED, "rmsnorm supports rows of at most 8192");
   if (rows > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "rmsnorm rows exceed int32");
-  hipLaunchKernelGGL(rmsnorm_half_kernel, dim3((unsigned)rows), dim3(LN_NT), 0, stream, in, w, out, (int)n, eps);
+  if (rows <= 0 || n <= 0) return;
+  const int depth = wave_depth(n);
+  if (depth && aligned16(in) && aligned8(w) && aligned8(out)) {
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    switch (depth) {
+      case 2: hipLaunchKernelGGL(rmsnorm_half_wave_kernel<2>, grid, dim3(256), 0, stream, in, w, out, (int)n,
+                                 (int)rows, eps); break;
+      case 4: hipLaunchKernelGGL(rmsnorm_half_wave_kernel<4>, grid, dim3(256), 0, stream, in, w, out, (int)n,
+                                 (int)rows, eps); break;
+      case 8: hipLaunchKernelGGL(rmsnorm_half_wave_kernel<8>, grid, dim3(256), 0, stream, in, w, out, (int)n,
+                                 (int)rows, eps); break;
+      default: hipLaunchKernelGGL(rmsnorm_half_wave_kernel<16>, grid, dim3(256), 0, stream, in, w, out, (int)n,
+                                  (int)rows, eps); break;
+    }
+  } else {
+    hipLaunchKernelGGL(rmsnorm_half_kernel, dim3((unsigned)rows), dim3(LN_NT), 0, stream, in, w, out, (int)n, eps);
+  }
   ANIMA_HIP(hipGetLastError());
 }
 void launch_gated_silu(const half_t* gate, const half_t* up, half_t* out, int64_t count, hipStream_t stream) {
-  hipLaunchKernelGGL(gated_silu_kernel, grid1d(count), dim3(256), 0, stream, gate, up, out, count);
+  if (count <= 0) return;
+  const int vec = aligned16(gate) && aligned16(up) && aligned16(out);
+  hipLaunchKernelGGL(gated_silu_kernel, grid_ew(count), dim3(256), 0, stream, gate, up, out, count, vec);
   ANIMA_HIP(hipGetLastError());
 }
 void launch_add_half(float* residual, const half_t* branch, int64_t count, hipStream_t stream) {
-  hipLaunchKernelGGL(add_half_kernel, grid1d(count), dim3(256), 0, stream, residual, branch, count);
+  if (count <= 0) return;
+  const int vec = aligned16(residual) && aligned16(branch);
+  hipLaunchKernelGGL(add_half_kernel, grid_ew(count), dim3(256), 0, stream, residual, branch, count, vec);
   ANIMA_HIP(hipGetLastError());
 }
 
@@ -200,6 +426,30 @@ DitBlockExecutor::DitBlockExecutor(anima_ctx* ctx)
       linear_(ctx, anima_linear_config{128, ANIMA_LINEAR_BACKEND_AUTO}) {}
 
 static anima_buffer sub(char* base, int64_t off, int64_t bytes) { return anima_buffer{base + off, bytes}; }
+
+void encode_linear_epilogue(LinearExecutor& lin, anima_buffer input, int64_t input_offset, const anima_qweight& weight,
+                            anima_buffer output, int64_t output_offset, int64_t input_rows, int32_t family,
+                            int epilogue, float* residual, const float* gate) {
+  if (lin.encode_fused(input, input_offset, weight, output, output_offset, input_rows, family, epilogue, residual, gate))
+    return;
+  lin.encode(input, input_offset, weight, output, output_offset, input_rows, family);
+  DeviceGuard guard(lin.context());
+  half_t* y = reinterpret_cast<half_t*>(byte_ptr_mut(output, output_offset));
+  const int64_t count = input_rows * weight.rows;  // bounded by the output range encode() checked
+  if (epilogue == GEMM_GELU)
+    launch_gelu(y, count, lin.context()->stream);
+  else
+    launch_gate_add(residual, y, gate, weight.rows, count, lin.context()->stream);
+}
+
+static MatvecParams matvec_params(const anima_qweight& weight, const float* x, float* y) {
+  const QWeightView v = validate_weight(weight, "DiT modulation");
+  MatvecParams p{};
+  p.w = v.packed; p.scale = v.scale; p.zero = v.zero; p.row_stride = v.row_stride;
+  p.x = x; p.y = y;
+  p.N = (int)v.rows; p.K = (int)v.cols; p.groups = (int)v.groups; p.storage = v.storage;
+  return p;
+}
 
 void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_block_args& a) {
   const int64_t S = a.tokens, dim = a.dim, H = a.heads, hd = a.head_dim, T = a.context_tokens, C = a.context_dim,
@@ -226,9 +476,8 @@ void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_
 
   // Workspace layout (bytes, 256-aligned).
   auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
-  const int64_t o_silu = 0;
-  const int64_t o_hid = o_silu + al(dim * 4);
-  const int64_t o_mod = o_hid + al(lora * 4);
+  const int64_t o_hid = 0, hid_bytes = al(lora * 4);
+  const int64_t o_mod = o_hid + 3 * hid_bytes;
   const int64_t mod_bytes = al(3 * dim * 4);
   const int64_t o_norm = o_mod + 3 * mod_bytes;
   const int64_t act = al(checked_product({S, dim, 2}, "DiT block"));
@@ -242,23 +491,27 @@ void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_
   hipStream_t stream = ctx_->stream;
   char* ws = static_cast<char*>(ws_.get(total, stream));
   float* residual = static_cast<float*>(a.residual.ptr);
-  anima_buffer silu_b = sub(ws, o_silu, dim * 4), hid_b = sub(ws, o_hid, lora * 4);
   anima_buffer norm_b = sub(ws, o_norm, S * dim * 2), q_b = sub(ws, o_q, S * dim * 2), k_b = sub(ws, o_k, S * dim * 2),
                v_b = sub(ws, o_v, S * dim * 2), a_b = sub(ws, o_a, S * dim * 2), br_b = sub(ws, o_b, S * dim * 2),
                ck_b = sub(ws, o_ck, T * dim * 2), cv_b = sub(ws, o_cv, T * dim * 2), h_b = sub(ws, o_h, S * hidden * 2);
 
-  // Modulation (DiTBlockExecutor.encodeModulation, :1403-1417): SiLU(emb) -> W1 -> W2 -> + adaln_lora.
-  launch_silu(static_cast<const float*>(a.emb.ptr), static_cast<float*>(silu_b.ptr), dim, stream);
+  // Modulation (DiTBlockExecutor.encodeModulation, :1403-1417): SiLU(emb) -> W1 -> W2 -> + adaln_lora,
+  // for the three branches at once: one launch for the W1 matvecs (SiLU applied to emb as it is
+  // read), one for the W2 matvecs (adaln_lora added to each output).
   const anima_qweight* w1s[3] = {&w.mod_self_w1, &w.mod_cross_w1, &w.mod_mlp_w1};
   const anima_qweight* w2s[3] = {&w.mod_self_w2, &w.mod_cross_w2, &w.mod_mlp_w2};
   float* mods[3];
+  MatvecParams mv1[3], mv2[3];
   for (int br = 0; br < 3; ++br) {
-    anima_buffer mod_b = sub(ws, o_mod + br * mod_bytes, 3 * dim * 4);
-    mods[br] = static_cast<float*>(mod_b.ptr);
-    encode_matvec(ctx_, *w1s[br], silu_b, 0, hid_b, 0);
-    encode_matvec(ctx_, *w2s[br], hid_b, 0, mod_b, 0);
-    launch_add(mods[br], static_cast<const float*>(a.adaln_lora.ptr), 3 * dim, stream);
+    mods[br] = reinterpret_cast<float*>(ws + o_mod + br * mod_bytes);
+    float* hid = reinterpret_cast<float*>(ws + o_hid + br * hid_bytes);
+    mv1[br] = matvec_params(*w1s[br], static_cast<const float*>(a.emb.ptr), hid);
+    mv1[br].silu_input = 1;
+    mv2[br] = matvec_params(*w2s[br], hid, mods[br]);
+    mv2[br].bias = static_cast<const float*>(a.adaln_lora.ptr);
   }
+  launch_matvec_batch(mv1, 3, stream);
+  launch_matvec_batch(mv2, 3, stream);
 
   anima_attention_args att{};
   att.heads = H; att.head_dim = hd; att.key_value_heads = H; att.layout = ANIMA_LAYOUT_TOKEN_MAJOR;
@@ -273,8 +526,8 @@ void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_
   att.query = q_b; att.key = k_b; att.value = v_b; att.output = a_b;
   att.query_count = S; att.key_count = S; att.prologue = &self_pro;
   attention_.encode(att);
-  linear_.encode(a_b, 0, w.self_o, br_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION);
-  launch_gate_add(residual, static_cast<const half_t*>(br_b.ptr), mods[0] + 2 * dim, dim, S * dim, stream);
+  encode_linear_epilogue(linear_, a_b, 0, w.self_o, br_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION, GEMM_GATE_ADD,
+                         residual, mods[0] + 2 * dim);
 
   // Cross attention to the context (no RoPE; per-head RMSNorm on Q and K).
   launch_layernorm_modulate(residual, mods[1], static_cast<half_t*>(norm_b.ptr), dim, S, a.eps, dim, stream);
@@ -285,15 +538,14 @@ void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_
   att.query = q_b; att.key = ck_b; att.value = cv_b; att.output = a_b;
   att.query_count = S; att.key_count = T; att.prologue = &cross_pro;
   attention_.encode(att);
-  linear_.encode(a_b, 0, w.cross_o, br_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION);
-  launch_gate_add(residual, static_cast<const half_t*>(br_b.ptr), mods[1] + 2 * dim, dim, S * dim, stream);
+  encode_linear_epilogue(linear_, a_b, 0, w.cross_o, br_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION, GEMM_GATE_ADD,
+                         residual, mods[1] + 2 * dim);
 
   // MLP (encodeMLP, :1244-1319): mlp1 -> exact GELU -> mlp2.
   launch_layernorm_modulate(residual, mods[2], static_cast<half_t*>(norm_b.ptr), dim, S, a.eps, dim, stream);
-  linear_.encode(norm_b, 0, w.mlp1, h_b, 0, S, ANIMA_FAMILY_MLP_UP);
-  launch_gelu(static_cast<half_t*>(h_b.ptr), S * hidden, stream);
-  linear_.encode(h_b, 0, w.mlp2, br_b, 0, S, ANIMA_FAMILY_MLP_DOWN);
-  launch_gate_add(residual, static_cast<const half_t*>(br_b.ptr), mods[2] + 2 * dim, dim, S * dim, stream);
+  encode_linear_epilogue(linear_, norm_b, 0, w.mlp1, h_b, 0, S, ANIMA_FAMILY_MLP_UP, GEMM_GELU, nullptr, nullptr);
+  encode_linear_epilogue(linear_, h_b, 0, w.mlp2, br_b, 0, S, ANIMA_FAMILY_MLP_DOWN, GEMM_GATE_ADD, residual,
+                         mods[2] + 2 * dim);
 }
 
 // ---------------------------------------------------------------------------

@@ -20,6 +20,13 @@ void launch_rmsnorm_half(const float* in, const half_t* w, half_t* out, int64_t 
 void launch_gated_silu(const half_t* gate, const half_t* up, half_t* out, int64_t count, hipStream_t stream);
 void launch_add_half(float* residual, const half_t* branch, int64_t count, hipStream_t stream);
 
+// lin.encode() followed by gelu (GEMM_GELU) on its output, or by gate_add of its
+// output into residual with gate (GEMM_GATE_ADD), fused into the GEMM when the
+// tiled kernel takes the shape.  residual / gate ranges are the caller's to check.
+void encode_linear_epilogue(LinearExecutor& lin, anima_buffer input, int64_t input_offset, const anima_qweight& weight,
+                            anima_buffer output, int64_t output_offset, int64_t input_rows, int32_t family,
+                            int epilogue, float* residual, const float* gate);
+
 class DitBlockExecutor {
  public:
   explicit DitBlockExecutor(anima_ctx* ctx);

@@ -48,6 +48,7 @@ inline int64_t checked_end(int64_t off, int64_t bytes, const char* what) {
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
 inline const char* byte_ptr(const anima_buffer& b, int64_t off) {
   return static_cast<const char*>(b.ptr) + off;
@@ -75,6 +76,39 @@ __device__ __forceinline__ half_t f32_to_f16(float v) {
   asm volatile("" : "+v"(v));
   return (half_t)v;
 }
+
+// erf by the Chebyshev fit of erfc in Numerical Recipes (erfcc: for z = |x|,
+// t = 1 / (1 + z/2), erfc(z) = t exp(-z^2 + P(t)) with a degree-9 P, fractional
+// error below 1.2e-7), the form of the reference's erf_f32
+// (AnimaKernels.metal:252-272); the coefficients are the published table.  The
+// reciprocal and the exponential are the hardware's v_rcp_f32 and v_exp_f32
+// (1 ulp each): branch-free, about 20 VALU operations.
+__device__ __forceinline__ float erf_nr(float x) {
+  const float z = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
+  float p = 0.17087277f;
+  p = fmaf(p, t, -0.82215223f);
+  p = fmaf(p, t, 1.48851587f);
+  p = fmaf(p, t, -1.13520398f);
+  p = fmaf(p, t, 0.27886807f);
+  p = fmaf(p, t, -0.18628806f);
+  p = fmaf(p, t, 0.09678418f);
+  p = fmaf(p, t, 0.37409196f);
+  p = fmaf(p, t, 1.00002368f);
+  p = fmaf(p, t, -1.26551223f);
+  const float erfc = t * __builtin_amdgcn_exp2f(fmaf(-z, z, p) * 1.4426950408889634f);
+  return copysignf(1.0f - erfc, x);
+}
+
+// Exact-erf GELU of an fp16 value, rounded once more to fp16
+// (dit_gelu_half_inplace, AnimaKernels.metal:312-322).
+__device__ __forceinline__ half_t gelu_erf_half(half_t h) {
+  const float x = (float)h;
+  return f32_to_f16(0.5f * x * (1.0f + erf_nr(x * 0.7071067811865475f)));
+}
+
+// SiLU in fp32 (silu, AnimaKernels.metal:388-397).
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 
 // s_waitcnt vmcnt(n) alone (expcnt / lgkmcnt unconstrained), n in [0, 15].
 template <int N>

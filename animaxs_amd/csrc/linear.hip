@@ -337,9 +337,76 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantParams p) {
 }
 
 // ===========================================================================
-// fp32 matvec (w4/w8/fp16_matvec_f32): one wave per output row, fp32 FMA per
-// lane then a wave tree reduction.
+// fp32 matvec (w4/w8/fp16_matvec_f32).
+//
+// Vectorised form: LPR lanes per output row, 64/LPR rows per wave.  Each lane
+// reads 16-byte chunks of the packed row (8 fp16 / 16 W8 / 32 W4 weights, always
+// inside one 64-column quantisation group) and accumulates x*w with fp32 FMAs; a
+// butterfly over the row's LPR lanes sums it.  One launch takes up to MV_BATCH
+// independent matvecs of one storage and lane split (the DiT modulation's three
+// branches), each with an optional SiLU on the input and bias on the output.
+// Rows that are not 16-byte aligned, or whose length is not a multiple of the
+// chunk, take the scalar kernel (one wave per row, one weight per lane and step).
 // ===========================================================================
+template <int STORAGE>
+struct MvChunk {
+  static constexpr int elems = STORAGE == ANIMA_STORAGE_W4 ? 32 : STORAGE == ANIMA_STORAGE_W8 ? 16 : 8;
+};
+
+__device__ __forceinline__ float mv_finish(const MatvecParams& p, int row, float sum) {
+  return p.bias ? sum + p.bias[row] : sum;
+}
+
+template <int STORAGE, int LPR>
+__global__ __launch_bounds__(256) void matvec_vec_kernel(MatvecBatch b) {
+  constexpr int E = MvChunk<STORAGE>::elems, RPW = 64 / LPR;
+  int bi = 0;
+#pragma unroll
+  for (int j = 1; j < MV_BATCH; ++j)
+    if (j < b.count && (int)blockIdx.x >= b.first_block[j]) bi = j;
+  MatvecParams p = b.p[0];
+  if (bi == 1) p = b.p[1];
+  if (bi == 2) p = b.p[2];
+  const int lane = threadIdx.x & 63, sub = lane & (LPR - 1);
+  const int row = ((int)blockIdx.x - b.first_block[bi]) * (4 * RPW) + (threadIdx.x >> 6) * RPW + lane / LPR;
+  float sum = 0.f;
+  if (row < p.N) {
+    const uint8_t* wrow = p.w + (int64_t)row * p.row_stride * (STORAGE == ANIMA_STORAGE_FP16 ? 2 : 1);
+    const int nch = p.K / E;
+    for (int c = sub; c < nch; c += LPR) {
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(wrow + (int64_t)c * 16);
+      const int k0 = c * E;
+      float xv[E];
+#pragma unroll
+      for (int e = 0; e < E; e += 4) {
+        const floatx4 t = *reinterpret_cast<const floatx4*>(p.x + k0 + e);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) xv[e + u] = p.silu_input ? silu_f32(t[u]) : t[u];
+      }
+      if (STORAGE == ANIMA_STORAGE_FP16) {
+        const half8v wv = __builtin_bit_cast(half8v, raw);
+#pragma unroll
+        for (int e = 0; e < E; ++e) sum = fmaf(xv[e], (float)wv[e], sum);
+      } else {
+        const int64_t g = (int64_t)row * p.groups + k0 / 64;
+        const float sc = (float)p.scale[g], zr = (float)p.zero[g];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          uint32_t q;
+          if (STORAGE == ANIMA_STORAGE_W4)
+            q = (raw[e / 8] >> (4 * (e % 8))) & 0x0Fu;
+          else
+            q = (raw[e / 4] >> (8 * (e % 4))) & 0xFFu;
+          sum = fmaf(xv[e], (float)q * sc + zr, sum);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int off = LPR / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  if (row < p.N && sub == 0) p.y[row] = mv_finish(p, row, sum);
+}
+
 __global__ __launch_bounds__(256) void matvec_kernel(MatvecParams p) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -347,7 +414,10 @@ __global__ __launch_bounds__(256) void matvec_kernel(MatvecParams p) {
   float sum = 0.f;
   if (p.storage == ANIMA_STORAGE_FP16) {
     const half_t* w16 = reinterpret_cast<const half_t*>(p.w) + (int64_t)row * p.row_stride;
-    for (int k = lane; k < p.K; k += 64) sum = fmaf(p.x[k], (float)w16[k], sum);
+    for (int k = lane; k < p.K; k += 64) {
+      const float x = p.silu_input ? silu_f32(p.x[k]) : p.x[k];
+      sum = fmaf(x, (float)w16[k], sum);
+    }
   } else {
     const uint8_t* w = p.w + (int64_t)row * p.row_stride;
     for (int k = lane; k < p.K; k += 64) {
@@ -360,11 +430,12 @@ __global__ __launch_bounds__(256) void matvec_kernel(MatvecParams p) {
       }
       const int64_t g = (int64_t)row * p.groups + k / 64;
       const float v = (float)q * (float)p.scale[g] + (float)p.zero[g];
-      sum = fmaf(p.x[k], v, sum);
+      const float x = p.silu_input ? silu_f32(p.x[k]) : p.x[k];
+      sum = fmaf(x, v, sum);
     }
   }
   for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-  if (lane == 0) p.y[row] = sum;
+  if (lane == 0) p.y[row] = mv_finish(p, row, sum);
 }
 
 // ===========================================================================
@@ -384,6 +455,7 @@ void launch_gemm(const GemmParams& p, int storage, hipStream_t stream) {
     launch_pingpong(p, storage, stream);
     return;
   }
+  if (p.epilogue != GEMM_STORE) fail(ANIMA_E_UNSUPPORTED, "fused GEMM epilogues need the ping-pong kernel");
   const int64_t tiles = (int64_t)((p.M + G_BM - 1) / G_BM) * ((p.N + G_BN - 1) / G_BN);
   if (tiles <= 0) return;
   if (tiles > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "GEMM grid too large");
@@ -416,10 +488,70 @@ void launch_dequant(const DequantParams& p, hipStream_t stream) {
   ANIMA_HIP(hipGetLastError());
 }
 
+// Lanes per row for the vectorised matvec: the smallest power of two in [8, 64]
+// that covers the row's chunks in one step, or 0 when the row does not vectorise.
+static int matvec_lanes(const MatvecParams& p) {
+  const int e = p.storage == ANIMA_STORAGE_W4 ? 32 : p.storage == ANIMA_STORAGE_W8 ? 16 : 8;
+  const int64_t stride_bytes = p.row_stride * (p.storage == ANIMA_STORAGE_FP16 ? 2 : 1);
+  if (p.K % e != 0 || stride_bytes % 16 != 0 || !aligned16(p.w) || !aligned16(p.x)) return 0;
+  const int nch = p.K / e;
+  int lpr = 8;
+  while (lpr < 64 && lpr < nch) lpr *= 2;
+  return lpr;
+}
+
+template <int STORAGE>
+static void launch_matvec_vec(const MatvecBatch& b, int lpr, unsigned blocks, hipStream_t stream) {
+  switch (lpr) {
+    case 8: hipLaunchKernelGGL((matvec_vec_kernel<STORAGE, 8>), dim3(blocks), dim3(256), 0, stream, b); break;
+    case 16: hipLaunchKernelGGL((matvec_vec_kernel<STORAGE, 16>), dim3(blocks), dim3(256), 0, stream, b); break;
+    case 32: hipLaunchKernelGGL((matvec_vec_kernel<STORAGE, 32>), dim3(blocks), dim3(256), 0, stream, b); break;
+    default: hipLaunchKernelGGL((matvec_vec_kernel<STORAGE, 64>), dim3(blocks), dim3(256), 0, stream, b); break;
+  }
+}
+
+void launch_matvec_batch(const MatvecParams* ps, int count, hipStream_t stream) {
+  if (count < 1 || count > MV_BATCH) fail(ANIMA_E_INVALID_ARGUMENT, "matvec batch holds 1 to 3 matvecs");
+  const int lpr = matvec_lanes(ps[0]);
+  bool together = lpr != 0;
+  for (int i = 1; i < count; ++i)
+    together = together && ps[i].storage == ps[0].storage && matvec_lanes(ps[i]) == lpr;
+  if (!together) {
+    for (int i = 0; i < count; ++i) {
+      if (ps[i].N <= 0) continue;
+      if (matvec_lanes(ps[i]) != 0) {
+        launch_matvec_batch(&ps[i], 1, stream);
+      } else {
+        hipLaunchKernelGGL(matvec_kernel, dim3((unsigned)((ps[i].N + 3) / 4)), dim3(256), 0, stream, ps[i]);
+        ANIMA_HIP(hipGetLastError());
+      }
+    }
+    return;
+  }
+  MatvecBatch b{};
+  const int rows_per_block = 4 * (64 / lpr);
+  int64_t blocks = 0;
+  for (int i = 0; i < count; ++i) {
+    b.p[i] = ps[i];
+    b.first_block[i] = (int)blocks;
+    blocks += ps[i].N > 0 ? (ps[i].N + rows_per_block - 1) / rows_per_block : 0;
+  }
+  for (int i = count; i < MV_BATCH; ++i) b.first_block[i] = (int)blocks;
+  b.count = count;
+  if (blocks <= 0) return;
+  if (blocks > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "matvec grid too large");
+  if (ps[0].storage == ANIMA_STORAGE_W4)
+    launch_matvec_vec<ANIMA_STORAGE_W4>(b, lpr, (unsigned)blocks, stream);
+  else if (ps[0].storage == ANIMA_STORAGE_W8)
+    launch_matvec_vec<ANIMA_STORAGE_W8>(b, lpr, (unsigned)blocks, stream);
+  else
+    launch_matvec_vec<ANIMA_STORAGE_FP16>(b, lpr, (unsigned)blocks, stream);
+  ANIMA_HIP(hipGetLastError());
+}
+
 void launch_matvec(const MatvecParams& p, hipStream_t stream) {
   if (p.N <= 0) return;
-  hipLaunchKernelGGL(matvec_kernel, dim3((unsigned)((p.N + 3) / 4)), dim3(256), 0, stream, p);
-  ANIMA_HIP(hipGetLastError());
+  launch_matvec_batch(&p, 1, stream);
 }
 
 }  // namespace anima

@@ -13,7 +13,17 @@ struct GemmParams {
   const half_t* zero;     // [N, groups]
   int64_t row_stride;     // bytes (W4/W8) or halfs (FP16)
   int M, N, K, groups;
+  // Output stage (ping-pong kernel only; the others require GEMM_STORE):
+  //   GEMM_STORE     y = half(acc)
+  //   GEMM_GELU      y = half(gelu_erf(half(acc)))   (dit_gelu_half_inplace fused)
+  //   GEMM_GATE_ADD  residual[m, n] += float(half(acc)) * gate[n]; y is not written
+  //                  (gate_add_half_f32 fused)
+  int epilogue;
+  float* residual;        // [M, N] fp32, GEMM_GATE_ADD
+  const float* gate;      // [N] fp32, GEMM_GATE_ADD
 };
+
+enum GemmEpilogue { GEMM_STORE = 0, GEMM_GELU = 1, GEMM_GATE_ADD = 2 };
 
 struct MatvecParams {
   const uint8_t* w;
@@ -23,6 +33,17 @@ struct MatvecParams {
   const float* x;
   float* y;
   int N, K, groups, storage;
+  int silu_input;         // use x / (1 + exp(-x)) in place of x (silu kernel fused)
+  const float* bias;      // optional [N]: y = sum + bias (add_f32 fused)
+};
+
+// Up to MV_BATCH independent matvecs in one launch; blocks [first_block[i],
+// first_block[i+1]) compute matvec i.
+constexpr int MV_BATCH = 3;
+struct MatvecBatch {
+  MatvecParams p[MV_BATCH];
+  int first_block[MV_BATCH];
+  int count;
 };
 
 struct DequantParams {
@@ -80,6 +101,8 @@ constexpr int SMALLM_MAX_ROWS = 64;
 bool smallm_supported(const GemmParams& p, int storage);
 void launch_smallm(const GemmParams& p, int storage, hipStream_t stream);
 void launch_matvec(const MatvecParams& p, hipStream_t stream);
+// count (1..MV_BATCH) matvecs; one launch when they share storage and lane split.
+void launch_matvec_batch(const MatvecParams* ps, int count, hipStream_t stream);
 void launch_dequant(const DequantParams& p, hipStream_t stream);
 
 class LinearExecutor {
@@ -87,9 +110,18 @@ class LinearExecutor {
   LinearExecutor(anima_ctx* ctx, const anima_linear_config& cfg);
   void encode(anima_buffer input, int64_t input_offset, const anima_qweight& weight, anima_buffer output,
               int64_t output_offset, int64_t input_rows, int32_t family);
+  // encode() with a fused output stage (GEMM_GELU or GEMM_GATE_ADD, see GemmParams)
+  // when the ping-pong kernel takes the shape under the automatic backend; returns
+  // false, having encoded nothing, otherwise.  residual is [input_rows, weight.rows]
+  // fp32 and gate [weight.rows] fp32, both ranges checked by the caller.
+  bool encode_fused(anima_buffer input, int64_t input_offset, const anima_qweight& weight, anima_buffer output,
+                    int64_t output_offset, int64_t input_rows, int32_t family, int epilogue, float* residual,
+                    const float* gate);
   anima_ctx* context() const { return ctx_; }
 
  private:
+  GemmParams prepare(anima_buffer input, int64_t input_offset, const QWeightView& w, anima_buffer output,
+                     int64_t output_offset, int64_t input_rows) const;
   anima_ctx* ctx_;
   anima_linear_config cfg_;
   Workspace ws_;

@@ -50,13 +50,10 @@ LinearExecutor::LinearExecutor(anima_ctx* ctx, const anima_linear_config& cfg) :
     fail(ANIMA_E_INVALID_ARGUMENT, "unknown linear backend");
 }
 
-void LinearExecutor::encode(anima_buffer input, int64_t input_offset, const anima_qweight& weight,
-                            anima_buffer output, int64_t output_offset, int64_t input_rows, int32_t family) {
-  if (family < ANIMA_FAMILY_OTHER || family > ANIMA_FAMILY_MLP_DOWN)
-    fail(ANIMA_E_INVALID_ARGUMENT, "unknown linear family");
+GemmParams LinearExecutor::prepare(anima_buffer input, int64_t input_offset, const QWeightView& w,
+                                   anima_buffer output, int64_t output_offset, int64_t input_rows) const {
   if (!(input_rows > 0 && input_offset >= 0 && output_offset >= 0))
     fail(ANIMA_E_INVALID_SHAPE, "invalid LinearExecutor shape or offset");
-  const QWeightView w = validate_weight(weight, "LinearExecutor");
   const int64_t in_bytes = checked_product({input_rows, w.cols, 2}, "LinearExecutor");
   const int64_t out_bytes = checked_product({input_rows, w.rows, 2}, "LinearExecutor");
   if (checked_end(input_offset, in_bytes, "LinearExecutor") > input.length ||
@@ -65,9 +62,6 @@ void LinearExecutor::encode(anima_buffer input, int64_t input_offset, const anim
   if (!input.ptr || !output.ptr) fail(ANIMA_E_INVALID_ARGUMENT, "LinearExecutor buffer pointer is null");
   if ((input_offset | output_offset) & 1) fail(ANIMA_E_MISALIGNED, "LinearExecutor offsets must be 2-byte aligned");
   if (input_rows > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "LinearExecutor input rows exceed int32");
-
-  DeviceGuard guard(ctx_);
-  hipStream_t stream = ctx_->stream;
   GemmParams p{};
   p.x = reinterpret_cast<const half_t*>(byte_ptr(input, input_offset));
   p.y = reinterpret_cast<half_t*>(byte_ptr_mut(output, output_offset));
@@ -75,6 +69,24 @@ void LinearExecutor::encode(anima_buffer input, int64_t input_offset, const anim
   p.N = (int)w.rows;
   p.K = (int)w.cols;
   p.groups = (int)w.groups;
+  p.w = w.packed;
+  p.scale = w.scale;
+  p.zero = w.zero;
+  p.row_stride = w.row_stride;
+  return p;
+}
+
+void LinearExecutor::encode(anima_buffer input, int64_t input_offset, const anima_qweight& weight,
+                            anima_buffer output, int64_t output_offset, int64_t input_rows, int32_t family) {
+  if (family < ANIMA_FAMILY_OTHER || family > ANIMA_FAMILY_MLP_DOWN)
+    fail(ANIMA_E_INVALID_ARGUMENT, "unknown linear family");
+  if (!(input_rows > 0 && input_offset >= 0 && output_offset >= 0))
+    fail(ANIMA_E_INVALID_SHAPE, "invalid LinearExecutor shape or offset");
+  const QWeightView w = validate_weight(weight, "LinearExecutor");
+  GemmParams p = prepare(input, input_offset, w, output, output_offset, input_rows);
+
+  DeviceGuard guard(ctx_);
+  hipStream_t stream = ctx_->stream;
   if (cfg_.backend == ANIMA_LINEAR_BACKEND_DEQUANT_THEN_GEMM && w.storage != ANIMA_STORAGE_FP16) {
     // Reference default shape: dequantise the whole weight once into fp16
     // scratch (LinearExecutor.swift:146-193), then the fp16 GEMM.
@@ -86,18 +98,36 @@ void LinearExecutor::encode(anima_buffer input, int64_t input_offset, const anim
     dp.groups = (int)w.groups; dp.storage = w.storage;
     launch_dequant(dp, stream);
     p.w = reinterpret_cast<const uint8_t*>(scratch);
+    p.scale = nullptr;
+    p.zero = nullptr;
     p.row_stride = stride;
     launch_gemm(p, ANIMA_STORAGE_FP16, stream);
     return;
   }
-  p.w = w.packed;
-  p.scale = w.scale;
-  p.zero = w.zero;
-  p.row_stride = w.row_stride;
   if (smallm_supported(p, w.storage))
     launch_smallm(p, w.storage, stream);
   else
     launch_gemm(p, w.storage, stream);
+}
+
+bool LinearExecutor::encode_fused(anima_buffer input, int64_t input_offset, const anima_qweight& weight,
+                                  anima_buffer output, int64_t output_offset, int64_t input_rows, int32_t family,
+                                  int epilogue, float* residual, const float* gate) {
+  if (family < ANIMA_FAMILY_OTHER || family > ANIMA_FAMILY_MLP_DOWN)
+    fail(ANIMA_E_INVALID_ARGUMENT, "unknown linear family");
+  if (epilogue != GEMM_GELU && epilogue != GEMM_GATE_ADD) fail(ANIMA_E_INVALID_ARGUMENT, "unknown linear epilogue");
+  if (!(input_rows > 0 && input_offset >= 0 && output_offset >= 0))
+    fail(ANIMA_E_INVALID_SHAPE, "invalid LinearExecutor shape or offset");
+  const QWeightView w = validate_weight(weight, "LinearExecutor");
+  GemmParams p = prepare(input, input_offset, w, output, output_offset, input_rows);
+  if (cfg_.backend != ANIMA_LINEAR_BACKEND_AUTO || smallm_supported(p, w.storage) || !pingpong_supported(p, w.storage))
+    return false;
+  p.epilogue = epilogue;
+  p.residual = residual;
+  p.gate = gate;
+  DeviceGuard guard(ctx_);
+  launch_pingpong(p, w.storage, ctx_->stream);
+  return true;
 }
 
 void encode_matvec(anima_ctx* ctx, const anima_qweight& weight, anima_buffer input, int64_t input_offset,

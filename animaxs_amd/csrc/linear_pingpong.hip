@@ -54,6 +54,8 @@ constexpr int PG_WIN = 8;                   // K blocks per scale/zero window
 constexpr int PG_WINBUF = PG_BN * PG_WIN * 2 * 2;    // one window: scale and zero of 256 rows (8 KiB)
 constexpr int PG_WINOFF = 2 * PG_XSTAGE;    // windows: [group][buffer] after the X stages
 static_assert(PG_WINOFF + 4 * PG_WINBUF <= PG_SMEM, "X stages and windows fit in the reduction area");
+constexpr int PG_OROW = PG_BN + 8;          // padded output-tile row in LDS (halfs)
+static_assert(PG_BM * PG_OROW * 2 <= PG_SMEM, "output tile fits in the reduction area");
 
 typedef __attribute__((address_space(3))) half8v lds_half8v;
 
@@ -367,7 +369,10 @@ void pingpong_gemm_kernel(GemmParams p, int vec_store) {
   }
 
   // K-split sum: group 0 finishes row tiles 0-1, group 1 row tiles 2-3; each hands
-  // the other half to its partner wave (same SIMD, same columns) through LDS.
+  // the other half to its partner wave (same SIMD, same columns) through LDS.  The
+  // rounded fp16 sums then go to an output tile in LDS (rows padded to PG_OROW) so
+  // that the output stage reads whole 16-byte row chunks: every global access of
+  // the output (and of the residual for the gate-add stage) is a full-row burst.
   auto finish = [&](auto mine_c) __attribute__((always_inline)) {
     constexpr int MINE = decltype(mine_c)::value, GIVE = 2 - MINE;
     char* own = smem + (group * 4 + wg) * PG_RED;
@@ -383,34 +388,87 @@ void pingpong_gemm_kernel(GemmParams p, int vec_store) {
           *reinterpret_cast<floatx4*>(own + (((t * 2 + j) * 4 + q) * 64 + lane) * 16) = v;
         }
     barrier();
+    half4v out[2][2][4];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int m = m0 + 32 * (MINE + j) + c32;
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const floatx4 o = *reinterpret_cast<const floatx4*>(partner + (((t * 2 + j) * 4 + q) * 64 + lane) * 16);
-          const int n = n0 + 64 * wg + 32 * t + 8 * q + 4 * hh;
-          const half4v v = {(half_t)(acc[t][MINE + j][4 * q] + o[0]), (half_t)(acc[t][MINE + j][4 * q + 1] + o[1]),
-                            (half_t)(acc[t][MINE + j][4 * q + 2] + o[2]), (half_t)(acc[t][MINE + j][4 * q + 3] + o[3])};
-          if (m < p.M) {
-            half_t* yrow = p.y + (int64_t)m * p.N;
-            if (vec_store && n + 3 < p.N) {
-              *reinterpret_cast<half4v*>(yrow + n) = v;
-            } else {
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                if (n + e < p.N) yrow[n + e] = v[e];
-            }
-          }
+          out[t][j][q] = half4v{(half_t)(acc[t][MINE + j][4 * q] + o[0]), (half_t)(acc[t][MINE + j][4 * q + 1] + o[1]),
+                                (half_t)(acc[t][MINE + j][4 * q + 2] + o[2]),
+                                (half_t)(acc[t][MINE + j][4 * q + 3] + o[3])};
         }
-      }
+    barrier();  // every partner read done: the tile may overwrite the exchange area
+    half_t* tile = reinterpret_cast<half_t*>(smem);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<half4v*>(tile + (32 * (MINE + j) + c32) * PG_OROW + 64 * wg + 32 * t + 8 * q + 4 * hh) =
+              out[t][j][q];
   };
   if (group == 0)
     finish(std::integral_constant<int, 0>{});
   else
     finish(std::integral_constant<int, 2>{});
+  barrier();
+
+  // Output stage: thread tid takes 16-byte chunk tid % 32 of tile rows tid / 32 + 16i.
+  const half_t* tile = reinterpret_cast<const half_t*>(smem);
+  const int ochunk = tid & 31, orow = tid >> 5;
+  const int n = n0 + 8 * ochunk;
+  auto store_tile = [&](auto epi_c) __attribute__((always_inline)) {
+    constexpr int EPI = decltype(epi_c)::value;
+#pragma unroll 2
+    for (int i = 0; i < PG_BM / 16; ++i) {
+      const int r = orow + 16 * i, m = m0 + r;
+      half8v v = *reinterpret_cast<const half8v*>(tile + r * PG_OROW + 8 * ochunk);
+      if (m >= p.M) continue;
+      if (EPI == GEMM_GELU) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = gelu_erf_half(v[e]);
+      }
+      if (EPI == GEMM_GATE_ADD) {
+        float* rrow = p.residual + (int64_t)m * p.N;
+        if (vec_store && n + 8 <= p.N) {
+          floatx4 r0 = *reinterpret_cast<const floatx4*>(rrow + n);
+          floatx4 r1 = *reinterpret_cast<const floatx4*>(rrow + n + 4);
+          const floatx4 g0 = *reinterpret_cast<const floatx4*>(p.gate + n);
+          const floatx4 g1 = *reinterpret_cast<const floatx4*>(p.gate + n + 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            r0[e] = fmaf((float)v[e], g0[e], r0[e]);
+            r1[e] = fmaf((float)v[4 + e], g1[e], r1[e]);
+          }
+          *reinterpret_cast<floatx4*>(rrow + n) = r0;
+          *reinterpret_cast<floatx4*>(rrow + n + 4) = r1;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (n + e < p.N) rrow[n + e] = fmaf((float)v[e], p.gate[n + e], rrow[n + e]);
+        }
+      } else {
+        half_t* yrow = p.y + (int64_t)m * p.N;
+        if (vec_store && n + 8 <= p.N) {
+          *reinterpret_cast<half8v*>(yrow + n) = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (n + e < p.N) yrow[n + e] = v[e];
+        }
+      }
+    }
+  };
+  if (p.epilogue == GEMM_GELU)
+    store_tile(std::integral_constant<int, GEMM_GELU>{});
+  else if (p.epilogue == GEMM_GATE_ADD)
+    store_tile(std::integral_constant<int, GEMM_GATE_ADD>{});
+  else
+    store_tile(std::integral_constant<int, GEMM_STORE>{});
 }
 
 bool pingpong_supported(const GemmParams& p, int storage) {
@@ -426,7 +484,11 @@ void launch_pingpong(const GemmParams& p, int storage, hipStream_t stream) {
   if (!pingpong_supported(p, storage)) fail(ANIMA_E_INVALID_SHAPE, "ping-pong GEMM: unsupported shape or alignment");
   const int64_t tiles = (int64_t)((p.M + PG_BM - 1) / PG_BM) * ((p.N + PG_BN - 1) / PG_BN);
   if (tiles > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "GEMM grid too large");
-  const int vec = ((reinterpret_cast<uintptr_t>(p.y) & 7u) == 0 && p.N % 4 == 0) ? 1 : 0;
+  if (p.epilogue == GEMM_GATE_ADD && (!p.residual || !p.gate))
+    fail(ANIMA_E_INVALID_ARGUMENT, "GEMM gate-add epilogue needs residual and gate");
+  // 16-byte output accesses: every row start 16-byte aligned.
+  const int vec = p.epilogue == GEMM_GATE_ADD ? (aligned16(p.residual) && aligned16(p.gate) && p.N % 8 == 0 ? 1 : 0)
+                                              : (aligned16(p.y) && p.N % 8 == 0 ? 1 : 0);
   const bool swin = p.groups % PG_WIN == 0 && aligned16(p.scale) && aligned16(p.zero);
   const dim3 grid((unsigned)tiles), block(PG_NT);
   if (storage == ANIMA_STORAGE_W4) {

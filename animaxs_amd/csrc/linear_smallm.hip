@@ -379,6 +379,7 @@ bool smallm_supported(const GemmParams& p, int storage) {
 }
 
 void launch_smallm(const GemmParams& g, int storage, hipStream_t stream) {
+  if (g.epilogue != GEMM_STORE) fail(ANIMA_E_UNSUPPORTED, "fused GEMM epilogues need the ping-pong kernel");
   SmallMParams p{};
   p.x = g.x; p.y = g.y; p.w = g.w; p.scale = g.scale; p.zero = g.zero;
   p.row_stride = g.row_stride; p.M = g.M; p.N = g.N; p.K = g.K; p.groups = g.groups;

@@ -220,6 +220,7 @@ class QuantizedLinearWeightBuffers:
 
 
 _LBACK = {"auto": _abi.LINEAR_AUTO, "fused": _abi.LINEAR_FUSED, "dequantizedGEMM": _abi.LINEAR_DEQUANT_THEN_GEMM}
+_EPILOGUE = {"gelu": 1, "gate_add": 2}
 _FAMILY = {"other": _abi.FAMILY_OTHER, "attentionProjection": _abi.FAMILY_ATTENTION_PROJECTION,
            "mlpUp": _abi.FAMILY_MLP_UP, "mlpDown": _abi.FAMILY_MLP_DOWN}
 
@@ -240,6 +241,17 @@ class LinearExecutor:
         w = weight.to_c()
         call("anima_linear_encode", self._h, as_buffer(input), int(input_offset), C.byref(w),
              as_buffer(output), int(output_offset), int(input_rows), _FAMILY[family])
+
+    def encode_epilogue(self, input, weight: QuantizedLinearWeightBuffers, output, input_rows: int,
+                        epilogue: str, residual=None, gate=None, input_offset: int = 0, output_offset: int = 0,
+                        family: str = "other") -> None:
+        """encode() followed by the DiT block's next step, fused into the GEMM where it can be:
+        epilogue "gelu" (dit_gelu_half_inplace on the output) or "gate_add" (gate_add_half_f32
+        of the output into the fp32 residual with the fp32 gate; output is then scratch)."""
+        w = weight.to_c()
+        call("anima_linear_encode_epilogue", self._h, as_buffer(input), int(input_offset), C.byref(w),
+             as_buffer(output), int(output_offset), int(input_rows), _FAMILY[family], _EPILOGUE[epilogue],
+             as_buffer(residual), as_buffer(gate))
 
     def execute(self, input, weight: QuantizedLinearWeightBuffers, output, input_rows: int,
                 input_offset: int = 0, output_offset: int = 0, family: str = "other") -> None:

@@ -248,6 +248,28 @@ anima_status anima_linear_execute(anima_linear* lin, anima_buffer input, int64_t
                                   const anima_qweight* weight, anima_buffer output,
                                   int64_t output_offset, int64_t input_rows, int32_t family);
 
+/* Extension, no reference entry point: a linear followed by the DiT block's next
+ * elementwise step, which DiTBlockExecutor encodes as two dispatches
+ * (DiTBlockExecutor.swift:1180-1242 output projection + gate_add_half_f32,
+ * :1244-1319 mlp1 + dit_gelu_half_inplace).
+ *   ANIMA_LINEAR_EPILOGUE_GELU:     output = half(gelu_erf(linear(input)))
+ *   ANIMA_LINEAR_EPILOGUE_GATE_ADD: residual[r, n] += float(linear(input)[r, n]) * gate[n]
+ *                                   (residual fp32 [input_rows, weight.rows], gate fp32
+ *                                   [weight.rows]); output is scratch the call may
+ *                                   leave unwritten.
+ * Results equal anima_linear_encode followed by anima_gelu_half_inplace_encode /
+ * anima_gate_add_half_f32_encode bit for bit: the tiled GEMM applies the step in
+ * its output stage when it takes the shape, otherwise the two kernels run in turn.
+ * residual and gate are ignored for ANIMA_LINEAR_EPILOGUE_GELU. */
+typedef enum anima_linear_epilogue {
+  ANIMA_LINEAR_EPILOGUE_GELU = 1,
+  ANIMA_LINEAR_EPILOGUE_GATE_ADD = 2
+} anima_linear_epilogue;
+anima_status anima_linear_encode_epilogue(anima_linear* lin, anima_buffer input, int64_t input_offset,
+                                          const anima_qweight* weight, anima_buffer output,
+                                          int64_t output_offset, int64_t input_rows, int32_t family,
+                                          int32_t epilogue, anima_buffer residual, anima_buffer gate);
+
 /* M=1 fp32 matvec w4_matvec_f32 / w8_matvec_f32 / fp16_matvec_f32
  * (AnimaKernels.metal:804-933; DiTQuantizedWeightFactory.matvecKernel,
  * LinearExecutor.swift:520-528): output_f32[N] = deq(W)[N,K] . input_f32[K]. */

@@ -147,3 +147,72 @@ def test_rmsnorm_gated_silu_add_half(ctx):
     ops.add_half_into_float(rd, dev(br), rows * n)
     torch.cuda.synchronize()
     assert torch.equal(rd.cpu(), res + br.float())
+
+
+@pytest.mark.parametrize("rows,n,off", [(5, 2050, 0), (3, 6000, 0), (9, 512, 2), (4, 4096, 0), (6, 100, 0),
+                                        (2, 8192, 0)])
+def test_norm_kernels_wave_and_row_forms(ctx, rows, n, off):
+    """The wave-per-row form (n % 4 == 0, n <= 4096, 16-byte aligned rows) and the
+    workgroup-per-row form (n % 4 != 0, n > 4096, or buffers offset by `off` elements) of
+    dit_layernorm_modulate_to_half and rmsnorm + float_to_half."""
+    g = torch.Generator().manual_seed(rows * n + off)
+    x = torch.randn(rows * n + off, generator=g) * 2 - 0.3
+    mod = torch.randn(3 * n + off, generator=g)
+    w = (torch.rand(n + off, generator=g) * 0.4 + 0.8).half()
+    ops = BlockOps(ctx)
+    xd, md, wd = dev(x), dev(mod), dev(w)
+    out = torch.full((rows * n + off,), float("nan"), dtype=torch.float16, device="cuda")
+    print(f"NORM rows={rows} n={n} off={off}", flush=True)
+    ops.layernorm_modulate_to_half(xd[off:], md[off:], out[off:], n, rows, 1e-6)
+    torch.cuda.synchronize()
+    xr = x[off:].reshape(rows, n)
+    ref = norms.layer_norm_modulated(xr, mod[off + n:off + 2 * n], mod[off:off + n]).half()
+    got = out.cpu()[off:].reshape(rows, n)
+    assert float((got.float() - ref.float()).abs().max()) <= 2 ** -9 * float(ref.float().abs().max())
+    out.fill_(float("nan"))
+    ops.rmsnorm_f32_to_half(xd[off:], wd[off:], out[off:], n, rows, 1e-6)
+    torch.cuda.synchronize()
+    rref = norms.rms_norm(xr, w[off:], 1e-6).half()
+    got = out.cpu()[off:].reshape(rows, n)
+    assert float((got.float() - rref.float()).abs().max()) <= 2 ** -10 * float(rref.float().abs().max())
+
+
+@pytest.mark.parametrize("count,n,off", [(8 * 2048, 2048, 0), (4099, 4099, 1), (2047 * 3, 2047, 0),
+                                         (13, 13, 3), (8 * 4096 + 5, 4096, 0)])
+def test_elementwise_chunk_and_tail_forms(ctx, count, n, off):
+    """Elementwise kernels in their 16-byte chunk form, with a partial last chunk, with buffers
+    offset by `off` elements (element-wise form) and a gate width that is not a multiple of 8."""
+    g = torch.Generator().manual_seed(count + off)
+    ops = BlockOps(ctx)
+    print(f"ELEMENTWISE count={count} n={n} off={off}", flush=True)
+    h = (torch.randn(count + off, generator=g) * 4).half()
+    hd = dev(h)
+    ops.gelu_half_inplace(hd[off:], count)
+    gref = norms.gelu_erf(h[off:].float()).half()
+    res = torch.randn(count + off, generator=g)
+    br = torch.randn(count + off, generator=g).half()
+    gate = torch.randn(n + off, generator=g)
+    rd = dev(res.clone())
+    ops.gate_add_half_f32(rd[off:], dev(br)[off:], dev(gate)[off:], n, count)
+    a = torch.randn(count + off, generator=g)
+    b = torch.randn(count + off, generator=g)
+    ad, so = dev(a.clone()), torch.zeros(count + off, device="cuda")
+    ops.silu(dev(b)[off:], so[off:], count)
+    ops.add_f32(ad[off:], so[off:], count)
+    gt = (torch.randn(count + off, generator=g) * 4).half()
+    up = torch.randn(count + off, generator=g).half()
+    o = torch.zeros(count + off, dtype=torch.float16, device="cuda")
+    ops.gated_silu_half(dev(gt)[off:], dev(up)[off:], o[off:], count)
+    rh = dev(res.clone())
+    ops.add_half_into_float(rh[off:], dev(br)[off:], count)
+    torch.cuda.synchronize()
+    assert torch.equal(hd.cpu()[:off], h[:off])
+    assert float((hd.cpu()[off:].float() - gref.float()).abs().max()) <= 2 ** -9 * 8
+    cols = torch.arange(count) % n
+    want = res[off:] + br[off:].float() * gate[off:][cols]
+    assert torch.allclose(rd.cpu()[off:], want, atol=1e-5, rtol=1e-6)
+    assert torch.equal(rd.cpu()[:off], res[:off])
+    assert torch.allclose(ad.cpu()[off:], a[off:] + norms.silu(b[off:]), atol=1e-6, rtol=1e-5)
+    sref = (norms.silu(gt[off:].float()) * up[off:].float()).half()
+    assert float((o.cpu()[off:].float() - sref.float()).abs().max()) <= 2 ** -10 * max(1.0, float(sref.float().abs().max()))
+    assert torch.equal(rh.cpu()[off:], res[off:] + br[off:].float())

@@ -399,3 +399,76 @@ def test_gemm_dequant_bit_exact_via_one_hot(ctx, storage, M):
               f"scale={sb.reshape(-1)[g]:#06x} zero={zb.reshape(-1)[g]:#06x}", flush=True)
     assert len(mism) == 0
     assert finite.mean() > 0.99
+
+
+@pytest.mark.parametrize("storage,M,N,K", [(0, 256, 2048, 2048), (1, 130, 520, 320), (0, 257, 1000, 448),
+                                           (1, 129, 770, 128), (0, 32, 512, 512), (2, 96, 256, 256),
+                                           (0, 100, 300, 200)])
+def test_linear_epilogues_equal_two_step(ctx, storage, M, N, K):
+    """anima_linear_encode_epilogue: the tiled GEMM's fused GELU / gate-add output stage (M > 64,
+    W4/W8, K a multiple of 64; N % 4 != 0 takes its element-wise stores) and the two-kernel
+    fallback (small M, fp16 storage, K not a multiple of 64) give the same bits as the linear
+    followed by dit_gelu_half_inplace / gate_add_half_f32."""
+    from animaxs_amd import BlockOps
+    w = _affine_weight(storage, N, K, seed=7 * M + N + K + storage)
+    qw, keep = device_weight(w)
+    g = torch.Generator().manual_seed(M * 3 + N)
+    x = dev(torch.randn(M, K, generator=g).half())
+    lin, ops = LinearExecutor(ctx), BlockOps(ctx)
+    print(f"EPILOGUE storage={storage} M={M} N={N} K={K}", flush=True)
+
+    y_ref = torch.empty(M * N, dtype=torch.float16, device="cuda")
+    lin.encode(x, qw, y_ref, M)
+    ops.gelu_half_inplace(y_ref, M * N)
+    y = torch.full((M * N,), float("nan"), dtype=torch.float16, device="cuda")
+    lin.encode_epilogue(x, qw, y, M, "gelu")
+
+    res0 = torch.randn(M * N, generator=g)
+    gate = dev(torch.randn(N, generator=g))
+    branch = torch.empty(M * N, dtype=torch.float16, device="cuda")
+    r_ref = dev(res0.clone())
+    lin.encode(x, qw, branch, M)
+    ops.gate_add_half_f32(r_ref, branch, gate, N, M * N)
+    r = dev(res0.clone())
+    lin.encode_epilogue(x, qw, torch.empty_like(branch), M, "gate_add", residual=r, gate=gate)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+    assert torch.equal(r.view(torch.int32), r_ref.view(torch.int32))
+    assert not torch.equal(r.cpu(), res0)
+
+
+def test_linear_epilogue_rejects_bad_arguments(ctx):
+    w = _affine_weight(0, 256, 256, seed=5)
+    qw, keep = device_weight(w)
+    x = torch.zeros(128, 256, dtype=torch.float16, device="cuda")
+    y = torch.empty(128, 256, dtype=torch.float16, device="cuda")
+    lin = LinearExecutor(ctx)
+    with pytest.raises(AnimaError) as e:
+        lin.encode_epilogue(x, qw, y, 128, "gate_add", residual=torch.zeros(128 * 256 - 1, device="cuda"),
+                            gate=torch.zeros(256, device="cuda"))
+    assert "out of bounds" in e.value.message
+    with pytest.raises(AnimaError):
+        lin.encode_epilogue(x, qw, y, 128, "gate_add", residual=torch.zeros(128 * 256, device="cuda"), gate=None)
+
+
+@pytest.mark.parametrize("storage", [0, 1, 2])
+@pytest.mark.parametrize("N,K,pad", [(6144, 256, 0), (256, 2048, 0), (33, 96, 16), (7, 4096, 0), (5, 130, 0)])
+def test_matvec_vectorised_every_storage(ctx, storage, N, K, pad):
+    """The fp32 matvec's 16-byte chunk form (8 to 64 lanes per row, several rows per wave, padded
+    strides) and its scalar form (K=130: not a multiple of the chunk) against an fp64 product of
+    the fp32 dequantised weights."""
+    w = _affine_weight(storage, N, K, seed=N + K + storage, pad=pad)
+    qw, keep = device_weight(w)
+    x = torch.randn(K, generator=torch.Generator().manual_seed(K)).float()
+    y = torch.full((N + 4,), float("nan"), device="cuda")
+    print(f"MATVEC storage={storage} N={N} K={K} pad={pad}", flush=True)
+    LinearExecutor.encode_matvec(ctx, qw, dev(x), y)
+    torch.cuda.synchronize()
+    wf = quant.dequant_matrix_f32(storage, w["packed"], w["scale_bits"], w["zero_bits"], N, K,
+                                  w["row_stride"]).astype(np.float64)
+    xd = x.double().numpy()
+    ref = wf @ xd
+    got = y.cpu().numpy().astype(np.float64)
+    assert np.isnan(got[N:]).all()
+    bound = 1e-5 * (np.abs(wf) @ np.abs(xd)) + 1e-6
+    assert (np.abs(got[:N] - ref) <= bound).all(), float(np.abs(got[:N] - ref).max())
