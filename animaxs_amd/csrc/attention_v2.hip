@@ -8,11 +8,11 @@
 //     2 waves per SIMD).  The waves form two groups, one wave of each group per
 //     SIMD (waves w and w+4 share a SIMD).  Work per key tile j is split into two
 //     phases:
-//       G(j)  MFMA phase: QK^T of tile j, PV of tile j-1 and the row sums of tile
-//             j-1 on the matrix cores (lsum += ones x P^T), as one fixed sequence
-//             of MFMAs whose LDS fragment reads run a few MFMAs ahead;
+//       G(j)  MFMA phase: QK^T of tile j and PV of tile j-1 on the matrix cores,
+//             as one fixed sequence of MFMAs whose LDS fragment reads run a few
+//             MFMAs ahead;
 //       X(j)  VALU phase: the tile copies (below), masking, row max, the (rare)
-//             O rescale, exp2 and fp16 P of tile j.
+//             O rescale, exp2, fp16 P and the fp32 row sums of tile j.
 //     Phases are separated by workgroup barriers, and group 1 runs one phase
 //     behind group 0 (one extra barrier at the start, group 0 one at the end), so
 //     in every barrier interval one wave of each SIMD issues MFMAs while the
@@ -21,8 +21,9 @@
 //     waves waiting on the same unit.
 //   * K and V tiles (64 keys) are copied global -> VGPR -> LDS: during X(j) a wave
 //     stores its staged segments of tile j+2 (ds_write_b128) and issues the
-//     buffer loads of tile j+3, so a full tile period hides the load latency and
-//     the LDS writes never queue ahead of the same wave's fragment reads.  Buffer
+//     buffer loads of tile j+4 into the staging registers those leave (two
+//     buffers), so two tile periods hide the load latency, and the LDS writes
+//     never queue ahead of the same wave's fragment reads.  Buffer
 //     descriptors bound every tile by the last key row in use: rows past it read
 //     as zeros without touching memory.
 //   * Rows are padded in LDS (K: +16 B, V: +64 B) so the fragment reads hit
@@ -201,10 +202,11 @@ void flash_attention_v2_kernel(FlashParams p) {
   };
 
   // Copies go global -> VGPR -> LDS: load_tile fetches this thread's chunks of tile
-  // j into staging registers, store_seg writes copy r into a stage one tile period
-  // later.
-  u32x4 stg[NCP];
-  auto load_tile = [&](int j) __attribute__((always_inline)) {
+  // j into staging buffer j % 2, store_seg writes copy r into a stage two tile
+  // periods later (two buffers keep two tiles in flight).
+  u32x4 stg2[2][NCP];
+  auto load_tile = [&](int j, auto bufc) __attribute__((always_inline)) {
+    u32x4 (&stg)[NCP] = stg2[decltype(bufc)::value];
     const char* kt = reinterpret_cast<const char*>(kbase) + (int64_t)j * F2_BN * ktok2;
     const char* vt = reinterpret_cast<const char*>(vbase) + (int64_t)j * F2_BN * vtok2;
     const int nk = tile_bytes(j, ktok2), nv = tile_bytes(j, vtok2);
@@ -213,15 +215,16 @@ void flash_attention_v2_kernel(FlashParams p) {
 #pragma unroll
     for (int r = 0; r < CPT; ++r) stg[CPT + r] = load16_bounded(vt, nv, goff_v[r]);
   };
-  auto store_seg = [&](int r, auto st) __attribute__((always_inline)) {
+  auto store_seg = [&](int r, auto st, auto bufc) __attribute__((always_inline)) {
+    u32x4 (&stg)[NCP] = stg2[decltype(bufc)::value];
     if (r < CPT)
       *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(kstage(st)) + loff_k + RSTEP * r * KROW * 2) = stg[r];
     else
       *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(vstage(st)) + loff_v + RSTEP * (r - CPT) * VROW * 2) = stg[r];
   };
-  auto store_tile = [&](auto st) __attribute__((always_inline)) {
+  auto store_tile = [&](auto st, auto bufc) __attribute__((always_inline)) {
 #pragma unroll
-    for (int r = 0; r < NCP; ++r) store_seg(r, st);
+    for (int r = 0; r < NCP; ++r) store_seg(r, st, bufc);
   };
 
   half8v qf[QS];
@@ -231,11 +234,11 @@ void flash_attention_v2_kernel(FlashParams p) {
 #pragma unroll
   for (int c = 0; c < OB; ++c) acc[c] = floatx16{};
   float m_run = -INFINITY;
-  // Row sums on the matrix cores: lsum += ones(32x16) x P^T gives, in every lane,
-  // the sum of its query's fp16 probabilities (fp32 accumulation).
-  floatx16 lsum = floatx16{};
-  const half8v ones = {(half_t)1.f, (half_t)1.f, (half_t)1.f, (half_t)1.f,
-                       (half_t)1.f, (half_t)1.f, (half_t)1.f, (half_t)1.f};
+  // Row sum of the fp32 probabilities over this lane's 32 keys of each tile (the
+  // other 32 are in lane c32 + 32(1-hh)); the two halves meet at the end.  Summing
+  // on the VALU costs 32 adds per tile in the VALU phase; the four MFMAs of an
+  // ones x P^T product cost more (they lengthen every MFMA phase by 1/8).
+  float lrow = 0.f;
   const float c2 = p.scale_log2;
 
   typedef __attribute__((address_space(3))) half8v lds_half8v;
@@ -284,12 +287,12 @@ void flash_attention_v2_kernel(FlashParams p) {
     // Anchor the keys-32..63 exponentials in this phase (the compiler would hoist
     // them above the barrier into the VALU phase).
     // The phase is a fixed sequence of NOPS MFMAs: QK (op i < 2*QS: key half i/QS,
-    // d-step i%QS), PV (op 2*QS + k: key half k/(4*OB), 16-key block k/OB % 2, d
-    // block k%OB) and the four row-sum MFMAs.  Operand fragments come from LDS
+    // d-step i%QS) and PV (op 2*QS + k: key half k/(4*OB), 16-key block k/OB % 2,
+    // d block k%OB).  Operand fragments come from LDS
     // F2_READ_AHEAD ops ahead of their MFMA through a small register ring; the
     // sched_barriers pin that order (the scheduler would otherwise trade the
     // read-ahead for registers).
-    constexpr int NQK = 2 * QS, NPV = 4 * OB, NOPS = NQK + NPV + 4;
+    constexpr int NQK = 2 * QS, NPV = 4 * OB, NOPS = NQK + NPV;
     constexpr int RING = F2_READ_AHEAD + 1;
     half8v ring[RING];
     auto read_op = [&](int i) __attribute__((always_inline)) -> half8v {
@@ -301,16 +304,13 @@ void flash_attention_v2_kernel(FlashParams p) {
     for (int i = 0; i < F2_READ_AHEAD; ++i) ring[i % RING] = read_op(i);
 #pragma unroll
     for (int i = 0; i < NOPS; ++i) {
-      if (i + F2_READ_AHEAD < NQK + NPV) ring[(i + F2_READ_AHEAD) % RING] = read_op(i + F2_READ_AHEAD);
+      if (i + F2_READ_AHEAD < NOPS) ring[(i + F2_READ_AHEAD) % RING] = read_op(i + F2_READ_AHEAD);
       if (i < NQK) {
         const int h = i / QS;
         S[h] = mfma32(ring[i % RING], qf[i % QS], i % QS == 0 ? floatx16{} : S[h]);
-      } else if (i < NQK + NPV) {
+      } else {
         const int k = i - NQK;
         acc[k % OB] = mfma32(ring[i % RING], P[k / (2 * OB)][(k / OB) & 1], acc[k % OB]);
-      } else {
-        const int r = i - NQK - NPV;
-        lsum = mfma32(ones, P[r >> 1][r & 1], lsum);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -325,21 +325,18 @@ void flash_attention_v2_kernel(FlashParams p) {
       for (int u = 0; u < 2; ++u)
 #pragma unroll
         for (int c = 0; c < OB; ++c) acc[c] = mfma32(vfrag_read(st, h, u, c), P[h][u], acc[c]);
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int u = 0; u < 2; ++u) lsum = mfma32(ones, P[h][u], lsum);
   };
 
-  // X(j): the tile copies (tile j+2, staged in registers during X(j-1), goes to
-  // LDS; the loads of tile j+3 start), then P = fp16(exp2(S*c - m)) with the
+  // X(j): the tile copies (tile j+2, staged in registers during X(j-2), goes to
+  // LDS; the loads of tile j+4 start into the buffer it leaves), then P = fp16(exp2(S*c - m)) with the
   // running max m, rescaling O first when a row's max grew by more than 2^8.  The
   // copies sit in the VALU phase so that their LDS writes never queue ahead of
   // the fragment reads of this wave's MFMA phase.
   auto x_phase = [&](int j, auto st) __attribute__((always_inline)) {
     using SW = std::integral_constant<int, (decltype(st)::value + 2) % F2_STAGES>;
-    store_tile(SW{});        // tile j+2
-    load_tile(j + 3);        // all zeros past the last tile
+    using BUF = std::integral_constant<int, decltype(st)::value % 2>;
+    store_tile(SW{}, BUF{});   // tile j+2
+    load_tile(j + 4, BUF{});   // all zeros past the last tile
     const int k0 = j * F2_BN;
     if ((k0 + F2_BN > kv_len) || (p.causal && k0 + F2_BN - 1 > wq0)) {
 #pragma unroll
@@ -362,16 +359,22 @@ void flash_attention_v2_kernel(FlashParams p) {
     if (__any(mloc > m_run + F2_RESCALE_THRESHOLD)) {
       const float mnew = fmaxf(m_run, mloc);
       const float alpha = (mnew == -INFINITY) ? 1.f : fast_exp2(m_run - mnew);
-      lsum *= alpha;
+      lrow *= alpha;
 #pragma unroll
       for (int c = 0; c < OB; ++c) acc[c] *= alpha;
       m_run = mnew;
     }
     msub = (m_run == -INFINITY) ? 0.f : m_run;
+    float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int e = 0; e < 16; ++e) P[0][e >> 3][e & 7] = exp_p(S[0][e]);
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) P[1][e >> 3][e & 7] = exp_p(S[1][e]);
+      for (int e = 0; e < 16; ++e) {
+        const float pe = fast_exp2(fmaf(S[h][e], c2, -msub));
+        P[h][e >> 3][e & 7] = (half_t)pe;
+        ls[e & 3] += pe;
+      }
+    lrow += (ls[0] + ls[1]) + (ls[2] + ls[3]);
     asm volatile("" ::"v"(P[0][0]), "v"(P[0][1]), "v"(P[1][0]), "v"(P[1][1]));
   };
 
@@ -385,11 +388,14 @@ void flash_attention_v2_kernel(FlashParams p) {
   using S1 = std::integral_constant<int, 1>;
   using S2 = std::integral_constant<int, 2>;
   using S3 = std::integral_constant<int, 3>;
-  load_tile(0);
-  store_tile(S0{});
-  load_tile(1);
-  store_tile(S1{});
-  load_tile(2);
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  load_tile(0, B0{});
+  store_tile(S0{}, B0{});
+  load_tile(1, B1{});
+  store_tile(S1{}, B1{});
+  load_tile(2, B0{});
+  load_tile(3, B1{});
 #pragma unroll
   for (int e = 0; e < 16; ++e) S[1][e] = -INFINITY;   // G(0) derives P[1] of tile "-1": zeros
   barrier();                      // tiles 0 and 1 resident
@@ -414,7 +420,7 @@ void flash_attention_v2_kernel(FlashParams p) {
   if (group == 0) barrier();      // same barrier count for both groups
   wait_vmcnt_imm<0>();            // loads of tiles past the end (no memory traffic)
 
-  const float l_tot = lsum[0];
+  const float l_tot = xlane32_sum(lrow);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (qi < p.Sq) {
     half_t* op = p.o + (int64_t)b * p.o_batch + (int64_t)head * p.o_head + (int64_t)qi * p.o_tok;
