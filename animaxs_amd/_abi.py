@@ -132,6 +132,7 @@ SIGNATURES = {
     "anima_linear_destroy": (_S, [_P]),
     "anima_linear_encode": (_S, [_P, Buffer, _I64, C.POINTER(QWeight), Buffer, _I64, _I64, _I32]),
     "anima_linear_execute": (_S, [_P, Buffer, _I64, C.POINTER(QWeight), Buffer, _I64, _I64, _I32]),
+    "anima_linear_encode_group": (_S, [_P, Buffer, _P, _P, _I32, _I64, _I32]),
     "anima_linear_encode_epilogue": (_S, [_P, Buffer, _I64, C.POINTER(QWeight), Buffer, _I64, _I64, _I32, _I32,
                                           Buffer, Buffer]),
     "anima_matvec_encode": (_S, [_P, C.POINTER(QWeight), Buffer, _I64, Buffer, _I64]),

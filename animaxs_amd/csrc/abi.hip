@@ -156,6 +156,19 @@ anima_status anima_linear_encode_epilogue(anima_linear* lin, anima_buffer input,
   });
 }
 
+anima_status anima_linear_encode_group(anima_linear* lin, anima_buffer input, const anima_qweight* const* weights,
+                                       const anima_buffer* outputs, int32_t count, int64_t input_rows,
+                                       int32_t family) {
+  return guarded([&] {
+    require(lin, "linear");
+    require(weights, "weights");
+    require(outputs, "outputs");
+    if (count < 1 || count > 3) fail(ANIMA_E_INVALID_ARGUMENT, "linear group holds 1 to 3 weights");
+    for (int i = 0; i < count; ++i) require(weights[i], "weight");
+    lin->impl.encode_group(input, weights, outputs, count, input_rows, family);
+  });
+}
+
 anima_status anima_linear_execute(anima_linear* lin, anima_buffer input, int64_t input_offset,
                                   const anima_qweight* weight, anima_buffer output, int64_t output_offset,
                                   int64_t input_rows, int32_t family) {

@@ -519,9 +519,11 @@ void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_
 
   // Self attention (encodeAttentionBranch, :1035-1242).
   launch_layernorm_modulate(residual, mods[0], static_cast<half_t*>(norm_b.ptr), dim, S, a.eps, dim, stream);
-  linear_.encode(norm_b, 0, w.self_q, q_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION);
-  linear_.encode(norm_b, 0, w.self_k, k_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION);
-  linear_.encode(norm_b, 0, w.self_v, v_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION);
+  {
+    const anima_qweight* ws3[3] = {&w.self_q, &w.self_k, &w.self_v};
+    const anima_buffer outs[3] = {q_b, k_b, v_b};
+    linear_.encode_group(norm_b, ws3, outs, 3, S, ANIMA_FAMILY_ATTENTION_PROJECTION);
+  }
   anima_qk_prologue self_pro{w.self_q_norm, w.self_k_norm, a.eps, a.rope, S, 1, 1};
   att.query = q_b; att.key = k_b; att.value = v_b; att.output = a_b;
   att.query_count = S; att.key_count = S; att.prologue = &self_pro;
@@ -532,8 +534,11 @@ void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_
   // Cross attention to the context (no RoPE; per-head RMSNorm on Q and K).
   launch_layernorm_modulate(residual, mods[1], static_cast<half_t*>(norm_b.ptr), dim, S, a.eps, dim, stream);
   linear_.encode(norm_b, 0, w.cross_q, q_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION);
-  linear_.encode(a.context, 0, w.cross_k, ck_b, 0, T, ANIMA_FAMILY_ATTENTION_PROJECTION);
-  linear_.encode(a.context, 0, w.cross_v, cv_b, 0, T, ANIMA_FAMILY_ATTENTION_PROJECTION);
+  {
+    const anima_qweight* ws2[2] = {&w.cross_k, &w.cross_v};
+    const anima_buffer outs[2] = {ck_b, cv_b};
+    linear_.encode_group(a.context, ws2, outs, 2, T, ANIMA_FAMILY_ATTENTION_PROJECTION);
+  }
   anima_qk_prologue cross_pro{w.cross_q_norm, w.cross_k_norm, a.eps, nullptr, 0, 0, 0};
   att.query = q_b; att.key = ck_b; att.value = cv_b; att.output = a_b;
   att.query_count = S; att.key_count = T; att.prologue = &cross_pro;
@@ -604,9 +609,11 @@ void QwenLayerExecutor::encode(const anima_qwen_layer_weights& w, const anima_qw
 
   // Attention branch (:244-282).
   launch_rmsnorm_half(residual, static_cast<const half_t*>(w.input_norm), norm, hidden, rows, a.eps, stream);
-  linear_.encode(norm_b, 0, w.q, q_b, 0, rows, ANIMA_FAMILY_ATTENTION_PROJECTION);
-  linear_.encode(norm_b, 0, w.k, k_b, 0, rows, ANIMA_FAMILY_ATTENTION_PROJECTION);
-  linear_.encode(norm_b, 0, w.v, v_b, 0, rows, ANIMA_FAMILY_ATTENTION_PROJECTION);
+  {
+    const anima_qweight* ws3[3] = {&w.q, &w.k, &w.v};
+    const anima_buffer outs[3] = {q_b, k_b, v_b};
+    linear_.encode_group(norm_b, ws3, outs, 3, rows, ANIMA_FAMILY_ATTENTION_PROJECTION);
+  }
   anima_qk_prologue pro{w.q_norm, w.k_norm, a.eps, a.rope, S, 1, 1};
   anima_attention_args att{};
   att.query = q_b; att.key = k_b; att.value = v_b; att.output = att_b;
@@ -619,8 +626,11 @@ void QwenLayerExecutor::encode(const anima_qwen_layer_weights& w, const anima_qw
 
   // MLP branch (:284-302): gate/up -> SwiGLU (into the gate buffer) -> down.
   launch_rmsnorm_half(residual, static_cast<const half_t*>(w.post_attention_norm), norm, hidden, rows, a.eps, stream);
-  linear_.encode(norm_b, 0, w.gate, gate_b, 0, rows, ANIMA_FAMILY_MLP_UP);
-  linear_.encode(norm_b, 0, w.up, up_b, 0, rows, ANIMA_FAMILY_MLP_UP);
+  {
+    const anima_qweight* ws2[2] = {&w.gate, &w.up};
+    const anima_buffer outs[2] = {gate_b, up_b};
+    linear_.encode_group(norm_b, ws2, outs, 2, rows, ANIMA_FAMILY_MLP_UP);
+  }
   launch_gated_silu(static_cast<const half_t*>(gate_b.ptr), static_cast<const half_t*>(up_b.ptr),
                     static_cast<half_t*>(gate_b.ptr), rows * inter, stream);
   linear_.encode(gate_b, 0, w.down, proj_b, 0, rows, ANIMA_FAMILY_MLP_DOWN);

@@ -25,6 +25,17 @@ struct GemmParams {
 
 enum GemmEpilogue { GEMM_STORE = 0, GEMM_GELU = 1, GEMM_GATE_ADD = 2 };
 
+// Up to PG_GROUP independent GEMMs of one K and storage in one ping-pong launch
+// (the Q/K/V projections of one input): logical tiles [first_tile[i],
+// first_tile[i+1]) compute problem i.
+constexpr int PG_GROUP = 3;
+struct GemmGroup {
+  GemmParams p[PG_GROUP];
+  int first_tile[PG_GROUP];
+  int vec[PG_GROUP];      // 16-byte output accesses allowed
+  int count;
+};
+
 struct MatvecParams {
   const uint8_t* w;
   const half_t* scale;
@@ -94,6 +105,8 @@ void launch_gemm(const GemmParams& p, int storage, hipStream_t stream);
 // and weight rows, buffers below 2 GiB.  launch_gemm routes to it when it applies.
 bool pingpong_supported(const GemmParams& p, int storage);
 void launch_pingpong(const GemmParams& p, int storage, hipStream_t stream);
+// count (1..PG_GROUP) ping-pong GEMMs sharing K and storage in one launch.
+void launch_pingpong_group(const GemmParams* ps, int count, int storage, hipStream_t stream);
 
 // Weight-streaming GEMM for M <= SMALLM_MAX_ROWS (linear_smallm.hip); requires K a
 // multiple of 128 and 16-byte aligned X and weight rows.
@@ -117,6 +130,11 @@ class LinearExecutor {
   bool encode_fused(anima_buffer input, int64_t input_offset, const anima_qweight& weight, anima_buffer output,
                     int64_t output_offset, int64_t input_rows, int32_t family, int epilogue, float* residual,
                     const float* gate);
+  // count (1..PG_GROUP) linears of one input, each into its own output, as one
+  // ping-pong launch when every one of them takes that kernel (same K and storage);
+  // otherwise encode() for each in turn.
+  void encode_group(anima_buffer input, const anima_qweight* const* weights, const anima_buffer* outputs, int count,
+                    int64_t input_rows, int32_t family);
   anima_ctx* context() const { return ctx_; }
 
  private:

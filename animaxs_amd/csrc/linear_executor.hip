@@ -110,6 +110,30 @@ void LinearExecutor::encode(anima_buffer input, int64_t input_offset, const anim
     launch_gemm(p, w.storage, stream);
 }
 
+void LinearExecutor::encode_group(anima_buffer input, const anima_qweight* const* weights, const anima_buffer* outputs,
+                                  int count, int64_t input_rows, int32_t family) {
+  if (count < 1 || count > PG_GROUP) fail(ANIMA_E_INVALID_ARGUMENT, "linear group holds 1 to 3 weights");
+  if (family < ANIMA_FAMILY_OTHER || family > ANIMA_FAMILY_MLP_DOWN)
+    fail(ANIMA_E_INVALID_ARGUMENT, "unknown linear family");
+  if (!(input_rows > 0)) fail(ANIMA_E_INVALID_SHAPE, "invalid LinearExecutor shape or offset");
+  GemmParams ps[PG_GROUP];
+  int storage = -1;
+  bool together = cfg_.backend == ANIMA_LINEAR_BACKEND_AUTO;
+  for (int i = 0; i < count; ++i) {
+    const QWeightView w = validate_weight(*weights[i], "LinearExecutor");
+    ps[i] = prepare(input, 0, w, outputs[i], 0, input_rows);
+    together = together && !smallm_supported(ps[i], w.storage) && pingpong_supported(ps[i], w.storage) &&
+               (i == 0 || (w.storage == storage && ps[i].K == ps[0].K));
+    storage = w.storage;
+  }
+  if (!together) {
+    for (int i = 0; i < count; ++i) encode(input, 0, *weights[i], outputs[i], 0, input_rows, family);
+    return;
+  }
+  DeviceGuard guard(ctx_);
+  launch_pingpong_group(ps, count, storage, ctx_->stream);
+}
+
 bool LinearExecutor::encode_fused(anima_buffer input, int64_t input_offset, const anima_qweight& weight,
                                   anima_buffer output, int64_t output_offset, int64_t input_rows, int32_t family,
                                   int epilogue, float* residual, const float* gate) {

@@ -71,7 +71,7 @@ typedef __attribute__((address_space(3))) half8v lds_half8v;
 // row and block.
 template <int STORAGE, bool SWIN>
 __global__ __launch_bounds__(PG_NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void pingpong_gemm_kernel(GemmParams p, int vec_store) {
+void pingpong_gemm_kernel(GemmGroup gp) {
   constexpr bool W4 = STORAGE == ANIMA_STORAGE_W4;
   constexpr int QBITS = W4 ? 4 : 8;
   constexpr int WCH = W4 ? 1 : 2;           // 16-byte weight chunks per lane per row per block
@@ -85,8 +85,17 @@ void pingpong_gemm_kernel(GemmParams p, int vec_store) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int group = wave >> 2, wg = wave & 3;
   const int c32 = lane & 31, hh = lane >> 5;
+  // Problem of this workgroup: logical tiles [first_tile[i], first_tile[i+1]) belong
+  // to problem i (every problem of a group shares K and storage).
+  const int lbg = xcd_logical_block(blockIdx.x, gridDim.x);
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < PG_GROUP; ++i)
+    if (i < gp.count && lbg >= gp.first_tile[i]) pi = i;
+  const GemmParams& p = gp.p[pi];
+  const int vec_store = gp.vec[pi];
   const int ntn = (p.N + PG_BN - 1) / PG_BN;
-  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int lb = lbg - gp.first_tile[pi];
   const int tn = lb % ntn, tm = lb / ntn;
   const int m0 = tm * PG_BM, n0 = tn * PG_BN;
   const int nk = p.K / PG_BK;
@@ -480,29 +489,46 @@ bool pingpong_supported(const GemmParams& p, int storage) {
   return (int64_t)p.M * p.K * 2 <= lim && (int64_t)p.N * p.row_stride <= lim && (int64_t)p.N * p.groups * 2 <= lim;
 }
 
-void launch_pingpong(const GemmParams& p, int storage, hipStream_t stream) {
-  if (!pingpong_supported(p, storage)) fail(ANIMA_E_INVALID_SHAPE, "ping-pong GEMM: unsupported shape or alignment");
-  const int64_t tiles = (int64_t)((p.M + PG_BM - 1) / PG_BM) * ((p.N + PG_BN - 1) / PG_BN);
-  if (tiles > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "GEMM grid too large");
-  if (p.epilogue == GEMM_GATE_ADD && (!p.residual || !p.gate))
-    fail(ANIMA_E_INVALID_ARGUMENT, "GEMM gate-add epilogue needs residual and gate");
-  // 16-byte output accesses: every row start 16-byte aligned.
-  const int vec = p.epilogue == GEMM_GATE_ADD ? (aligned16(p.residual) && aligned16(p.gate) && p.N % 8 == 0 ? 1 : 0)
-                                              : (aligned16(p.y) && p.N % 8 == 0 ? 1 : 0);
-  const bool swin = p.groups % PG_WIN == 0 && aligned16(p.scale) && aligned16(p.zero);
+void launch_pingpong_group(const GemmParams* ps, int count, int storage, hipStream_t stream) {
+  if (count < 1 || count > PG_GROUP) fail(ANIMA_E_INVALID_ARGUMENT, "ping-pong GEMM group holds 1 to 3 problems");
+  GemmGroup g{};
+  bool swin = true;
+  int64_t tiles = 0;
+  for (int i = 0; i < count; ++i) {
+    const GemmParams& p = ps[i];
+    if (!pingpong_supported(p, storage)) fail(ANIMA_E_INVALID_SHAPE, "ping-pong GEMM: unsupported shape or alignment");
+    if (p.K != ps[0].K) fail(ANIMA_E_INVALID_SHAPE, "ping-pong GEMM group: problems must share K");
+    if (p.epilogue == GEMM_GATE_ADD && (!p.residual || !p.gate))
+      fail(ANIMA_E_INVALID_ARGUMENT, "GEMM gate-add epilogue needs residual and gate");
+    swin = swin && p.groups % PG_WIN == 0 && aligned16(p.scale) && aligned16(p.zero);
+    g.p[i] = p;
+    g.first_tile[i] = (int)tiles;
+    // 16-byte output accesses: every row start 16-byte aligned.
+    g.vec[i] = p.epilogue == GEMM_GATE_ADD ? (aligned16(p.residual) && aligned16(p.gate) && p.N % 8 == 0 ? 1 : 0)
+                                           : (aligned16(p.y) && p.N % 8 == 0 ? 1 : 0);
+    tiles += (int64_t)((p.M + PG_BM - 1) / PG_BM) * ((p.N + PG_BN - 1) / PG_BN);
+    if (tiles > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "GEMM grid too large");
+  }
+  for (int i = count; i < PG_GROUP; ++i) g.first_tile[i] = (int)tiles;
+  g.count = count;
+  if (tiles <= 0) return;
   const dim3 grid((unsigned)tiles), block(PG_NT);
   if (storage == ANIMA_STORAGE_W4) {
     if (swin)
-      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W4, true>), grid, block, 0, stream, p, vec);
+      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W4, true>), grid, block, 0, stream, g);
     else
-      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W4, false>), grid, block, 0, stream, p, vec);
+      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W4, false>), grid, block, 0, stream, g);
   } else {
     if (swin)
-      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W8, true>), grid, block, 0, stream, p, vec);
+      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W8, true>), grid, block, 0, stream, g);
     else
-      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W8, false>), grid, block, 0, stream, p, vec);
+      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W8, false>), grid, block, 0, stream, g);
   }
   ANIMA_HIP(hipGetLastError());
+}
+
+void launch_pingpong(const GemmParams& p, int storage, hipStream_t stream) {
+  launch_pingpong_group(&p, 1, storage, stream);
 }
 
 }  // namespace anima

@@ -242,6 +242,18 @@ class LinearExecutor:
         call("anima_linear_encode", self._h, as_buffer(input), int(input_offset), C.byref(w),
              as_buffer(output), int(output_offset), int(input_rows), _FAMILY[family])
 
+    def encode_group(self, input, weights, outputs, input_rows: int, family: str = "other") -> None:
+        """1..3 linears of one input, each into its own output (one launch when the tiled
+        GEMM takes them all)."""
+        n = len(weights)
+        if n != len(outputs):
+            raise ValueError("weights and outputs differ in length")
+        ws = [w.to_c() for w in weights]
+        wp = (C.POINTER(_abi.QWeight) * n)(*[C.pointer(w) for w in ws])
+        ob = (_abi.Buffer * n)(*[as_buffer(o) for o in outputs])
+        call("anima_linear_encode_group", self._h, as_buffer(input), C.cast(wp, C.c_void_p),
+             C.cast(ob, C.c_void_p), n, int(input_rows), _FAMILY[family])
+
     def encode_epilogue(self, input, weight: QuantizedLinearWeightBuffers, output, input_rows: int,
                         epilogue: str, residual=None, gate=None, input_offset: int = 0, output_offset: int = 0,
                         family: str = "other") -> None:

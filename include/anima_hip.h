@@ -270,6 +270,16 @@ anima_status anima_linear_encode_epilogue(anima_linear* lin, anima_buffer input,
                                           int64_t output_offset, int64_t input_rows, int32_t family,
                                           int32_t epilogue, anima_buffer residual, anima_buffer gate);
 
+/* Extension, no reference entry point: count (1..3) linears of one input, each into
+ * its own output -- the Q/K/V (or gate/up) projections that DiTBlockExecutor and
+ * QwenEncoderMetal encode one after another on the same normalised input
+ * (DiTBlockExecutor.swift:1035-1105, QwenEncoderMetal.swift:244-262).  Results equal
+ * count anima_linear_encode calls bit for bit; when every weight takes the tiled
+ * W4/W8 GEMM with the same K and storage, the linears run as one launch. */
+anima_status anima_linear_encode_group(anima_linear* lin, anima_buffer input, const anima_qweight* const* weights,
+                                       const anima_buffer* outputs, int32_t count, int64_t input_rows,
+                                       int32_t family);
+
 /* M=1 fp32 matvec w4_matvec_f32 / w8_matvec_f32 / fp16_matvec_f32
  * (AnimaKernels.metal:804-933; DiTQuantizedWeightFactory.matvecKernel,
  * LinearExecutor.swift:520-528): output_f32[N] = deq(W)[N,K] . input_f32[K]. */

@@ -472,3 +472,27 @@ def test_matvec_vectorised_every_storage(ctx, storage, N, K, pad):
     assert np.isnan(got[N:]).all()
     bound = 1e-5 * (np.abs(wf) @ np.abs(xd)) + 1e-6
     assert (np.abs(got[:N] - ref) <= bound).all(), float(np.abs(got[:N] - ref).max())
+
+
+@pytest.mark.parametrize("storage,M,Ns,K", [(0, 4096 + 40, (2048, 1024, 1024), 1024), (1, 130, (520, 256), 320),
+                                            (0, 512, (2048, 2048), 1024), (0, 257, (1000, 300, 1030), 448),
+                                            (0, 48, (512, 256), 512), (1, 200, (256, 256), 200)])
+def test_linear_group_equals_separate_encodes(ctx, storage, M, Ns, K):
+    """anima_linear_encode_group: one ping-pong launch over 2-3 weights of different N (tile ->
+    problem mapping, ragged M and N) gives the bits of separate encodes; groups the tiled GEMM
+    does not take (small M, K not a multiple of 64) fall back to separate encodes."""
+    ws = [_affine_weight(storage, N, K, seed=N + K + i) for i, N in enumerate(Ns)]
+    qws, keeps = zip(*[device_weight(w) for w in ws])
+    x = dev(torch.randn(M, K, generator=torch.Generator().manual_seed(M + K)).half())
+    lin = LinearExecutor(ctx)
+    refs = []
+    for qw, N in zip(qws, Ns):
+        y = torch.empty(M * N, dtype=torch.float16, device="cuda")
+        lin.encode(x, qw, y, M)
+        refs.append(y)
+    outs = [torch.full((M * N,), float("nan"), dtype=torch.float16, device="cuda") for N in Ns]
+    print(f"GROUP storage={storage} M={M} Ns={Ns} K={K}", flush=True)
+    lin.encode_group(x, list(qws), outs, M)
+    torch.cuda.synchronize()
+    for r, o in zip(refs, outs):
+        assert torch.equal(r.view(torch.int16), o.view(torch.int16))
