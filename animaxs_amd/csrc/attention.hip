@@ -498,6 +498,28 @@ __global__ __launch_bounds__(256) void qk_prologue_d128_kernel(PrologueParams p)
 // Number of compute units the 256-row variant must cover to be chosen by default.
 constexpr int64_t F2_MIN_BLOCKS = 256;
 
+// Key splits for the 256-row kernel when its query tiles alone cannot cover the chip
+// (non-causal, no per-sequence key lengths, automatic row choice): enough splits to
+// reach F2_MIN_BLOCKS workgroups, each of at least F2_MIN_SPLIT_KEYS keys.
+constexpr int F2_MIN_SPLIT_KEYS = 256;
+constexpr int F2_MAX_SPLITS = 8;
+
+int flash_kv_splits(const FlashParams& p, int D, int batch, int flash_rows) {
+  if (flash_rows != 0 || p.causal || p.key_lengths_dev || p.use_host_lengths || (D != 128 && D != 64)) return 1;
+  const int64_t t256 = (int64_t)((p.Sq + FLASH_V2_ROWS - 1) / FLASH_V2_ROWS) * p.H * batch;
+  if (t256 >= F2_MIN_BLOCKS || t256 <= 0) return 1;
+  if (64 * std::max(p.k_tok, p.v_tok) * (int64_t)sizeof(half_t) >= ((int64_t)1 << 31)) return 1;
+  int splits = (int)((F2_MIN_BLOCKS + t256 - 1) / t256);
+  splits = std::min<int>(splits, F2_MAX_SPLITS);
+  splits = std::min<int>(splits, p.Sk / F2_MIN_SPLIT_KEYS);
+  return splits >= 2 ? splits : 1;
+}
+
+int64_t flash_split_bytes(const FlashParams& p, int D, int batch, int splits) {
+  const int64_t rows = checked_product({(int64_t)splits, (int64_t)batch, (int64_t)p.H, (int64_t)p.Sq}, "attention");
+  return checked_product({rows, (int64_t)D + 2, 4}, "attention");
+}
+
 void launch_flash(FlashParams p, int D, int batch, int flash_rows, hipStream_t stream) {
   if (D != 128 && D != 64) fail(ANIMA_E_UNSUPPORTED, "flash attention requires head_dim 64 or 128");
   const int64_t t256 = (int64_t)((p.Sq + FLASH_V2_ROWS - 1) / FLASH_V2_ROWS) * p.H * batch;
@@ -505,6 +527,19 @@ void launch_flash(FlashParams p, int D, int batch, int flash_rows, hipStream_t s
   const bool v2_fits = 64 * std::max(p.k_tok, p.v_tok) * (int64_t)sizeof(half_t) < ((int64_t)1 << 31);
   if (flash_rows == 256 && !v2_fits)
     fail(ANIMA_E_INVALID_SHAPE, "256-row flash attention requires 64 key rows to span < 2 GiB");
+  if (p.kv_splits > 1) {
+    if (p.kv_splits != flash_kv_splits(p, D, batch, flash_rows) || !p.part_o || !p.part_ml)
+      fail(ANIMA_E_INVALID_ARGUMENT, "flash key splits do not match the shape");
+    p.nbatch = batch;
+    p.kv_chunk = ((p.Sk + p.kv_splits - 1) / p.kv_splits + 63) / 64 * 64;
+    p.q_tiles = (p.Sq + FLASH_V2_ROWS - 1) / FLASH_V2_ROWS;
+    const int64_t blocks = t256 * p.kv_splits;
+    if (blocks > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "attention grid too large");
+    launch_flash_v2(p, D, dim3((unsigned)blocks), stream);
+    launch_flash_combine(p, D, batch, stream);
+    return;
+  }
+  p.kv_splits = 0;
   const bool v2 = flash_rows == 256 || (flash_rows == 0 && v2_fits && t256 >= F2_MIN_BLOCKS);
   p.q_tiles = v2 ? (p.Sq + FLASH_V2_ROWS - 1) / FLASH_V2_ROWS : (p.Sq + FA_BM - 1) / FA_BM;
   const int64_t blocks = (int64_t)p.q_tiles * p.H * batch;

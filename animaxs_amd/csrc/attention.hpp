@@ -26,6 +26,15 @@ struct FlashParams {
   const half_t* q_norm_w;          // fused Q RMSNorm weight or null
   float eps;
   const float* rope;               // fused Q RoPE table or null
+  // Key splits (256-row kernel, non-causal, no key lengths): workgroup split s takes keys
+  // [s*kv_chunk, (s+1)*kv_chunk) and writes its unnormalised fp32 O rows to part_o
+  // ([split][batch][head][Sq][D]) and (running max in log2 units, row sum) to part_ml
+  // ([split][batch][head][Sq][2]); flash_combine_kernel merges them into o.
+  int kv_splits;                   // 0 or 1: no split
+  int nbatch;                      // batch count (partial row index)
+  int kv_chunk;                    // keys per split, a multiple of 64
+  float* part_o;
+  float* part_ml;
 };
 
 struct PrologueParams {
@@ -39,10 +48,15 @@ struct PrologueParams {
 };
 
 void launch_flash(FlashParams p, int D, int batch, int flash_rows, hipStream_t stream);
+// Key splits launch_flash will use for this shape (1: none); the caller provides
+// p.part_o / p.part_ml of flash_split_bytes() when it returns more than 1.
+int flash_kv_splits(const FlashParams& p, int D, int batch, int flash_rows);
+int64_t flash_split_bytes(const FlashParams& p, int D, int batch, int splits);
 
 // 256-row flash variant (attention_v2.hip); p.q_tiles counts 256-row tiles.
 constexpr int FLASH_V2_ROWS = 256;
 void launch_flash_v2(const FlashParams& p, int D, dim3 grid, hipStream_t stream);
+void launch_flash_combine(const FlashParams& p, int D, int batch, hipStream_t stream);
 void launch_generic(const FlashParams& p, int D, int batch, hipStream_t stream);
 void launch_prologue(const PrologueParams& p, hipStream_t stream);
 
@@ -51,13 +65,14 @@ class AttentionExecutor {
   AttentionExecutor(anima_ctx* ctx, const anima_attention_config& cfg);
   void encode(const anima_attention_args& a);
   int64_t maximum_score_scratch_bytes(int64_t key_count, int64_t query_count) const;
-  int64_t workspace_bytes() const { return ws_.capacity(); }
+  int64_t workspace_bytes() const { return ws_.capacity() + split_ws_.capacity(); }
   anima_ctx* context() const { return ctx_; }
 
  private:
   anima_ctx* ctx_;
   anima_attention_config cfg_;
   Workspace ws_;
+  Workspace split_ws_;   // key-split partial rows (fp32 O, max, row sum)
 };
 
 }  // namespace anima

@@ -211,6 +211,14 @@ void AttentionExecutor::encode(const anima_attention_args& a) {
     p.rope = rope_q;
   }
   if (use_flash) {
+    const int splits = flash_kv_splits(p, (int)D, (int)B, cfg_.flash_rows);
+    if (splits > 1) {
+      const int64_t part = flash_split_bytes(p, (int)D, (int)B, splits);
+      char* pw = static_cast<char*>(split_ws_.get(part, stream));
+      p.kv_splits = splits;
+      p.part_o = reinterpret_cast<float*>(pw);
+      p.part_ml = reinterpret_cast<float*>(pw + checked_product({(int64_t)splits, B, H, Sq, D, 4}, "attention"));
+    }
     launch_flash(p, (int)D, (int)B, cfg_.flash_rows, stream);
   } else {
     launch_generic(p, (int)D, (int)B, stream);

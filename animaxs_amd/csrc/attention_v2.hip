@@ -150,6 +150,11 @@ void flash_attention_v2_kernel(FlashParams p) {
   const int group = wave >> 2;
 
   int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  int split = 0;
+  if (p.kv_splits > 1) {
+    split = lb % p.kv_splits;
+    lb /= p.kv_splits;
+  }
   const int qt = lb % p.q_tiles;
   lb /= p.q_tiles;
   const int head = lb % p.H;
@@ -166,12 +171,16 @@ void flash_attention_v2_kernel(FlashParams p) {
   } else if (p.use_host_lengths) {
     kv_len = p.host_lengths[b];
   }
+  // With key splits (non-causal, no key lengths) this workgroup's keys start at kofs;
+  // kv_len and kend count keys from there.
+  const int kofs = p.kv_splits > 1 ? split * p.kv_chunk : 0;
+  if (p.kv_splits > 1) kv_len = max(0, min(kv_len, kofs + p.kv_chunk) - kofs);
   int kend = kv_len;
   if (p.causal) kend = min(kend, q0 + FLASH_V2_ROWS);
   const int ntiles = (kend + F2_BN - 1) / F2_BN;
 
-  const half_t* kbase = p.k + (int64_t)b * p.k_batch + (int64_t)kvh * p.k_head;
-  const half_t* vbase = p.v + (int64_t)b * p.v_batch + (int64_t)kvh * p.v_head;
+  const half_t* kbase = p.k + (int64_t)b * p.k_batch + (int64_t)kvh * p.k_head + (int64_t)kofs * p.k_tok;
+  const half_t* vbase = p.v + (int64_t)b * p.v_batch + (int64_t)kvh * p.v_head + (int64_t)kofs * p.v_tok;
 
   // Tile copies: thread t moves the 16-byte chunks t + F2_NT*r (r < CPT) of the K
   // tile and of the V tile (chunk -> row, column: 16-lane coalesced rows in
@@ -421,6 +430,20 @@ void flash_attention_v2_kernel(FlashParams p) {
   wait_vmcnt_imm<0>();            // loads of tiles past the end (no memory traffic)
 
   const float l_tot = xlane32_sum(lrow);
+  if (p.kv_splits > 1) {
+    if (qi < p.Sq) {
+      const int64_t row = (((int64_t)split * p.nbatch + b) * p.H + head) * p.Sq + qi;
+      float* po = p.part_o + row * D;
+#pragma unroll
+      for (int c = 0; c < OB; ++c)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4)
+          *reinterpret_cast<floatx4*>(po + 32 * c + 8 * e4 + 4 * hh) =
+              floatx4{acc[c][4 * e4], acc[c][4 * e4 + 1], acc[c][4 * e4 + 2], acc[c][4 * e4 + 3]};
+      if (hh == 0) *reinterpret_cast<float2*>(p.part_ml + row * 2) = make_float2(m_run, l_tot);
+    }
+    return;
+  }
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (qi < p.Sq) {
     half_t* op = p.o + (int64_t)b * p.o_batch + (int64_t)head * p.o_head + (int64_t)qi * p.o_tok;
@@ -433,6 +456,53 @@ void flash_attention_v2_kernel(FlashParams p) {
         *reinterpret_cast<half4v*>(op + 32 * c + 8 * e4 + 4 * hh) = val;
       }
   }
+}
+
+// Merge of the key splits: O = sum_s w_s O_s / sum_s w_s l_s with w_s = 2^(m_s - max m).
+// Thread t of a row handles columns 8t .. 8t+7.
+template <int D>
+__global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p, int64_t rows) {
+  constexpr int TPR = D / 8;
+  const int64_t row = (int64_t)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
+  const int t = threadIdx.x % TPR;
+  if (row >= rows) return;
+  const int qi = (int)(row % p.Sq);
+  const int head = (int)((row / p.Sq) % p.H);
+  const int b = (int)(row / ((int64_t)p.Sq * p.H));
+  float mmax = -INFINITY;
+  for (int s = 0; s < p.kv_splits; ++s) mmax = fmaxf(mmax, p.part_ml[(s * rows + row) * 2]);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float l = 0.f;
+  for (int s = 0; s < p.kv_splits; ++s) {
+    const float ms = p.part_ml[(s * rows + row) * 2];
+    const float w = ms == -INFINITY ? 0.f : fast_exp2(ms - mmax);
+    l = fmaf(w, p.part_ml[(s * rows + row) * 2 + 1], l);
+    const float* po = p.part_o + (s * rows + row) * D + 8 * t;
+    const floatx4 a = *reinterpret_cast<const floatx4*>(po), c = *reinterpret_cast<const floatx4*>(po + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[e] = fmaf(w, a[e], acc[e]);
+      acc[4 + e] = fmaf(w, c[e], acc[4 + e]);
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  half8v o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (half_t)(acc[e] * inv);
+  half_t* op = p.o + (int64_t)b * p.o_batch + (int64_t)head * p.o_head + (int64_t)qi * p.o_tok + 8 * t;
+  *reinterpret_cast<half8v*>(op) = o;
+}
+
+void launch_flash_combine(const FlashParams& p, int D, int batch, hipStream_t stream) {
+  const int64_t rows = (int64_t)batch * p.H * p.Sq;
+  const int rpb = 256 / (D / 8);
+  const int64_t blocks = (rows + rpb - 1) / rpb;
+  if (blocks > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "attention combine grid too large");
+  if (D == 128)
+    hipLaunchKernelGGL(flash_combine_kernel<128>, dim3((unsigned)blocks), dim3(256), 0, stream, p, rows);
+  else
+    hipLaunchKernelGGL(flash_combine_kernel<64>, dim3((unsigned)blocks), dim3(256), 0, stream, p, rows);
+  ANIMA_HIP(hipGetLastError());
 }
 
 void launch_flash_v2(const FlashParams& p, int D, dim3 grid, hipStream_t stream) {

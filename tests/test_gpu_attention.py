@@ -193,12 +193,31 @@ def test_flash_matches_oracle_ragged(ctx, D, Sq, Sk, causal):
     k = torch.randn(1, H, Sk, D, generator=g).half()
     v = torch.randn(1, H, Sk, D, generator=g).half()
     outs = {}
-    for name, backend, rows in (("flash128", "flash", 128), ("flash256", "flash", 256), ("generic", "generic", 0)):
+    for name, backend, rows in (("flash128", "flash", 128), ("flash256", "flash", 256), ("flashauto", "flash", 0),
+                                ("generic", "generic", 0)):
         outs[name] = _run(ctx, dev(q), dev(k), dev(v), layout="headMajor", heads=H, Sq=Sq, Sk=Sk, D=D,
                           out_shape=(1, H, Sq, D), backend=backend, flash_rows=rows, causal=causal)
     ref = oatt.sdpa(q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3), causal=causal)
     for name, o in outs.items():
         assert_attention_close(o.permute(0, 2, 1, 3), ref, label=f"{name} D{D} Sq{Sq} Sk{Sk} causal={causal}")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("B,Sq,Sk", [(2, 300, 2056), (1, 1024, 1024), (3, 64, 520), (1, 1, 4096)])
+def test_flash_key_splits(ctx, D, B, Sq, Sk):
+    """Short query sequences over long key sequences: the 256-row kernel splits the keys across
+    workgroups (last split possibly empty for Sk=2056 with 8 splits) and a second kernel merges the
+    fp32 partial rows; token-major layout, batch > 1."""
+    g = torch.Generator().manual_seed(B * Sq + Sk + D)
+    H = 4
+    q = torch.randn(B, Sq, H, D, generator=g).half()
+    k = torch.randn(B, Sk, H, D, generator=g).half()
+    v = torch.randn(B, Sk, H, D, generator=g).half()
+    print(f"SPLITS D={D} B={B} Sq={Sq} Sk={Sk}", flush=True)
+    o = _run(ctx, dev(q), dev(k), dev(v), layout=("tokenMajor", H * D), heads=H, Sq=Sq, Sk=Sk, D=D,
+             out_shape=(B, Sq, H, D), batch=B)
+    ref = oatt.sdpa(q, k, v)
+    assert_attention_close(o, ref, label=f"splits D{D} B{B} Sq{Sq} Sk{Sk}")
 
 
 @pytest.mark.parametrize("flash_rows", [128, 256])
