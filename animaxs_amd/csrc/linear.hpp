@@ -21,6 +21,11 @@ struct GemmParams {
   int epilogue;
   float* residual;        // [M, N] fp32, GEMM_GATE_ADD
   const float* gate;      // [N] fp32, GEMM_GATE_ADD
+  // Split K (ping-pong kernel, GEMM_STORE, single problem): ksplit workgroups per
+  // tile each sum K / ksplit and write fp32 rows to part [ksplit][M][N]; a second
+  // kernel adds them in split order and rounds once.
+  int ksplit;
+  float* part;
 };
 
 enum GemmEpilogue { GEMM_STORE = 0, GEMM_GELU = 1, GEMM_GATE_ADD = 2 };
@@ -105,6 +110,10 @@ void launch_gemm(const GemmParams& p, int storage, hipStream_t stream);
 // and weight rows, buffers below 2 GiB.  launch_gemm routes to it when it applies.
 bool pingpong_supported(const GemmParams& p, int storage);
 void launch_pingpong(const GemmParams& p, int storage, hipStream_t stream);
+// K splits the ping-pong kernel uses for this plain GEMM (1: none): when its tiles
+// fill less than half the chip, as many splits of >= 16 K blocks as keep the grid
+// within 256 workgroups (shorter splits lose more to the partial rows than they gain).
+int pingpong_ksplit(const GemmParams& p, int storage);
 // count (1..PG_GROUP) ping-pong GEMMs sharing K and storage in one launch.
 void launch_pingpong_group(const GemmParams* ps, int count, int storage, hipStream_t stream);
 

@@ -104,10 +104,16 @@ void LinearExecutor::encode(anima_buffer input, int64_t input_offset, const anim
     launch_gemm(p, ANIMA_STORAGE_FP16, stream);
     return;
   }
-  if (smallm_supported(p, w.storage))
+  if (smallm_supported(p, w.storage)) {
     launch_smallm(p, w.storage, stream);
-  else
-    launch_gemm(p, w.storage, stream);
+    return;
+  }
+  const int ks = pingpong_ksplit(p, w.storage);
+  if (ks > 1) {
+    p.ksplit = ks;
+    p.part = static_cast<float*>(ws_.get(checked_product({(int64_t)ks, p.M, p.N, 4}, "LinearExecutor"), stream));
+  }
+  launch_gemm(p, w.storage, stream);
 }
 
 void LinearExecutor::encode_group(anima_buffer input, const anima_qweight* const* weights, const anima_buffer* outputs,
@@ -122,8 +128,9 @@ void LinearExecutor::encode_group(anima_buffer input, const anima_qweight* const
   for (int i = 0; i < count; ++i) {
     const QWeightView w = validate_weight(*weights[i], "LinearExecutor");
     ps[i] = prepare(input, 0, w, outputs[i], 0, input_rows);
+    // A weight encode() would split over K runs on its own, so the bits match encode().
     together = together && !smallm_supported(ps[i], w.storage) && pingpong_supported(ps[i], w.storage) &&
-               (i == 0 || (w.storage == storage && ps[i].K == ps[0].K));
+               pingpong_ksplit(ps[i], w.storage) == 1 && (i == 0 || (w.storage == storage && ps[i].K == ps[0].K));
     storage = w.storage;
   }
   if (!together) {
@@ -144,7 +151,8 @@ bool LinearExecutor::encode_fused(anima_buffer input, int64_t input_offset, cons
     fail(ANIMA_E_INVALID_SHAPE, "invalid LinearExecutor shape or offset");
   const QWeightView w = validate_weight(weight, "LinearExecutor");
   GemmParams p = prepare(input, input_offset, w, output, output_offset, input_rows);
-  if (cfg_.backend != ANIMA_LINEAR_BACKEND_AUTO || smallm_supported(p, w.storage) || !pingpong_supported(p, w.storage))
+  if (cfg_.backend != ANIMA_LINEAR_BACKEND_AUTO || smallm_supported(p, w.storage) || !pingpong_supported(p, w.storage) ||
+      pingpong_ksplit(p, w.storage) > 1)
     return false;
   p.epilogue = epilogue;
   p.residual = residual;

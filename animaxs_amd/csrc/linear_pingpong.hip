@@ -96,9 +96,14 @@ void pingpong_gemm_kernel(GemmGroup gp) {
   const int vec_store = gp.vec[pi];
   const int ntn = (p.N + PG_BN - 1) / PG_BN;
   const int lb = lbg - gp.first_tile[pi];
-  const int tn = lb % ntn, tm = lb / ntn;
+  // Split K: workgroup lb takes K-block range `split` of tile lb / ksplit.
+  const int ks = p.ksplit > 1 ? p.ksplit : 1;
+  const int split = lb % ks;
+  const int lt = lb / ks;
+  const int tn = lt % ntn, tm = lt / ntn;
   const int m0 = tm * PG_BM, n0 = tn * PG_BN;
-  const int nk = p.K / PG_BK;
+  const int nk = p.K / PG_BK / ks;
+  const int kbeg = split * nk;
   // Group 0 takes K blocks [0, half), group 1 [half, nk); with windows, half is a
   // multiple of the window so every window is aligned.
   int half = SWIN ? PG_WIN * ((nk + 2 * PG_WIN - 1) / (2 * PG_WIN)) : (nk + 1) / 2;
@@ -107,13 +112,14 @@ void pingpong_gemm_kernel(GemmGroup gp) {
   const int nown = group == 0 ? half : nk - half;
 
   // Tile-relative buffers (sizes fit in 31 bits; checked on the host).
-  const half_t* xb = p.x + (int64_t)m0 * p.K;
-  const int xbytes = (p.M - m0) * p.K * 2;
-  const uint8_t* wb = p.w + (int64_t)n0 * p.row_stride;
-  const int wbytes = (int)((int64_t)(p.N - n0) * p.row_stride);
-  const half_t* sb = p.scale + (int64_t)n0 * p.groups;
-  const half_t* zb = p.zero + (int64_t)n0 * p.groups;
-  const int sbytes = (p.N - n0) * p.groups * 2;
+  // With split K they start at the split's first K block; the sizes end where they did.
+  const half_t* xb = p.x + (int64_t)m0 * p.K + kbeg * PG_BK;
+  const int xbytes = (p.M - m0) * p.K * 2 - kbeg * PG_BK * 2;
+  const uint8_t* wb = p.w + (int64_t)n0 * p.row_stride + kbeg * 32 * WCH;
+  const int wbytes = (int)((int64_t)(p.N - n0) * p.row_stride) - kbeg * 32 * WCH;
+  const half_t* sb = p.scale + (int64_t)n0 * p.groups + kbeg;
+  const half_t* zb = p.zero + (int64_t)n0 * p.groups + kbeg;
+  const int sbytes = (p.N - n0) * p.groups * 2 - kbeg * 2;
 
   // X copies: thread t of a group moves chunks t + 256r (r < 4) of its group's
   // block: row t/8 + 32r, 16-byte column t%8 (8 lanes read one 128-byte row).
@@ -397,6 +403,33 @@ void pingpong_gemm_kernel(GemmGroup gp) {
           *reinterpret_cast<floatx4*>(own + (((t * 2 + j) * 4 + q) * 64 + lane) * 16) = v;
         }
     barrier();
+    if (p.ksplit > 1) {
+      // Split K: the fp32 sums of this K range go to the split's partial rows.
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int m = m0 + 32 * (MINE + j) + c32;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const floatx4 o = *reinterpret_cast<const floatx4*>(partner + (((t * 2 + j) * 4 + q) * 64 + lane) * 16);
+            const floatx4 sv = {acc[t][MINE + j][4 * q] + o[0], acc[t][MINE + j][4 * q + 1] + o[1],
+                                acc[t][MINE + j][4 * q + 2] + o[2], acc[t][MINE + j][4 * q + 3] + o[3]};
+            const int n = n0 + 64 * wg + 32 * t + 8 * q + 4 * hh;
+            if (m < p.M) {
+              float* prow = p.part + ((int64_t)split * p.M + m) * p.N;
+              if ((p.N & 3) == 0 && n + 3 < p.N) {
+                *reinterpret_cast<floatx4*>(prow + n) = sv;
+              } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  if (n + e < p.N) prow[n + e] = sv[e];
+              }
+            }
+          }
+        }
+      return;
+    }
     half4v out[2][2][4];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -424,6 +457,7 @@ void pingpong_gemm_kernel(GemmGroup gp) {
     finish(std::integral_constant<int, 0>{});
   else
     finish(std::integral_constant<int, 2>{});
+  if (p.ksplit > 1) return;   // partial rows written; splitk_reduce_kernel finishes
   barrier();
 
   // Output stage: thread tid takes 16-byte chunk tid % 32 of tile rows tid / 32 + 16i.
@@ -489,6 +523,38 @@ bool pingpong_supported(const GemmParams& p, int storage) {
   return (int64_t)p.M * p.K * 2 <= lim && (int64_t)p.N * p.row_stride <= lim && (int64_t)p.N * p.groups * 2 <= lim;
 }
 
+// Sum of the K splits in a fixed order, rounded once to fp16: y = half(sum_s part[s]).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, half_t* __restrict__ y,
+                                                            int64_t count, int ksplit, int vec) {
+  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i0 >= count) return;
+  if (vec && i0 + 4 <= count) {
+    floatx4 acc = *reinterpret_cast<const floatx4*>(part + i0);
+    for (int s = 1; s < ksplit; ++s) acc += *reinterpret_cast<const floatx4*>(part + s * count + i0);
+    *reinterpret_cast<half4v*>(y + i0) = half4v{(half_t)acc[0], (half_t)acc[1], (half_t)acc[2], (half_t)acc[3]};
+  } else {
+    for (int64_t i = i0; i < count && i < i0 + 4; ++i) {
+      float acc = part[i];
+      for (int s = 1; s < ksplit; ++s) acc += part[s * count + i];
+      y[i] = (half_t)acc;
+    }
+  }
+}
+
+int pingpong_ksplit(const GemmParams& p, int storage) {
+  if (!pingpong_supported(p, storage) || p.epilogue != GEMM_STORE) return 1;
+  const int64_t tiles = (int64_t)((p.M + PG_BM - 1) / PG_BM) * ((p.N + PG_BN - 1) / PG_BN);
+  if (tiles >= 128) return 1;
+  const int nk = p.K / PG_BK;
+  const bool swin = p.groups % PG_WIN == 0 && aligned16(p.scale) && aligned16(p.zero);
+  int best = 1;
+  for (int k = 2; k <= 8; ++k) {
+    if (nk % k != 0 || nk / k < 16 || (swin && (nk / k) % PG_WIN != 0) || tiles * k > 256) continue;
+    best = k;
+  }
+  return best;
+}
+
 void launch_pingpong_group(const GemmParams* ps, int count, int storage, hipStream_t stream) {
   if (count < 1 || count > PG_GROUP) fail(ANIMA_E_INVALID_ARGUMENT, "ping-pong GEMM group holds 1 to 3 problems");
   GemmGroup g{};
@@ -501,12 +567,16 @@ void launch_pingpong_group(const GemmParams* ps, int count, int storage, hipStre
     if (p.epilogue == GEMM_GATE_ADD && (!p.residual || !p.gate))
       fail(ANIMA_E_INVALID_ARGUMENT, "GEMM gate-add epilogue needs residual and gate");
     swin = swin && p.groups % PG_WIN == 0 && aligned16(p.scale) && aligned16(p.zero);
+    if (p.ksplit > 1) {
+      if (count != 1 || p.epilogue != GEMM_STORE || !p.part || p.ksplit != pingpong_ksplit(p, storage))
+        fail(ANIMA_E_INVALID_ARGUMENT, "ping-pong GEMM: split K needs a single plain GEMM and its partial buffer");
+    }
     g.p[i] = p;
     g.first_tile[i] = (int)tiles;
     // 16-byte output accesses: every row start 16-byte aligned.
     g.vec[i] = p.epilogue == GEMM_GATE_ADD ? (aligned16(p.residual) && aligned16(p.gate) && p.N % 8 == 0 ? 1 : 0)
                                            : (aligned16(p.y) && p.N % 8 == 0 ? 1 : 0);
-    tiles += (int64_t)((p.M + PG_BM - 1) / PG_BM) * ((p.N + PG_BN - 1) / PG_BN);
+    tiles += (int64_t)((p.M + PG_BM - 1) / PG_BM) * ((p.N + PG_BN - 1) / PG_BN) * (p.ksplit > 1 ? p.ksplit : 1);
     if (tiles > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "GEMM grid too large");
   }
   for (int i = count; i < PG_GROUP; ++i) g.first_tile[i] = (int)tiles;
@@ -525,6 +595,14 @@ void launch_pingpong_group(const GemmParams* ps, int count, int storage, hipStre
       hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W8, false>), grid, block, 0, stream, g);
   }
   ANIMA_HIP(hipGetLastError());
+  if (count == 1 && ps[0].ksplit > 1) {
+    const GemmParams& p = ps[0];
+    const int64_t n = (int64_t)p.M * p.N;
+    const int vec = aligned8(p.y) ? 1 : 0;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, stream, p.part, p.y, n,
+                       p.ksplit, vec);
+    ANIMA_HIP(hipGetLastError());
+  }
 }
 
 void launch_pingpong(const GemmParams& p, int storage, hipStream_t stream) {
