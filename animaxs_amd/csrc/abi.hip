@@ -140,19 +140,24 @@ anima_status anima_linear_encode_epilogue(anima_linear* lin, anima_buffer input,
   return guarded([&] {
     require(lin, "linear");
     const anima_qweight& w = *require(weight, "weight");
-    if (epilogue != ANIMA_LINEAR_EPILOGUE_GELU && epilogue != ANIMA_LINEAR_EPILOGUE_GATE_ADD)
+    if (epilogue != ANIMA_LINEAR_EPILOGUE_GELU && epilogue != ANIMA_LINEAR_EPILOGUE_GATE_ADD &&
+        epilogue != ANIMA_LINEAR_EPILOGUE_RESIDUAL_ADD)
       fail(ANIMA_E_INVALID_ARGUMENT, "unknown linear epilogue");
     float* res = nullptr;
     const float* gt = nullptr;
-    if (epilogue == ANIMA_LINEAR_EPILOGUE_GATE_ADD) {
+    if (epilogue != ANIMA_LINEAR_EPILOGUE_GELU) {
       if (!(input_rows > 0 && w.rows > 0)) fail(ANIMA_E_INVALID_SHAPE, "invalid LinearExecutor shape or offset");
       check_elementwise(residual, checked_product({input_rows, w.rows}, "linear epilogue"), 4, "linear residual");
-      check_elementwise(gate, w.rows, 4, "linear gate");
       res = static_cast<float*>(residual.ptr);
+    }
+    if (epilogue == ANIMA_LINEAR_EPILOGUE_GATE_ADD) {
+      check_elementwise(gate, w.rows, 4, "linear gate");
       gt = static_cast<const float*>(gate.ptr);
     }
-    encode_linear_epilogue(lin->impl, input, input_offset, w, output, output_offset, input_rows, family,
-                           epilogue == ANIMA_LINEAR_EPILOGUE_GELU ? GEMM_GELU : GEMM_GATE_ADD, res, gt);
+    const int epi = epilogue == ANIMA_LINEAR_EPILOGUE_GELU       ? GEMM_GELU
+                    : epilogue == ANIMA_LINEAR_EPILOGUE_GATE_ADD ? GEMM_GATE_ADD
+                                                                 : GEMM_RESIDUAL_ADD;
+    encode_linear_epilogue(lin->impl, input, input_offset, w, output, output_offset, input_rows, family, epi, res, gt);
   });
 }
 

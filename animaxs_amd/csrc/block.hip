@@ -438,6 +438,8 @@ void encode_linear_epilogue(LinearExecutor& lin, anima_buffer input, int64_t inp
   const int64_t count = input_rows * weight.rows;  // bounded by the output range encode() checked
   if (epilogue == GEMM_GELU)
     launch_gelu(y, count, lin.context()->stream);
+  else if (epilogue == GEMM_RESIDUAL_ADD)
+    launch_add_half(residual, y, count, lin.context()->stream);
   else
     launch_gate_add(residual, y, gate, weight.rows, count, lin.context()->stream);
 }
@@ -621,8 +623,8 @@ void QwenLayerExecutor::encode(const anima_qwen_layer_weights& w, const anima_qw
   att.causal = 1; att.layout = ANIMA_LAYOUT_TOKEN_MAJOR; att.token_stride = qdim; att.kv_token_stride = kvdim;
   att.batch = B; att.key_lengths = a.key_lengths; att.key_lengths_on_device = 0; att.prologue = &pro;
   attention_.encode(att);
-  linear_.encode(att_b, 0, w.o, proj_b, 0, rows, ANIMA_FAMILY_ATTENTION_PROJECTION);
-  launch_add_half(residual, static_cast<const half_t*>(proj_b.ptr), rows * hidden, stream);
+  encode_linear_epilogue(linear_, att_b, 0, w.o, proj_b, 0, rows, ANIMA_FAMILY_ATTENTION_PROJECTION, GEMM_RESIDUAL_ADD,
+                         residual, nullptr);
 
   // MLP branch (:284-302): gate/up -> SwiGLU (into the gate buffer) -> down.
   launch_rmsnorm_half(residual, static_cast<const half_t*>(w.post_attention_norm), norm, hidden, rows, a.eps, stream);
@@ -633,8 +635,8 @@ void QwenLayerExecutor::encode(const anima_qwen_layer_weights& w, const anima_qw
   }
   launch_gated_silu(static_cast<const half_t*>(gate_b.ptr), static_cast<const half_t*>(up_b.ptr),
                     static_cast<half_t*>(gate_b.ptr), rows * inter, stream);
-  linear_.encode(gate_b, 0, w.down, proj_b, 0, rows, ANIMA_FAMILY_MLP_DOWN);
-  launch_add_half(residual, static_cast<const half_t*>(proj_b.ptr), rows * hidden, stream);
+  encode_linear_epilogue(linear_, gate_b, 0, w.down, proj_b, 0, rows, ANIMA_FAMILY_MLP_DOWN, GEMM_RESIDUAL_ADD,
+                         residual, nullptr);
 }
 
 }  // namespace anima

@@ -18,17 +18,19 @@ struct GemmParams {
   //   GEMM_GELU      y = half(gelu_erf(half(acc)))   (dit_gelu_half_inplace fused)
   //   GEMM_GATE_ADD  residual[m, n] += float(half(acc)) * gate[n]; y is not written
   //                  (gate_add_half_f32 fused)
+  //   GEMM_RESIDUAL_ADD  residual[m, n] += float(half(acc)); y is not written
+  //                  (add_half_into_float fused)
   int epilogue;
-  float* residual;        // [M, N] fp32, GEMM_GATE_ADD
+  float* residual;        // [M, N] fp32, GEMM_GATE_ADD / GEMM_RESIDUAL_ADD
   const float* gate;      // [N] fp32, GEMM_GATE_ADD
-  // Split K (ping-pong kernel, GEMM_STORE, single problem): ksplit workgroups per
+  // Split K (ping-pong kernel, GEMM_STORE or GEMM_RESIDUAL_ADD, single problem): ksplit workgroups per
   // tile each sum K / ksplit and write fp32 rows to part [ksplit][M][N]; a second
   // kernel adds them in split order and rounds once.
   int ksplit;
   float* part;
 };
 
-enum GemmEpilogue { GEMM_STORE = 0, GEMM_GELU = 1, GEMM_GATE_ADD = 2 };
+enum GemmEpilogue { GEMM_STORE = 0, GEMM_GELU = 1, GEMM_GATE_ADD = 2, GEMM_RESIDUAL_ADD = 3 };
 
 // Up to PG_GROUP independent GEMMs of one K and storage in one ping-pong launch
 // (the Q/K/V projections of one input): logical tiles [first_tile[i],

@@ -146,18 +146,25 @@ bool LinearExecutor::encode_fused(anima_buffer input, int64_t input_offset, cons
                                   int epilogue, float* residual, const float* gate) {
   if (family < ANIMA_FAMILY_OTHER || family > ANIMA_FAMILY_MLP_DOWN)
     fail(ANIMA_E_INVALID_ARGUMENT, "unknown linear family");
-  if (epilogue != GEMM_GELU && epilogue != GEMM_GATE_ADD) fail(ANIMA_E_INVALID_ARGUMENT, "unknown linear epilogue");
+  if (epilogue != GEMM_GELU && epilogue != GEMM_GATE_ADD && epilogue != GEMM_RESIDUAL_ADD)
+    fail(ANIMA_E_INVALID_ARGUMENT, "unknown linear epilogue");
   if (!(input_rows > 0 && input_offset >= 0 && output_offset >= 0))
     fail(ANIMA_E_INVALID_SHAPE, "invalid LinearExecutor shape or offset");
   const QWeightView w = validate_weight(weight, "LinearExecutor");
   GemmParams p = prepare(input, input_offset, w, output, output_offset, input_rows);
-  if (cfg_.backend != ANIMA_LINEAR_BACKEND_AUTO || smallm_supported(p, w.storage) || !pingpong_supported(p, w.storage) ||
-      pingpong_ksplit(p, w.storage) > 1)
+  if (cfg_.backend != ANIMA_LINEAR_BACKEND_AUTO || smallm_supported(p, w.storage) || !pingpong_supported(p, w.storage))
     return false;
+  // The split decision is the one encode() makes, so the bits match encode() + the step.
+  const int ks = pingpong_ksplit(p, w.storage);
+  if (ks > 1 && epilogue != GEMM_RESIDUAL_ADD) return false;
   p.epilogue = epilogue;
   p.residual = residual;
   p.gate = gate;
   DeviceGuard guard(ctx_);
+  if (ks > 1) {
+    p.ksplit = ks;
+    p.part = static_cast<float*>(ws_.get(checked_product({(int64_t)ks, p.M, p.N, 4}, "LinearExecutor"), ctx_->stream));
+  }
   launch_pingpong(p, w.storage, ctx_->stream);
   return true;
 }

@@ -475,7 +475,24 @@ void pingpong_gemm_kernel(GemmGroup gp) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = gelu_erf_half(v[e]);
       }
-      if (EPI == GEMM_GATE_ADD) {
+      if (EPI == GEMM_RESIDUAL_ADD) {
+        float* rrow = p.residual + (int64_t)m * p.N;
+        if (vec_store && n + 8 <= p.N) {
+          floatx4 r0 = *reinterpret_cast<const floatx4*>(rrow + n);
+          floatx4 r1 = *reinterpret_cast<const floatx4*>(rrow + n + 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            r0[e] += (float)v[e];
+            r1[e] += (float)v[4 + e];
+          }
+          *reinterpret_cast<floatx4*>(rrow + n) = r0;
+          *reinterpret_cast<floatx4*>(rrow + n + 4) = r1;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (n + e < p.N) rrow[n + e] += (float)v[e];
+        }
+      } else if (EPI == GEMM_GATE_ADD) {
         float* rrow = p.residual + (int64_t)m * p.N;
         if (vec_store && n + 8 <= p.N) {
           floatx4 r0 = *reinterpret_cast<const floatx4*>(rrow + n);
@@ -510,6 +527,8 @@ void pingpong_gemm_kernel(GemmGroup gp) {
     store_tile(std::integral_constant<int, GEMM_GELU>{});
   else if (p.epilogue == GEMM_GATE_ADD)
     store_tile(std::integral_constant<int, GEMM_GATE_ADD>{});
+  else if (p.epilogue == GEMM_RESIDUAL_ADD)
+    store_tile(std::integral_constant<int, GEMM_RESIDUAL_ADD>{});
   else
     store_tile(std::integral_constant<int, GEMM_STORE>{});
 }
@@ -523,26 +542,39 @@ bool pingpong_supported(const GemmParams& p, int storage) {
   return (int64_t)p.M * p.K * 2 <= lim && (int64_t)p.N * p.row_stride <= lim && (int64_t)p.N * p.groups * 2 <= lim;
 }
 
-// Sum of the K splits in a fixed order, rounded once to fp16: y = half(sum_s part[s]).
+// Sum of the K splits in a fixed order, rounded once to fp16: y = half(sum_s part[s]),
+// or residual += float(half(sum_s part[s])) when residual is given.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, half_t* __restrict__ y,
-                                                            int64_t count, int ksplit, int vec) {
+                                                            float* __restrict__ residual, int64_t count, int ksplit,
+                                                            int vec) {
   const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i0 >= count) return;
   if (vec && i0 + 4 <= count) {
     floatx4 acc = *reinterpret_cast<const floatx4*>(part + i0);
     for (int s = 1; s < ksplit; ++s) acc += *reinterpret_cast<const floatx4*>(part + s * count + i0);
-    *reinterpret_cast<half4v*>(y + i0) = half4v{(half_t)acc[0], (half_t)acc[1], (half_t)acc[2], (half_t)acc[3]};
+    const half4v h = {(half_t)acc[0], (half_t)acc[1], (half_t)acc[2], (half_t)acc[3]};
+    if (residual) {
+      floatx4 r = *reinterpret_cast<const floatx4*>(residual + i0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] += (float)h[e];
+      *reinterpret_cast<floatx4*>(residual + i0) = r;
+    } else {
+      *reinterpret_cast<half4v*>(y + i0) = h;
+    }
   } else {
     for (int64_t i = i0; i < count && i < i0 + 4; ++i) {
       float acc = part[i];
       for (int s = 1; s < ksplit; ++s) acc += part[s * count + i];
-      y[i] = (half_t)acc;
+      if (residual)
+        residual[i] += (float)(half_t)acc;
+      else
+        y[i] = (half_t)acc;
     }
   }
 }
 
 int pingpong_ksplit(const GemmParams& p, int storage) {
-  if (!pingpong_supported(p, storage) || p.epilogue != GEMM_STORE) return 1;
+  if (!pingpong_supported(p, storage) || (p.epilogue != GEMM_STORE && p.epilogue != GEMM_RESIDUAL_ADD)) return 1;
   const int64_t tiles = (int64_t)((p.M + PG_BM - 1) / PG_BM) * ((p.N + PG_BN - 1) / PG_BN);
   if (tiles >= 128) return 1;
   const int nk = p.K / PG_BK;
@@ -566,16 +598,19 @@ void launch_pingpong_group(const GemmParams* ps, int count, int storage, hipStre
     if (p.K != ps[0].K) fail(ANIMA_E_INVALID_SHAPE, "ping-pong GEMM group: problems must share K");
     if (p.epilogue == GEMM_GATE_ADD && (!p.residual || !p.gate))
       fail(ANIMA_E_INVALID_ARGUMENT, "GEMM gate-add epilogue needs residual and gate");
+    if (p.epilogue == GEMM_RESIDUAL_ADD && !p.residual)
+      fail(ANIMA_E_INVALID_ARGUMENT, "GEMM residual-add epilogue needs the residual");
     swin = swin && p.groups % PG_WIN == 0 && aligned16(p.scale) && aligned16(p.zero);
     if (p.ksplit > 1) {
-      if (count != 1 || p.epilogue != GEMM_STORE || !p.part || p.ksplit != pingpong_ksplit(p, storage))
+      if (count != 1 || !p.part || p.ksplit != pingpong_ksplit(p, storage))
         fail(ANIMA_E_INVALID_ARGUMENT, "ping-pong GEMM: split K needs a single plain GEMM and its partial buffer");
     }
     g.p[i] = p;
     g.first_tile[i] = (int)tiles;
     // 16-byte output accesses: every row start 16-byte aligned.
-    g.vec[i] = p.epilogue == GEMM_GATE_ADD ? (aligned16(p.residual) && aligned16(p.gate) && p.N % 8 == 0 ? 1 : 0)
-                                           : (aligned16(p.y) && p.N % 8 == 0 ? 1 : 0);
+    g.vec[i] = p.epilogue == GEMM_GATE_ADD       ? (aligned16(p.residual) && aligned16(p.gate) && p.N % 8 == 0 ? 1 : 0)
+               : p.epilogue == GEMM_RESIDUAL_ADD ? (aligned16(p.residual) && p.N % 8 == 0 ? 1 : 0)
+                                                 : (aligned16(p.y) && p.N % 8 == 0 ? 1 : 0);
     tiles += (int64_t)((p.M + PG_BM - 1) / PG_BM) * ((p.N + PG_BN - 1) / PG_BN) * (p.ksplit > 1 ? p.ksplit : 1);
     if (tiles > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "GEMM grid too large");
   }
@@ -598,9 +633,10 @@ void launch_pingpong_group(const GemmParams* ps, int count, int storage, hipStre
   if (count == 1 && ps[0].ksplit > 1) {
     const GemmParams& p = ps[0];
     const int64_t n = (int64_t)p.M * p.N;
-    const int vec = aligned8(p.y) ? 1 : 0;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, stream, p.part, p.y, n,
-                       p.ksplit, vec);
+    float* res = p.epilogue == GEMM_RESIDUAL_ADD ? p.residual : nullptr;
+    const int vec = (res ? aligned16(res) : aligned8(p.y)) ? 1 : 0;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, stream, p.part, p.y, res,
+                       n, p.ksplit, vec);
     ANIMA_HIP(hipGetLastError());
   }
 }

@@ -220,7 +220,7 @@ class QuantizedLinearWeightBuffers:
 
 
 _LBACK = {"auto": _abi.LINEAR_AUTO, "fused": _abi.LINEAR_FUSED, "dequantizedGEMM": _abi.LINEAR_DEQUANT_THEN_GEMM}
-_EPILOGUE = {"gelu": 1, "gate_add": 2}
+_EPILOGUE = {"gelu": 1, "gate_add": 2, "residual_add": 3}
 _FAMILY = {"other": _abi.FAMILY_OTHER, "attentionProjection": _abi.FAMILY_ATTENTION_PROJECTION,
            "mlpUp": _abi.FAMILY_MLP_UP, "mlpDown": _abi.FAMILY_MLP_DOWN}
 

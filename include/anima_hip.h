@@ -257,13 +257,17 @@ anima_status anima_linear_execute(anima_linear* lin, anima_buffer input, int64_t
  *                                   (residual fp32 [input_rows, weight.rows], gate fp32
  *                                   [weight.rows]); output is scratch the call may
  *                                   leave unwritten.
+ *   ANIMA_LINEAR_EPILOGUE_RESIDUAL_ADD: residual[r, n] += float(linear(input)[r, n]) (the
+ *                                   Qwen layer's add_half_into_float, QwenEncoderMetal.swift:
+ *                                   280-302); gate is ignored, output as above.
  * Results equal anima_linear_encode followed by anima_gelu_half_inplace_encode /
- * anima_gate_add_half_f32_encode bit for bit: the tiled GEMM applies the step in
+ * anima_gate_add_half_f32_encode / anima_add_half_into_float_encode bit for bit: the tiled GEMM applies the step in
  * its output stage when it takes the shape, otherwise the two kernels run in turn.
  * residual and gate are ignored for ANIMA_LINEAR_EPILOGUE_GELU. */
 typedef enum anima_linear_epilogue {
   ANIMA_LINEAR_EPILOGUE_GELU = 1,
-  ANIMA_LINEAR_EPILOGUE_GATE_ADD = 2
+  ANIMA_LINEAR_EPILOGUE_GATE_ADD = 2,
+  ANIMA_LINEAR_EPILOGUE_RESIDUAL_ADD = 3
 } anima_linear_epilogue;
 anima_status anima_linear_encode_epilogue(anima_linear* lin, anima_buffer input, int64_t input_offset,
                                           const anima_qweight* weight, anima_buffer output,

@@ -408,7 +408,7 @@ def test_linear_epilogues_equal_two_step(ctx, storage, M, N, K):
     """anima_linear_encode_epilogue: the tiled GEMM's fused GELU / gate-add output stage (M > 64,
     W4/W8, K a multiple of 64; N % 4 != 0 takes its element-wise stores) and the two-kernel
     fallback (small M, fp16 storage, K not a multiple of 64) give the same bits as the linear
-    followed by dit_gelu_half_inplace / gate_add_half_f32."""
+    followed by dit_gelu_half_inplace / gate_add_half_f32 / add_half_into_float."""
     from animaxs_amd import BlockOps
     w = _affine_weight(storage, N, K, seed=7 * M + N + K + storage)
     qw, keep = device_weight(w)
@@ -431,9 +431,15 @@ def test_linear_epilogues_equal_two_step(ctx, storage, M, N, K):
     ops.gate_add_half_f32(r_ref, branch, gate, N, M * N)
     r = dev(res0.clone())
     lin.encode_epilogue(x, qw, torch.empty_like(branch), M, "gate_add", residual=r, gate=gate)
+    # residual add (add_half_into_float); M=256 N=2048 K=2048 runs split over K in both forms
+    r2_ref = dev(res0.clone())
+    ops.add_half_into_float(r2_ref, branch, M * N)
+    r2 = dev(res0.clone())
+    lin.encode_epilogue(x, qw, torch.empty_like(branch), M, "residual_add", residual=r2)
     torch.cuda.synchronize()
     assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
     assert torch.equal(r.view(torch.int32), r_ref.view(torch.int32))
+    assert torch.equal(r2.view(torch.int32), r2_ref.view(torch.int32))
     assert not torch.equal(r.cpu(), res0)
 
 
