@@ -68,7 +68,26 @@ def gen_attention_inputs(torch, sets, seed=1002):
     return out, qw, kw
 
 
-def time_region(torch, stream, fn, steps, warmup):
+def settle_clock(torch, fn, seconds=0.03, rest=0.3):
+    """Untimed: give every timed region the same starting state.  The part first rests for
+    `rest` seconds (after tens of milliseconds of back-to-back launches its clock steps
+    down), then runs fn back to back for about `seconds` (the first region after idle
+    otherwise runs ~10 % slower while the clock ramps up)."""
+    import time
+    torch.cuda.synchronize()
+    time.sleep(rest)
+    t0 = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(16):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+
+
+def time_region(torch, stream, fn, steps, warmup, settle=True):
+    if settle:
+        settle_clock(torch, fn)
     for _ in range(warmup):
         fn(0)
     torch.cuda.synchronize()
@@ -175,7 +194,7 @@ def main():
     if args.profile_kernel:
         # The same timed region as the normal run, so the trace's average duration of
         # these launches can be set beside the live HIP-event figure printed here.
-        kms = time_region(torch, stream, kstep, args.steps, args.warmup)
+        kms = time_region(torch, stream, kstep, args.steps, args.warmup, settle=False)
         print(f"# profile-kernel: flash kernel alone {kms:.4f} ms (HIP events, {args.steps} timed launches)",
               file=sys.stderr, flush=True)
         # calibration: a plain copy of known size (256 MiB read + 256 MiB written)
