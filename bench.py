@@ -194,7 +194,7 @@ def main():
     if args.profile_kernel:
         # The same timed region as the normal run, so the trace's average duration of
         # these launches can be set beside the live HIP-event figure printed here.
-        kms = time_region(torch, stream, kstep, args.steps, args.warmup, settle=False)
+        kms = time_region(torch, stream, kstep, args.steps, args.warmup)
         print(f"# profile-kernel: flash kernel alone {kms:.4f} ms (HIP events, {args.steps} timed launches)",
               file=sys.stderr, flush=True)
         # calibration: a plain copy of known size (256 MiB read + 256 MiB written)
@@ -203,7 +203,8 @@ def main():
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(f"# profile-kernel: {args.warmup + args.steps} flash launches, 3 x 256 MiB copies", file=sys.stderr)
+        print(f"# profile-kernel: settle launches, then {args.warmup} warmup + {args.steps} timed flash launches, "
+              "3 x 256 MiB copies", file=sys.stderr)
         return
 
     kms = time_region(torch, stream, kstep, args.steps, args.warmup)
