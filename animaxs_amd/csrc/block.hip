@@ -533,17 +533,27 @@ void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_
   encode_linear_epilogue(linear_, a_b, 0, w.self_o, br_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION, GEMM_GATE_ADD,
                          residual, mods[0] + 2 * dim);
 
-  // Cross attention to the context (no RoPE; per-head RMSNorm on Q and K).
+  // Cross attention to the context (no RoPE; per-head RMSNorm on Q and K, run in the
+  // projections' output stage when the tiled GEMM takes them, else in the prologue).
   launch_layernorm_modulate(residual, mods[1], static_cast<half_t*>(norm_b.ptr), dim, S, a.eps, dim, stream);
-  linear_.encode(norm_b, 0, w.cross_q, q_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION);
+  bool cq_fused, ckv_fused;
   {
+    const anima_qweight* wq[1] = {&w.cross_q};
+    const anima_buffer oq[1] = {q_b};
+    const GemmEpilogueArgs eq[1] = {{GEMM_QK_NORM, static_cast<const half_t*>(w.cross_q_norm), a.eps}};
+    cq_fused = hd == 128 && linear_.encode_group(norm_b, wq, oq, 1, S, ANIMA_FAMILY_ATTENTION_PROJECTION, eq);
+    if (!cq_fused) linear_.encode(norm_b, 0, w.cross_q, q_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION);
     const anima_qweight* ws2[2] = {&w.cross_k, &w.cross_v};
     const anima_buffer outs[2] = {ck_b, cv_b};
-    linear_.encode_group(a.context, ws2, outs, 2, T, ANIMA_FAMILY_ATTENTION_PROJECTION);
+    const GemmEpilogueArgs ekv[2] = {{GEMM_QK_NORM, static_cast<const half_t*>(w.cross_k_norm), a.eps},
+                                     {GEMM_STORE, nullptr, 0.f}};
+    ckv_fused = hd == 128 && linear_.encode_group(a.context, ws2, outs, 2, T, ANIMA_FAMILY_ATTENTION_PROJECTION, ekv);
+    if (!ckv_fused) linear_.encode_group(a.context, ws2, outs, 2, T, ANIMA_FAMILY_ATTENTION_PROJECTION);
   }
-  anima_qk_prologue cross_pro{w.cross_q_norm, w.cross_k_norm, a.eps, nullptr, 0, 0, 0};
+  anima_qk_prologue cross_pro{cq_fused ? nullptr : w.cross_q_norm, ckv_fused ? nullptr : w.cross_k_norm, a.eps, nullptr,
+                              0, 0, 0};
   att.query = q_b; att.key = ck_b; att.value = cv_b; att.output = a_b;
-  att.query_count = S; att.key_count = T; att.prologue = &cross_pro;
+  att.query_count = S; att.key_count = T; att.prologue = (cq_fused && ckv_fused) ? nullptr : &cross_pro;
   attention_.encode(att);
   encode_linear_epilogue(linear_, a_b, 0, w.cross_o, br_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION, GEMM_GATE_ADD,
                          residual, mods[1] + 2 * dim);

@@ -20,6 +20,10 @@ struct GemmParams {
   //                  (gate_add_half_f32 fused)
   //   GEMM_RESIDUAL_ADD  residual[m, n] += float(half(acc)); y is not written
   //                  (add_half_into_float fused)
+  //   GEMM_QK_NORM   y = half(the per-head (128 columns) RMSNorm of half(acc) times
+  //                  norm_w): the attention's Q/K RMSNorm prologue fused, for projections
+  //                  without RoPE (the RoPE'd form, with a table row per token, cost more
+  //                  in the output stage than the prologue kernel it replaced)
   int epilogue;
   float* residual;        // [M, N] fp32, GEMM_GATE_ADD / GEMM_RESIDUAL_ADD
   const float* gate;      // [N] fp32, GEMM_GATE_ADD
@@ -28,9 +32,18 @@ struct GemmParams {
   // kernel adds them in split order and rounds once.
   int ksplit;
   float* part;
+  const half_t* norm_w;   // [128] fp16, GEMM_QK_NORM
+  float eps;
 };
 
-enum GemmEpilogue { GEMM_STORE = 0, GEMM_GELU = 1, GEMM_GATE_ADD = 2, GEMM_RESIDUAL_ADD = 3 };
+enum GemmEpilogue { GEMM_STORE = 0, GEMM_GELU = 1, GEMM_GATE_ADD = 2, GEMM_RESIDUAL_ADD = 3, GEMM_QK_NORM = 4 };
+
+// Output stage of one member of a grouped linear (GEMM_STORE or GEMM_QK_NORM).
+struct GemmEpilogueArgs {
+  int epilogue;
+  const half_t* norm_w;
+  float eps;
+};
 
 // Up to PG_GROUP independent GEMMs of one K and storage in one ping-pong launch
 // (the Q/K/V projections of one input): logical tiles [first_tile[i],
@@ -144,8 +157,11 @@ class LinearExecutor {
   // count (1..PG_GROUP) linears of one input, each into its own output, as one
   // ping-pong launch when every one of them takes that kernel (same K and storage);
   // otherwise encode() for each in turn.
-  void encode_group(anima_buffer input, const anima_qweight* const* weights, const anima_buffer* outputs, int count,
-                    int64_t input_rows, int32_t family);
+  // With epi (one per weight): the output stages run in the GEMM and encode_group
+  // returns true; if the group cannot run as one ping-pong launch it encodes nothing
+  // and returns false.  Without epi it always encodes and returns true.
+  bool encode_group(anima_buffer input, const anima_qweight* const* weights, const anima_buffer* outputs, int count,
+                    int64_t input_rows, int32_t family, const GemmEpilogueArgs* epi = nullptr);
   anima_ctx* context() const { return ctx_; }
 
  private:

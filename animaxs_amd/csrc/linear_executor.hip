@@ -116,8 +116,8 @@ void LinearExecutor::encode(anima_buffer input, int64_t input_offset, const anim
   launch_gemm(p, w.storage, stream);
 }
 
-void LinearExecutor::encode_group(anima_buffer input, const anima_qweight* const* weights, const anima_buffer* outputs,
-                                  int count, int64_t input_rows, int32_t family) {
+bool LinearExecutor::encode_group(anima_buffer input, const anima_qweight* const* weights, const anima_buffer* outputs,
+                                  int count, int64_t input_rows, int32_t family, const GemmEpilogueArgs* epi) {
   if (count < 1 || count > PG_GROUP) fail(ANIMA_E_INVALID_ARGUMENT, "linear group holds 1 to 3 weights");
   if (family < ANIMA_FAMILY_OTHER || family > ANIMA_FAMILY_MLP_DOWN)
     fail(ANIMA_E_INVALID_ARGUMENT, "unknown linear family");
@@ -133,12 +133,26 @@ void LinearExecutor::encode_group(anima_buffer input, const anima_qweight* const
                pingpong_ksplit(ps[i], w.storage) == 1 && (i == 0 || (w.storage == storage && ps[i].K == ps[0].K));
     storage = w.storage;
   }
+  if (epi) {
+    for (int i = 0; i < count; ++i) {
+      if (epi[i].epilogue != GEMM_STORE && epi[i].epilogue != GEMM_QK_NORM)
+        fail(ANIMA_E_INVALID_ARGUMENT, "grouped linears take plain or Q/K-norm output stages");
+      if (epi[i].epilogue == GEMM_QK_NORM) {
+        together = together && epi[i].norm_w && aligned16(epi[i].norm_w) && ps[i].N % 128 == 0;
+        ps[i].epilogue = GEMM_QK_NORM;
+        ps[i].norm_w = epi[i].norm_w;
+        ps[i].eps = epi[i].eps;
+      }
+    }
+    if (!together) return false;
+  }
   if (!together) {
     for (int i = 0; i < count; ++i) encode(input, 0, *weights[i], outputs[i], 0, input_rows, family);
-    return;
+    return true;
   }
   DeviceGuard guard(ctx_);
   launch_pingpong_group(ps, count, storage, ctx_->stream);
+  return true;
 }
 
 bool LinearExecutor::encode_fused(anima_buffer input, int64_t input_offset, const anima_qweight& weight,

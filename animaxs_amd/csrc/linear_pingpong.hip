@@ -471,6 +471,25 @@ void pingpong_gemm_kernel(GemmGroup gp) {
       const int r = orow + 16 * i, m = m0 + r;
       half8v v = *reinterpret_cast<const half8v*>(tile + r * PG_OROW + 8 * ochunk);
       if (m >= p.M) continue;
+      if (EPI == GEMM_QK_NORM) {
+        // Per-head RMSNorm: 16 lanes hold one 128-column head row.
+        float x[8];
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          x[e] = (float)v[e];
+          ss = fmaf(x[e], x[e], ss);
+        }
+        ss += __shfl_xor(ss, 1);
+        ss += __shfl_xor(ss, 2);
+        ss += __shfl_xor(ss, 4);
+        ss += __shfl_xor(ss, 8);
+        const float inv = rsqrtf(ss / 128.f + p.eps);
+        const int dh = 8 * (ochunk & 15);
+        const half8v w = *reinterpret_cast<const half8v*>(p.norm_w + dh);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = f32_to_f16(x[e] * inv * (float)w[e]);
+      }
       if (EPI == GEMM_GELU) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = gelu_erf_half(v[e]);
@@ -529,6 +548,8 @@ void pingpong_gemm_kernel(GemmGroup gp) {
     store_tile(std::integral_constant<int, GEMM_GATE_ADD>{});
   else if (p.epilogue == GEMM_RESIDUAL_ADD)
     store_tile(std::integral_constant<int, GEMM_RESIDUAL_ADD>{});
+  else if (p.epilogue == GEMM_QK_NORM)
+    store_tile(std::integral_constant<int, GEMM_QK_NORM>{});
   else
     store_tile(std::integral_constant<int, GEMM_STORE>{});
 }
@@ -600,6 +621,8 @@ void launch_pingpong_group(const GemmParams* ps, int count, int storage, hipStre
       fail(ANIMA_E_INVALID_ARGUMENT, "GEMM gate-add epilogue needs residual and gate");
     if (p.epilogue == GEMM_RESIDUAL_ADD && !p.residual)
       fail(ANIMA_E_INVALID_ARGUMENT, "GEMM residual-add epilogue needs the residual");
+    if (p.epilogue == GEMM_QK_NORM && (!p.norm_w || p.N % 128 != 0 || !aligned16(p.norm_w)))
+      fail(ANIMA_E_INVALID_ARGUMENT, "GEMM Q/K-norm epilogue needs 128-column heads and the norm weight");
     swin = swin && p.groups % PG_WIN == 0 && aligned16(p.scale) && aligned16(p.zero);
     if (p.ksplit > 1) {
       if (count != 1 || !p.part || p.ksplit != pingpong_ksplit(p, storage))
