@@ -317,9 +317,8 @@ constexpr int smallm_rows() { return MB == 2 ? 2 : 1; }
 // Waves per workgroup (S) times chunks per wave (NCH x NST) must cover K; the
 // fewest chunks per wave wins (the most waves share the dequantization), within
 // smallm_max_waves and a reduction buffer (S x R*MB KiB) of at most 64 KiB.
-template <int STORAGE, int MB>
+template <int STORAGE, int MB, int R = smallm_rows<STORAGE, MB>()>
 static int smallm_steps(int K, int* S) {
-  constexpr int R = smallm_rows<STORAGE, MB>();
   constexpr int NCH = smallm_max_chunks<STORAGE, MB>();
   const int chunks = K / SM_CHUNK;
   const int max_s = std::min(smallm_max_waves<MB>(), 64 / (R * MB));
@@ -328,7 +327,8 @@ static int smallm_steps(int K, int* S) {
     const int per = NCH * nst;
     const int s = (chunks + per - 1) / per;
     // the scale/zero copy: 16R rows x groups halfs over 64*S threads
-    if (s <= max_s && 16 * R * groups <= SM_PARAM_REGS * 64 * s) {
+    const int64_t lds = (int64_t)s * R * MB * 4 * 64 * 4 + (int64_t)2 * 16 * R * groups * 2;
+    if (s <= max_s && 16 * R * groups <= SM_PARAM_REGS * 64 * s && lds <= 65536) {
       *S = s;
       return nst;
     }
@@ -336,18 +336,33 @@ static int smallm_steps(int K, int* S) {
   return 0;
 }
 
-template <int STORAGE, int MB>
-static void launch_smallm_r(const SmallMParams& p, hipStream_t stream) {
-  constexpr int R = smallm_rows<STORAGE, MB>();
+template <int STORAGE, int MB, int R>
+static void launch_smallm_rr(const SmallMParams& p, hipStream_t stream) {
   constexpr int NCH = smallm_max_chunks<STORAGE, MB>();
   int S = 0;
-  switch (smallm_steps<STORAGE, MB>(p.K, &S)) {
+  switch (smallm_steps<STORAGE, MB, R>(p.K, &S)) {
     case 1: launch_smallm_t<STORAGE, MB, R, NCH, 1>(p, S, stream); break;
     case 2: launch_smallm_t<STORAGE, MB, R, NCH, 2>(p, S, stream); break;
     case 4: launch_smallm_t<STORAGE, MB, R, NCH, 4>(p, S, stream); break;
     case 8: launch_smallm_t<STORAGE, MB, R, NCH, 8>(p, S, stream); break;
     default: fail(ANIMA_E_UNSUPPORTED, "small-M GEMM: K too large for the weight-streaming kernel");
   }
+}
+
+// With 33..64 input rows every workgroup re-reads X for its K slices, so wide N pays
+// X traffic per 16 weight rows; two row blocks per wave halve it when N leaves
+// enough workgroups (>= 256 of 32 rows).
+template <int STORAGE, int MB>
+static void launch_smallm_r(const SmallMParams& p, hipStream_t stream) {
+  constexpr int R = smallm_rows<STORAGE, MB>();
+  if constexpr (MB >= 3 && R == 1 && STORAGE != ANIMA_STORAGE_FP16) {
+    int S = 0;
+    if (p.N >= 32 * 256 && smallm_steps<STORAGE, MB, 2>(p.K, &S) > 0) {
+      launch_smallm_rr<STORAGE, MB, 2>(p, stream);
+      return;
+    }
+  }
+  launch_smallm_rr<STORAGE, MB, R>(p, stream);
 }
 
 template <int STORAGE>

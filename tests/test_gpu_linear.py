@@ -302,7 +302,7 @@ def _affine_weight(storage: int, N: int, K: int, seed: int, pad: int = 0) -> dic
 @pytest.mark.parametrize("storage", [0, 1, 2])
 @pytest.mark.parametrize("M,N,K,pad", [(1, 2048, 2048, 0), (5, 1000, 384, 16), (16, 8192, 2048, 0),
                                        (17, 130, 1280, 32), (33, 2048, 1024, 0), (64, 2048, 8192, 0),
-                                       (64, 4000, 2048, 16)])
+                                       (64, 4000, 2048, 16), (64, 8192, 2048, 0), (40, 8200, 1024, 16)])
 def test_small_m_weight_stream_gemm(ctx, storage, M, N, K, pad):
     """M <= 64 with K a multiple of 128 takes the weight-streaming kernel: every storage, ragged N,
     padded row strides; the output's neighbours stay untouched."""
