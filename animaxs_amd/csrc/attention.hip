@@ -419,12 +419,16 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(PrologueParams p) {
 // loads, so the token's RoPE blocks (eight float4 loads per lane) and the norm
 // weights are read once per HPT heads.  The per-head sum of squares needs three
 // lane exchanges.  Same arithmetic as the generic kernel (and as the fused Q path
-// of the flash kernels).
+// of the flash kernels).  Every byte is touched once, so the loads and stores are
+// nontemporal, and small (128-thread) workgroups spread the one-pass grid evenly:
+// 6.5-7 us against 8 us with cached accesses in 256-thread groups at S=4096, H=16.
+constexpr int PRO_D128_THREADS = 128;
+
 template <int HPT>
-__global__ __launch_bounds__(256) void qk_prologue_d128_kernel(PrologueParams p) {
+__global__ __launch_bounds__(PRO_D128_THREADS) void qk_prologue_d128_kernel(PrologueParams p) {
   const int sub = threadIdx.x & 7;
   const int groups = p.heads / HPT;
-  const int64_t unit = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int64_t unit = (int64_t)blockIdx.x * (PRO_D128_THREADS / 8) + (threadIdx.x >> 3);
   const int64_t total = (int64_t)p.batch * p.rows * groups;
   const bool live = unit < total;
   const int64_t uu = live ? unit : total - 1;   // tail lanes recompute the last unit, never store
@@ -435,8 +439,8 @@ __global__ __launch_bounds__(256) void qk_prologue_d128_kernel(PrologueParams p)
 #pragma unroll
   for (int j = 0; j < HPT; ++j) {
     const half_t* x = p.in + (int64_t)b * p.in_batch + t * p.in_tok + (int64_t)(hg * HPT + j) * p.in_head;
-    const half8v xa = *reinterpret_cast<const half8v*>(x + 8 * sub);
-    const half8v xc = *reinterpret_cast<const half8v*>(x + 64 + 8 * sub);
+    const half8v xa = __builtin_nontemporal_load(reinterpret_cast<const half8v*>(x + 8 * sub));
+    const half8v xc = __builtin_nontemporal_load(reinterpret_cast<const half8v*>(x + 64 + 8 * sub));
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       a[j][i] = (float)xa[i];
@@ -486,8 +490,8 @@ __global__ __launch_bounds__(256) void qk_prologue_d128_kernel(PrologueParams p)
         oc[i] = f32_to_f16(c[j][i]);
       }
       half_t* y = p.out + (((int64_t)b * p.heads + hg * HPT + j) * p.rows + t) * 128;
-      *reinterpret_cast<half8v*>(y + 8 * sub) = oa;
-      *reinterpret_cast<half8v*>(y + 64 + 8 * sub) = oc;
+      __builtin_nontemporal_store(oa, reinterpret_cast<half8v*>(y + 8 * sub));
+      __builtin_nontemporal_store(oc, reinterpret_cast<half8v*>(y + 64 + 8 * sub));
     }
   }
 }
@@ -574,14 +578,16 @@ void launch_prologue(const PrologueParams& p, hipStream_t stream) {
                     (!p.rope || aligned16(p.rope));
   if (fast) {
     const int hpt = p.heads % 4 == 0 ? 4 : (p.heads % 2 == 0 ? 2 : 1);
-    const int64_t blocks = (rows / hpt + 31) / 32;
+    constexpr int units = PRO_D128_THREADS / 8;
+    const int64_t blocks = (rows / hpt + units - 1) / units;
     if (blocks > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "prologue grid too large");
+    const dim3 block(PRO_D128_THREADS);
     if (hpt == 4)
-      hipLaunchKernelGGL(qk_prologue_d128_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL(qk_prologue_d128_kernel<4>, dim3((unsigned)blocks), block, 0, stream, p);
     else if (hpt == 2)
-      hipLaunchKernelGGL(qk_prologue_d128_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL(qk_prologue_d128_kernel<2>, dim3((unsigned)blocks), block, 0, stream, p);
     else
-      hipLaunchKernelGGL(qk_prologue_d128_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL(qk_prologue_d128_kernel<1>, dim3((unsigned)blocks), block, 0, stream, p);
     ANIMA_HIP(hipGetLastError());
     return;
   }
