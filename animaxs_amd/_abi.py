@@ -48,8 +48,9 @@ class AttentionConfig(C.Structure):
 
 
 class QKPrologue(C.Structure):
-    _fields_ = [("q_norm_weight", C.c_void_p), ("k_norm_weight", C.c_void_p), ("eps", C.c_float),
-                ("rope", C.c_void_p), ("rope_tokens", C.c_int64), ("rope_q", C.c_int32), ("rope_k", C.c_int32)]
+    _fields_ = [("q_norm_weight", Buffer), ("k_norm_weight", Buffer), ("eps", C.c_float),
+                ("rope", Buffer), ("rope_tokens", C.c_int64), ("rope_q", C.c_int32), ("rope_k", C.c_int32),
+                ("k_rope", Buffer), ("k_rope_tokens", C.c_int64)]
 
 
 class AttentionArgs(C.Structure):
@@ -85,25 +86,25 @@ class DitBlockWeights(C.Structure):
     _fields_ = [(n, QWeight) for n in (
         "self_q", "self_k", "self_v", "self_o", "cross_q", "cross_k", "cross_v", "cross_o", "mlp1", "mlp2",
         "mod_self_w1", "mod_self_w2", "mod_cross_w1", "mod_cross_w2", "mod_mlp_w1", "mod_mlp_w2")] + [
-        ("self_q_norm", C.c_void_p), ("self_k_norm", C.c_void_p),
-        ("cross_q_norm", C.c_void_p), ("cross_k_norm", C.c_void_p)]
+        ("self_q_norm", Buffer), ("self_k_norm", Buffer),
+        ("cross_q_norm", Buffer), ("cross_k_norm", Buffer)]
 
 
 class DitBlockArgs(C.Structure):
     _fields_ = [("residual", Buffer), ("emb", Buffer), ("adaln_lora", Buffer), ("context", Buffer),
-                ("rope", C.c_void_p), ("tokens", C.c_int64), ("dim", C.c_int64), ("heads", C.c_int64),
+                ("rope", Buffer), ("tokens", C.c_int64), ("dim", C.c_int64), ("heads", C.c_int64),
                 ("head_dim", C.c_int64), ("context_tokens", C.c_int64), ("context_dim", C.c_int64),
                 ("mlp_hidden", C.c_int64), ("eps", C.c_float)]
 
 
 class QwenLayerWeights(C.Structure):
     _fields_ = [(n, QWeight) for n in ("q", "k", "v", "o", "gate", "up", "down")] + [
-        ("input_norm", C.c_void_p), ("post_attention_norm", C.c_void_p),
-        ("q_norm", C.c_void_p), ("k_norm", C.c_void_p)]
+        ("input_norm", Buffer), ("post_attention_norm", Buffer),
+        ("q_norm", Buffer), ("k_norm", Buffer)]
 
 
 class QwenLayerArgs(C.Structure):
-    _fields_ = [("residual", Buffer), ("rope", C.c_void_p), ("key_lengths", C.c_void_p),
+    _fields_ = [("residual", Buffer), ("rope", Buffer), ("key_lengths", C.c_void_p),
                 ("batch", C.c_int64), ("tokens", C.c_int64), ("hidden", C.c_int64), ("heads", C.c_int64),
                 ("kv_heads", C.c_int64), ("head_dim", C.c_int64), ("intermediate", C.c_int64),
                 ("eps", C.c_float)]
@@ -158,6 +159,19 @@ SIGNATURES = {
     "anima_dit_block_create": (_S, [_P, _PP]),
     "anima_dit_block_destroy": (_S, [_P]),
     "anima_dit_block_encode": (_S, [_P, C.POINTER(DitBlockWeights), C.POINTER(DitBlockArgs)]),
+    "anima_dit_block_encode_cached": (_S, [_P, C.POINTER(DitBlockWeights), C.POINTER(DitBlockArgs), _P, _I64]),
+    "anima_dit_forward_encode": (_S, [_P, C.POINTER(DitBlockWeights), _I64, C.POINTER(DitBlockArgs), _P]),
+    "anima_dit_forward_encode_streamed": (_S, [_P, _P, C.POINTER(DitBlockWeights), _P, _P, _I64,
+                                               C.POINTER(DitBlockArgs), _P]),
+    "anima_cross_kv_cache_create": (_S, [_P, _I64, _I64, _I64, _PP]),
+    "anima_cross_kv_cache_destroy": (_S, [_P]),
+    "anima_cross_kv_cache_reset": (_S, [_P]),
+    "anima_cross_kv_cache_is_ready": (_S, [_P, _I64, C.POINTER(_I32)]),
+    "anima_cross_kv_cache_bytes": (_S, [_P, C.POINTER(_I64)]),
+    "anima_weight_streamer_create": (_S, [_P, _I64, _I32, _PP]),
+    "anima_weight_streamer_destroy": (_S, [_P]),
+    "anima_linear_encode_head_rmsnorm": (_S, [_P, Buffer, _I64, C.POINTER(QWeight), Buffer, _I64, _I64, _I32,
+                                              Buffer, _I64, C.c_float]),
 }
 
 _lib = None

@@ -174,6 +174,21 @@ anima_status anima_linear_encode_group(anima_linear* lin, anima_buffer input, co
   });
 }
 
+anima_status anima_linear_encode_head_rmsnorm(anima_linear* lin, anima_buffer input, int64_t input_offset,
+                                              const anima_qweight* weight, anima_buffer output, int64_t output_offset,
+                                              int64_t input_rows, int32_t family, anima_buffer norm_weight,
+                                              int64_t head_dim, float eps) {
+  return guarded([&] {
+    require(lin, "linear");
+    const anima_qweight& w = *require(weight, "weight");
+    if (head_dim <= 0) fail(ANIMA_E_INVALID_SHAPE, "per-head RMSNorm head_dim must be positive");
+    if (!norm_weight.ptr) fail(ANIMA_E_INVALID_ARGUMENT, "per-head RMSNorm weight pointer is null");
+    check_elementwise(norm_weight, head_dim, 2, "per-head RMSNorm weight");
+    lin->impl.encode_head_rmsnorm(input, input_offset, w, output, output_offset, input_rows, family,
+                                  static_cast<const half_t*>(norm_weight.ptr), head_dim, eps);
+  });
+}
+
 anima_status anima_linear_execute(anima_linear* lin, anima_buffer input, int64_t input_offset,
                                   const anima_qweight* weight, anima_buffer output, int64_t output_offset,
                                   int64_t input_rows, int32_t family) {
@@ -341,6 +356,84 @@ anima_status anima_dit_block_destroy(anima_dit_block* blk) {
 anima_status anima_dit_block_encode(anima_dit_block* blk, const anima_dit_block_weights* w,
                                     const anima_dit_block_args* args) {
   return guarded([&] { require(blk, "block")->impl.encode(*require(w, "block weights"), *require(args, "block args")); });
+}
+
+anima_status anima_dit_block_encode_cached(anima_dit_block* blk, const anima_dit_block_weights* w,
+                                           const anima_dit_block_args* args, anima_cross_kv_cache* cache,
+                                           int64_t block_index) {
+  return guarded([&] {
+    require(blk, "block")->impl.encode(*require(w, "block weights"), *require(args, "block args"),
+                                       cache ? &cache->impl : nullptr, block_index);
+  });
+}
+
+anima_status anima_dit_forward_encode(anima_dit_block* blk, const anima_dit_block_weights* blocks,
+                                      int64_t block_count, const anima_dit_block_args* args,
+                                      anima_cross_kv_cache* cache) {
+  return guarded([&] {
+    require(blk, "block")->impl.forward(blocks, block_count, *require(args, "block args"),
+                                        cache ? &cache->impl : nullptr);
+  });
+}
+
+anima_status anima_dit_forward_encode_streamed(anima_dit_block* blk, anima_weight_streamer* streamer,
+                                               const anima_dit_block_weights* templates,
+                                               const void* const* host_ranges, const int64_t* range_bytes,
+                                               int64_t block_count, const anima_dit_block_args* args,
+                                               anima_cross_kv_cache* cache) {
+  return guarded([&] {
+    require(blk, "block")->impl.forward_streamed(require(streamer, "weight streamer")->impl, templates, host_ranges,
+                                                 range_bytes, block_count, *require(args, "block args"),
+                                                 cache ? &cache->impl : nullptr);
+  });
+}
+
+// ---------------------------------------------------------------- cross K/V cache, weight streamer
+anima_status anima_cross_kv_cache_create(anima_ctx* ctx, int64_t blocks, int64_t context_tokens, int64_t dim,
+                                         anima_cross_kv_cache** out) {
+  return guarded([&] {
+    require(out, "cache output");
+    *out = nullptr;
+    require(ctx, "context");
+    if (!(blocks > 0 && context_tokens > 0 && dim > 0)) fail(ANIMA_E_INVALID_SHAPE, "invalid cross K/V cache shape");
+    *out = new anima_cross_kv_cache(ctx, blocks, context_tokens, dim);
+  });
+}
+
+anima_status anima_cross_kv_cache_destroy(anima_cross_kv_cache* cache) {
+  return guarded([&] { delete cache; });
+}
+
+anima_status anima_cross_kv_cache_reset(anima_cross_kv_cache* cache) {
+  return guarded([&] { require(cache, "cross K/V cache")->impl.reset(); });
+}
+
+anima_status anima_cross_kv_cache_is_ready(const anima_cross_kv_cache* cache, int64_t block, int32_t* ready) {
+  return guarded([&] {
+    const CrossKVCache& c = require(cache, "cross K/V cache")->impl;
+    if (block < 0 || block >= c.blocks()) fail(ANIMA_E_INVALID_ARGUMENT, "cross K/V cache block index out of range");
+    *require(ready, "output") = c.ready(block) ? 1 : 0;
+  });
+}
+
+anima_status anima_cross_kv_cache_bytes(const anima_cross_kv_cache* cache, int64_t* bytes) {
+  return guarded([&] { *require(bytes, "output") = require(cache, "cross K/V cache")->impl.bytes(); });
+}
+
+anima_status anima_weight_streamer_create(anima_ctx* ctx, int64_t capacity, int32_t slots,
+                                          anima_weight_streamer** out) {
+  return guarded([&] {
+    require(out, "streamer output");
+    *out = nullptr;
+    require(ctx, "context");
+    if (capacity <= 0) fail(ANIMA_E_INVALID_SHAPE, "weight ring capacity must be positive");
+    if (slots < 1 || slots > 4) fail(ANIMA_E_INVALID_ARGUMENT, "weight slot count must be in 1...4");
+    *out = new anima_weight_streamer(ctx, capacity, slots);
+  });
+}
+
+anima_status anima_weight_streamer_destroy(anima_weight_streamer* streamer) {
+  return guarded([&] { delete streamer; });
 }
 
 }  // extern "C"

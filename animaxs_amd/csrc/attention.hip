@@ -358,7 +358,7 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(PrologueParams p) {
   const int64_t t = (row / p.heads) % p.rows;
   const int b = (int)(row / ((int64_t)p.heads * p.rows));
   const half_t* x = p.in + (int64_t)b * p.in_batch + t * p.in_tok + (int64_t)h * p.in_head;
-  half_t* y = p.out + (((int64_t)b * p.heads + h) * p.rows + t) * p.D;
+  half_t* y = p.out + (int64_t)b * p.out_batch + t * p.out_tok + (int64_t)h * p.out_head;
   const int half = p.D / 2;
   constexpr int EMAX = GEN_MAX_D / 128;  // pairs per lane
   float a[EMAX], c[EMAX];
@@ -489,7 +489,7 @@ __global__ __launch_bounds__(PRO_D128_THREADS) void qk_prologue_d128_kernel(Prol
         oa[i] = f32_to_f16(a[j][i]);
         oc[i] = f32_to_f16(c[j][i]);
       }
-      half_t* y = p.out + (((int64_t)b * p.heads + hg * HPT + j) * p.rows + t) * 128;
+      half_t* y = p.out + (int64_t)b * p.out_batch + t * p.out_tok + (int64_t)(hg * HPT + j) * p.out_head;
       __builtin_nontemporal_store(oa, reinterpret_cast<half8v*>(y + 8 * sub));
       __builtin_nontemporal_store(oc, reinterpret_cast<half8v*>(y + 64 + 8 * sub));
     }
@@ -574,8 +574,8 @@ void launch_prologue(const PrologueParams& p, hipStream_t stream) {
   const int64_t rows = (int64_t)p.batch * p.rows * p.heads;
   if (rows <= 0) return;
   const bool fast = p.D == 128 && aligned16(p.in) && p.in_tok % 8 == 0 && p.in_head % 8 == 0 &&
-                    p.in_batch % 8 == 0 && aligned16(p.out) && (!p.norm_w || aligned16(p.norm_w)) &&
-                    (!p.rope || aligned16(p.rope));
+                    p.in_batch % 8 == 0 && aligned16(p.out) && p.out_tok % 8 == 0 && p.out_head % 8 == 0 &&
+                    p.out_batch % 8 == 0 && (!p.norm_w || aligned16(p.norm_w)) && (!p.rope || aligned16(p.rope));
   if (fast) {
     const int hpt = p.heads % 4 == 0 ? 4 : (p.heads % 2 == 0 ? 2 : 1);
     constexpr int units = PRO_D128_THREADS / 8;

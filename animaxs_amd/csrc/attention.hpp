@@ -40,7 +40,8 @@ struct FlashParams {
 struct PrologueParams {
   const half_t* in;
   int64_t in_tok, in_head, in_batch;
-  half_t* out;                     // dense [batch][heads][rows][D]
+  half_t* out;                     // element strides below (the attention uses dense
+  int64_t out_tok, out_head, out_batch;  // head-major [batch][heads][rows][D])
   int batch, rows, heads, D;
   const half_t* norm_w;
   float eps;

@@ -112,19 +112,43 @@ void AttentionExecutor::encode(const anima_attention_args& a) {
   const float* rope_k = nullptr;
   float eps = 0.f;
   if (pro) {
-    q_norm = static_cast<const half_t*>(pro->q_norm_weight);
-    k_norm = static_cast<const half_t*>(pro->k_norm_weight);
     eps = pro->eps;
     if (!std::isfinite(eps) || eps < 0.f) fail(ANIMA_E_INVALID_ARGUMENT, "RMSNorm epsilon must be finite and >= 0");
-    if (pro->rope) {
+    const int64_t w_bytes = checked_product({D, 2}, "attention prologue");
+    if (pro->q_norm_weight.ptr) {
+      if (pro->q_norm_weight.length < w_bytes)
+        fail(ANIMA_E_OUT_OF_BOUNDS, "Q RMSNorm weight holds fewer than head_dim fp16 values");
+      q_norm = static_cast<const half_t*>(pro->q_norm_weight.ptr);
+    }
+    if (pro->k_norm_weight.ptr) {
+      if (pro->k_norm_weight.length < w_bytes)
+        fail(ANIMA_E_OUT_OF_BOUNDS, "K RMSNorm weight holds fewer than head_dim fp16 values");
+      k_norm = static_cast<const half_t*>(pro->k_norm_weight.ptr);
+    }
+    const bool want_q = pro->rope.ptr && pro->rope_q;
+    const bool want_k = pro->rope_k && (pro->k_rope.ptr || pro->rope.ptr);
+    if (want_q || want_k) {
       if (D % 2) fail(ANIMA_E_INVALID_SHAPE, "RoPE requires an even head_dim");
-      if (pro->rope_q) {
+      // [tokens][D/2][2][2] fp32 = 8 * D bytes per token.
+      const int64_t row_bytes = checked_product({D, 8}, "attention prologue");
+      if (want_q) {
         if (pro->rope_tokens < Sq) fail(ANIMA_E_OUT_OF_BOUNDS, "RoPE table has fewer rows than query_count");
-        rope_q = pro->rope;
+        if (checked_product({pro->rope_tokens, row_bytes}, "attention prologue") > pro->rope.length)
+          fail(ANIMA_E_OUT_OF_BOUNDS, "RoPE table buffer is shorter than rope_tokens rows");
+        rope_q = static_cast<const float*>(pro->rope.ptr);
       }
-      if (pro->rope_k) {
-        if (pro->rope_tokens < Sk) fail(ANIMA_E_OUT_OF_BOUNDS, "RoPE table has fewer rows than key_count");
-        rope_k = pro->rope;
+      if (want_k) {
+        if (pro->k_rope.ptr) {
+          if (pro->k_rope_tokens < Sk) fail(ANIMA_E_OUT_OF_BOUNDS, "K RoPE table has fewer rows than key_count");
+          if (checked_product({pro->k_rope_tokens, row_bytes}, "attention prologue") > pro->k_rope.length)
+            fail(ANIMA_E_OUT_OF_BOUNDS, "K RoPE table buffer is shorter than k_rope_tokens rows");
+          rope_k = static_cast<const float*>(pro->k_rope.ptr);
+        } else {
+          if (pro->rope_tokens < Sk) fail(ANIMA_E_OUT_OF_BOUNDS, "RoPE table has fewer rows than key_count");
+          if (checked_product({pro->rope_tokens, row_bytes}, "attention prologue") > pro->rope.length)
+            fail(ANIMA_E_OUT_OF_BOUNDS, "RoPE table buffer is shorter than rope_tokens rows");
+          rope_k = static_cast<const float*>(pro->rope.ptr);
+        }
       }
     }
   }
@@ -175,6 +199,7 @@ void AttentionExecutor::encode(const anima_attention_args& a) {
     PrologueParams pp{};
     pp.in = kp; pp.in_tok = k_tok; pp.in_head = k_head; pp.in_batch = k_batch;
     pp.out = reinterpret_cast<half_t*>(ws);
+    pp.out_tok = D; pp.out_head = Sk * D; pp.out_batch = kvh * Sk * D;
     pp.batch = (int)B; pp.rows = (int)Sk; pp.heads = (int)kvh; pp.D = (int)D;
     pp.norm_w = k_norm; pp.eps = eps; pp.rope = rope_k;
     launch_prologue(pp, stream);
@@ -185,6 +210,7 @@ void AttentionExecutor::encode(const anima_attention_args& a) {
     PrologueParams pp{};
     pp.in = qp; pp.in_tok = q_tok; pp.in_head = q_head; pp.in_batch = q_batch;
     pp.out = reinterpret_cast<half_t*>(ws + k_ws);
+    pp.out_tok = D; pp.out_head = Sq * D; pp.out_batch = H * Sq * D;
     pp.batch = (int)B; pp.rows = (int)Sq; pp.heads = (int)H; pp.D = (int)D;
     pp.norm_w = q_norm; pp.eps = eps; pp.rope = rope_q;
     launch_prologue(pp, stream);

@@ -453,19 +453,33 @@ static MatvecParams matvec_params(const anima_qweight& weight, const float* x, f
   return p;
 }
 
-void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_block_args& a) {
+static void require_buffer(const anima_buffer& b, int64_t bytes, const char* what) {
+  if (!b.ptr) fail(ANIMA_E_INVALID_ARGUMENT, std::string(what) + " pointer is null");
+  if (b.length < bytes) fail(ANIMA_E_OUT_OF_BOUNDS, std::string(what) + " buffer range is out of bounds");
+}
+
+void DitBlockExecutor::check(const anima_dit_block_weights& w, const anima_dit_block_args& a,
+                             const CrossKVCache* cache, int64_t block_index) const {
   const int64_t S = a.tokens, dim = a.dim, H = a.heads, hd = a.head_dim, T = a.context_tokens, C = a.context_dim,
                 hidden = a.mlp_hidden;
   if (!(S > 0 && dim > 0 && H > 0 && hd > 0 && T > 0 && C > 0 && hidden > 0 && H * hd == dim))
     fail(ANIMA_E_INVALID_SHAPE, "invalid DiT block shape (requires heads * head_dim == dim)");
+  if (hd % 2) fail(ANIMA_E_INVALID_SHAPE, "DiT block RoPE requires an even head_dim");
   if (!(a.eps >= 0.f && std::isfinite(a.eps))) fail(ANIMA_E_INVALID_ARGUMENT, "DiT block epsilon must be finite");
-  if (checked_product({S, dim, 4}, "DiT block") > a.residual.length || checked_product({dim, 4}, "DiT block") > a.emb.length ||
-      checked_product({3 * dim, 4}, "DiT block") > a.adaln_lora.length ||
-      checked_product({T, C, 2}, "DiT block") > a.context.length)
-    fail(ANIMA_E_OUT_OF_BOUNDS, "DiT block buffer range is out of bounds");
-  if (!a.rope) fail(ANIMA_E_INVALID_ARGUMENT, "DiT block requires a RoPE table");
+  require_buffer(a.residual, checked_product({S, dim, 4}, "DiT block"), "DiT block residual");
+  require_buffer(a.emb, checked_product({dim, 4}, "DiT block"), "DiT block emb");
+  require_buffer(a.adaln_lora, checked_product({3 * dim, 4}, "DiT block"), "DiT block adaln_lora");
+  require_buffer(a.context, checked_product({T, C, 2}, "DiT block"), "DiT block context");
+  // [tokens][head_dim/2][2][2] fp32
+  require_buffer(a.rope, checked_product({S, hd, 8}, "DiT block"), "DiT block RoPE table");
+  const int64_t nb = checked_product({hd, 2}, "DiT block");
+  require_buffer(w.self_q_norm, nb, "DiT block self Q norm");
+  require_buffer(w.self_k_norm, nb, "DiT block self K norm");
+  require_buffer(w.cross_q_norm, nb, "DiT block cross Q norm");
+  require_buffer(w.cross_k_norm, nb, "DiT block cross K norm");
   auto need = [&](const anima_qweight& q, int64_t rows, int64_t cols, const char* nm) {
     if (q.rows != rows || q.columns != cols) fail(ANIMA_E_INVALID_SHAPE, std::string(nm) + " shape mismatch");
+    (void)validate_weight(q, nm);
   };
   need(w.self_q, dim, dim, "self_q"); need(w.self_k, dim, dim, "self_k"); need(w.self_v, dim, dim, "self_v");
   need(w.self_o, dim, dim, "self_o"); need(w.cross_q, dim, dim, "cross_q"); need(w.cross_k, dim, C, "cross_k");
@@ -475,6 +489,20 @@ void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_
   need(w.mod_self_w1, lora, dim, "mod_self_w1"); need(w.mod_cross_w1, lora, dim, "mod_cross_w1");
   need(w.mod_mlp_w1, lora, dim, "mod_mlp_w1"); need(w.mod_self_w2, 3 * dim, lora, "mod_self_w2");
   need(w.mod_cross_w2, 3 * dim, lora, "mod_cross_w2"); need(w.mod_mlp_w2, 3 * dim, lora, "mod_mlp_w2");
+  if (cache) {
+    if (block_index < 0 || block_index >= cache->blocks())
+      fail(ANIMA_E_INVALID_ARGUMENT, "cross K/V cache block index out of range");
+    if (cache->tokens() != T || cache->dim() != dim)
+      fail(ANIMA_E_INVALID_SHAPE, "cross K/V cache shape differs from the block's context tokens or dim");
+  }
+}
+
+void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_block_args& a, CrossKVCache* cache,
+                              int64_t block_index) {
+  check(w, a, cache, block_index);
+  const int64_t S = a.tokens, dim = a.dim, H = a.heads, hd = a.head_dim, T = a.context_tokens,
+                hidden = a.mlp_hidden;
+  const int64_t lora = w.mod_self_w1.rows;
 
   // Workspace layout (bytes, 256-aligned).
   auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
@@ -496,6 +524,11 @@ void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_
   anima_buffer norm_b = sub(ws, o_norm, S * dim * 2), q_b = sub(ws, o_q, S * dim * 2), k_b = sub(ws, o_k, S * dim * 2),
                v_b = sub(ws, o_v, S * dim * 2), a_b = sub(ws, o_a, S * dim * 2), br_b = sub(ws, o_b, S * dim * 2),
                ck_b = sub(ws, o_ck, T * dim * 2), cv_b = sub(ws, o_cv, T * dim * 2), h_b = sub(ws, o_h, S * hidden * 2);
+  if (cache) {
+    ck_b = anima_buffer{cache->k(block_index), T * dim * 2};
+    cv_b = anima_buffer{cache->v(block_index), T * dim * 2};
+  }
+  const bool cache_hit = cache && cache->ready(block_index);
 
   // Modulation (DiTBlockExecutor.encodeModulation, :1403-1417): SiLU(emb) -> W1 -> W2 -> + adaln_lora,
   // for the three branches at once: one launch for the W1 matvecs (SiLU applied to emb as it is
@@ -526,34 +559,43 @@ void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_
     const anima_buffer outs[3] = {q_b, k_b, v_b};
     linear_.encode_group(norm_b, ws3, outs, 3, S, ANIMA_FAMILY_ATTENTION_PROJECTION);
   }
-  anima_qk_prologue self_pro{w.self_q_norm, w.self_k_norm, a.eps, a.rope, S, 1, 1};
+  anima_qk_prologue self_pro{};
+  self_pro.q_norm_weight = w.self_q_norm; self_pro.k_norm_weight = w.self_k_norm; self_pro.eps = a.eps;
+  self_pro.rope = a.rope; self_pro.rope_tokens = S; self_pro.rope_q = 1; self_pro.rope_k = 1;
   att.query = q_b; att.key = k_b; att.value = v_b; att.output = a_b;
   att.query_count = S; att.key_count = S; att.prologue = &self_pro;
   attention_.encode(att);
   encode_linear_epilogue(linear_, a_b, 0, w.self_o, br_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION, GEMM_GATE_ADD,
                          residual, mods[0] + 2 * dim);
 
-  // Cross attention to the context (no RoPE; per-head RMSNorm on Q and K, run in the
-  // projections' output stage when the tiled GEMM takes them, else in the prologue).
+  // Cross attention to the context (no RoPE).  The per-head RMSNorm of Q and of the
+  // context K runs in the projections' output stage when the tiled GEMM takes them,
+  // else as an in-place pass right after; either way Q and K reach the attention
+  // normalised, so the cached K is the attention's input itself (CrossKVCache holds
+  // the post-norm K, DiTBlockExecutor.swift:1110-1161).
   launch_layernorm_modulate(residual, mods[1], static_cast<half_t*>(norm_b.ptr), dim, S, a.eps, dim, stream);
-  bool cq_fused, ckv_fused;
-  {
-    const anima_qweight* wq[1] = {&w.cross_q};
-    const anima_buffer oq[1] = {q_b};
-    const GemmEpilogueArgs eq[1] = {{GEMM_QK_NORM, static_cast<const half_t*>(w.cross_q_norm), a.eps}};
-    cq_fused = hd == 128 && linear_.encode_group(norm_b, wq, oq, 1, S, ANIMA_FAMILY_ATTENTION_PROJECTION, eq);
-    if (!cq_fused) linear_.encode(norm_b, 0, w.cross_q, q_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION);
+  linear_.encode_head_rmsnorm(norm_b, 0, w.cross_q, q_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION,
+                              static_cast<const half_t*>(w.cross_q_norm.ptr), hd, a.eps);
+  if (!cache_hit) {
     const anima_qweight* ws2[2] = {&w.cross_k, &w.cross_v};
     const anima_buffer outs[2] = {ck_b, cv_b};
-    const GemmEpilogueArgs ekv[2] = {{GEMM_QK_NORM, static_cast<const half_t*>(w.cross_k_norm), a.eps},
+    const GemmEpilogueArgs ekv[2] = {{GEMM_QK_NORM, static_cast<const half_t*>(w.cross_k_norm.ptr), a.eps},
                                      {GEMM_STORE, nullptr, 0.f}};
-    ckv_fused = hd == 128 && linear_.encode_group(a.context, ws2, outs, 2, T, ANIMA_FAMILY_ATTENTION_PROJECTION, ekv);
-    if (!ckv_fused) linear_.encode_group(a.context, ws2, outs, 2, T, ANIMA_FAMILY_ATTENTION_PROJECTION);
+    const bool fused = hd == 128 && linear_.encode_group(a.context, ws2, outs, 2, T, ANIMA_FAMILY_ATTENTION_PROJECTION, ekv);
+    if (!fused) {
+      linear_.encode_group(a.context, ws2, outs, 2, T, ANIMA_FAMILY_ATTENTION_PROJECTION);
+      PrologueParams pp{};
+      half_t* kx = static_cast<half_t*>(ck_b.ptr);
+      pp.in = kx; pp.in_tok = dim; pp.in_head = hd; pp.in_batch = T * dim;
+      pp.out = kx; pp.out_tok = dim; pp.out_head = hd; pp.out_batch = T * dim;
+      pp.batch = 1; pp.rows = (int)T; pp.heads = (int)H; pp.D = (int)hd;
+      pp.norm_w = static_cast<const half_t*>(w.cross_k_norm.ptr); pp.eps = a.eps; pp.rope = nullptr;
+      launch_prologue(pp, stream);
+    }
+    if (cache) cache->mark_ready(block_index);
   }
-  anima_qk_prologue cross_pro{cq_fused ? nullptr : w.cross_q_norm, ckv_fused ? nullptr : w.cross_k_norm, a.eps, nullptr,
-                              0, 0, 0};
   att.query = q_b; att.key = ck_b; att.value = cv_b; att.output = a_b;
-  att.query_count = S; att.key_count = T; att.prologue = (cq_fused && ckv_fused) ? nullptr : &cross_pro;
+  att.query_count = S; att.key_count = T; att.prologue = nullptr;
   attention_.encode(att);
   encode_linear_epilogue(linear_, a_b, 0, w.cross_o, br_b, 0, S, ANIMA_FAMILY_ATTENTION_PROJECTION, GEMM_GATE_ADD,
                          residual, mods[1] + 2 * dim);
@@ -564,6 +606,143 @@ void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_
   encode_linear_epilogue(linear_, h_b, 0, w.mlp2, br_b, 0, S, ANIMA_FAMILY_MLP_DOWN, GEMM_GATE_ADD, residual,
                          mods[2] + 2 * dim);
 }
+
+void DitBlockExecutor::forward(const anima_dit_block_weights* blocks, int64_t count, const anima_dit_block_args& a,
+                               CrossKVCache* cache) {
+  if (!blocks) fail(ANIMA_E_INVALID_ARGUMENT, "DiT forward block array is null");
+  if (count <= 0) fail(ANIMA_E_INVALID_SHAPE, "DiT forward needs at least one block");
+  if (cache && cache->blocks() < count) fail(ANIMA_E_INVALID_SHAPE, "cross K/V cache holds fewer blocks than the forward");
+  // Every block validates before the first launch.
+  for (int64_t i = 0; i < count; ++i) check(blocks[i], a, cache, i);
+  for (int64_t i = 0; i < count; ++i) encode(blocks[i], a, cache, i);
+}
+
+// Rebase one template buffer (ptr holds a byte offset into the block's range) onto
+// the slot the range was copied to.
+static anima_buffer rebase(const anima_buffer& t, char* base, int64_t range_bytes, const char* what) {
+  const uintptr_t off = reinterpret_cast<uintptr_t>(t.ptr);
+  if (off > (uintptr_t)range_bytes)
+    fail(ANIMA_E_OUT_OF_BOUNDS, std::string("streamed ") + what + " offset lies outside its block range");
+  return anima_buffer{base + off, range_bytes - (int64_t)off};
+}
+
+static anima_qweight rebase(const anima_qweight& t, char* base, int64_t range_bytes, const char* what) {
+  anima_qweight q = t;
+  q.packed = rebase(t.packed, base, range_bytes, what);
+  q.scale = rebase(t.scale, base, range_bytes, what);
+  q.zero = rebase(t.zero, base, range_bytes, what);
+  return q;
+}
+
+static anima_dit_block_weights rebase(const anima_dit_block_weights& t, char* base, int64_t range_bytes) {
+  anima_dit_block_weights w = t;
+  anima_qweight* dst[] = {&w.self_q, &w.self_k, &w.self_v, &w.self_o, &w.cross_q, &w.cross_k, &w.cross_v, &w.cross_o,
+                          &w.mlp1, &w.mlp2, &w.mod_self_w1, &w.mod_self_w2, &w.mod_cross_w1, &w.mod_cross_w2,
+                          &w.mod_mlp_w1, &w.mod_mlp_w2};
+  for (anima_qweight* q : dst) *q = rebase(*q, base, range_bytes, "weight");
+  w.self_q_norm = rebase(t.self_q_norm, base, range_bytes, "norm weight");
+  w.self_k_norm = rebase(t.self_k_norm, base, range_bytes, "norm weight");
+  w.cross_q_norm = rebase(t.cross_q_norm, base, range_bytes, "norm weight");
+  w.cross_k_norm = rebase(t.cross_k_norm, base, range_bytes, "norm weight");
+  return w;
+}
+
+void DitBlockExecutor::forward_streamed(WeightStreamer& st, const anima_dit_block_weights* templates,
+                                        const void* const* ranges, const int64_t* range_bytes, int64_t count,
+                                        const anima_dit_block_args& a, CrossKVCache* cache) {
+  if (!templates || !ranges || !range_bytes) fail(ANIMA_E_INVALID_ARGUMENT, "streamed DiT forward array is null");
+  if (count <= 0) fail(ANIMA_E_INVALID_SHAPE, "DiT forward needs at least one block");
+  if (st.context() != ctx_) fail(ANIMA_E_INVALID_ARGUMENT, "weight streamer belongs to another context");
+  if (cache && cache->blocks() < count) fail(ANIMA_E_INVALID_SHAPE, "cross K/V cache holds fewer blocks than the forward");
+  // Validate every block against the slot it will land in before anything is queued.
+  for (int64_t i = 0; i < count; ++i) {
+    if (!ranges[i]) fail(ANIMA_E_INVALID_ARGUMENT, "streamed block range pointer is null");
+    if (range_bytes[i] <= 0 || range_bytes[i] > st.capacity())
+      fail(ANIMA_E_OUT_OF_BOUNDS, "execution range does not fit the weight slot");
+    check(rebase(templates[i], st.slot((int)(i % st.slots())), range_bytes[i]), a, cache, i);
+  }
+  DeviceGuard guard(ctx_);
+  // DitForward.loopStep (DitForward.swift:21-35): with two or more slots block i runs from
+  // slot i % slots while the copy stream fills the slot of block i+1, last read by block
+  // i+1-slots <= i-1, whose release is already queued.  With one slot there is no look-ahead:
+  // block i is copied in only after block i-1's release (queued at the end of the previous
+  // iteration), so the copy waits for every kernel that still reads the slot.
+  st.load(0, ranges[0], range_bytes[0]);
+  for (int64_t i = 0; i < count; ++i) {
+    const int s = (int)(i % st.slots());
+    if (st.slots() == 1) {
+      if (i > 0) st.load(0, ranges[i], range_bytes[i]);
+    } else if (i + 1 < count) {
+      const int ns = (int)((i + 1) % st.slots());
+      st.load(ns, ranges[i + 1], range_bytes[i + 1]);
+    }
+    st.acquire(s);
+    encode(rebase(templates[i], st.slot(s), range_bytes[i]), a, cache, i);
+    st.release(s);
+  }
+}
+
+CrossKVCache::CrossKVCache(anima_ctx* ctx, int64_t blocks, int64_t tokens, int64_t dim)
+    : ctx_(ctx), blocks_(blocks), tokens_(tokens), dim_(dim) {
+  if (!(blocks > 0 && tokens > 0 && dim > 0)) fail(ANIMA_E_INVALID_SHAPE, "invalid cross K/V cache shape");
+  bytes_ = checked_product({blocks, 2, tokens, dim, 2}, "cross K/V cache");
+  ready_.assign((size_t)blocks, 0);
+  DeviceGuard guard(ctx_);
+  void* p = nullptr;
+  ANIMA_HIP(hipMalloc(&p, (size_t)bytes_));
+  base_ = static_cast<half_t*>(p);
+}
+
+CrossKVCache::~CrossKVCache() {
+  if (base_) (void)hipFree(base_);  // hipFree waits for outstanding work on the device
+}
+
+WeightStreamer::WeightStreamer(anima_ctx* ctx, int64_t capacity, int slots)
+    : ctx_(ctx), capacity_(capacity), slots_(slots) {
+  if (capacity <= 0) fail(ANIMA_E_INVALID_SHAPE, "weight ring capacity must be positive");
+  if (slots < 1 || slots > 4) fail(ANIMA_E_INVALID_ARGUMENT, "weight slot count must be in 1...4");
+  DeviceGuard guard(ctx_);
+  try {
+    for (int s = 0; s < slots_; ++s) {
+      void* p = nullptr;
+      ANIMA_HIP(hipMalloc(&p, (size_t)capacity_));
+      slot_[s] = static_cast<char*>(p);
+      ANIMA_HIP(hipEventCreateWithFlags(&loaded_[s], hipEventDisableTiming));
+      ANIMA_HIP(hipEventCreateWithFlags(&released_[s], hipEventDisableTiming));
+    }
+    ANIMA_HIP(hipStreamCreateWithFlags(&copy_, hipStreamNonBlocking));
+  } catch (...) {
+    this->~WeightStreamer();
+    throw;
+  }
+}
+
+WeightStreamer::~WeightStreamer() {
+  if (copy_) {
+    (void)hipStreamSynchronize(copy_);
+    (void)hipStreamDestroy(copy_);
+    copy_ = nullptr;
+  }
+  for (int s = 0; s < 4; ++s) {
+    if (slot_[s]) (void)hipFree(slot_[s]);
+    if (loaded_[s]) (void)hipEventDestroy(loaded_[s]);
+    if (released_[s]) (void)hipEventDestroy(released_[s]);
+    slot_[s] = nullptr;
+    loaded_[s] = released_[s] = nullptr;
+  }
+}
+
+void WeightStreamer::load(int s, const void* src, int64_t bytes) {
+  // released_[s] was last recorded after the kernels of the previous block in this slot
+  // were queued on the context stream (or never recorded: then the wait is a no-op).
+  ANIMA_HIP(hipStreamWaitEvent(copy_, released_[s], 0));
+  ANIMA_HIP(hipMemcpyAsync(slot_[s], src, (size_t)bytes, hipMemcpyHostToDevice, copy_));
+  ANIMA_HIP(hipEventRecord(loaded_[s], copy_));
+}
+
+void WeightStreamer::acquire(int s) { ANIMA_HIP(hipStreamWaitEvent(ctx_->stream, loaded_[s], 0)); }
+
+void WeightStreamer::release(int s) { ANIMA_HIP(hipEventRecord(released_[s], ctx_->stream)); }
 
 // ---------------------------------------------------------------------------
 // Qwen encoder layer (QwenLayerExecutor.execute, QwenEncoderMetal.swift:232-304),
@@ -586,11 +765,19 @@ void QwenLayerExecutor::encode(const anima_qwen_layer_weights& w, const anima_qw
   if (!(a.eps >= 0.f && std::isfinite(a.eps))) fail(ANIMA_E_INVALID_ARGUMENT, "Qwen layer epsilon must be finite");
   const int64_t rows = checked_product({B, S}, "Qwen layer");
   const int64_t qdim = H * D, kvdim = Hkv * D;
+  if (D % 2) fail(ANIMA_E_INVALID_SHAPE, "Qwen layer RoPE requires an even head_dim");
   if (checked_product({rows, hidden, 4}, "Qwen layer") > a.residual.length)
     fail(ANIMA_E_OUT_OF_BOUNDS, "invalid Qwen layer input buffers");
-  if (!a.rope) fail(ANIMA_E_INVALID_ARGUMENT, "Qwen layer requires a RoPE table");
-  if (!w.input_norm || !w.post_attention_norm || !w.q_norm || !w.k_norm)
+  if (!a.residual.ptr) fail(ANIMA_E_INVALID_ARGUMENT, "Qwen layer residual pointer is null");
+  if (!a.rope.ptr) fail(ANIMA_E_INVALID_ARGUMENT, "Qwen layer requires a RoPE table");
+  if (checked_product({S, D, 8}, "Qwen layer") > a.rope.length)
+    fail(ANIMA_E_OUT_OF_BOUNDS, "Qwen layer RoPE table is shorter than tokens rows");
+  if (!w.input_norm.ptr || !w.post_attention_norm.ptr || !w.q_norm.ptr || !w.k_norm.ptr)
     fail(ANIMA_E_INVALID_ARGUMENT, "Qwen layer norm weight pointer is null");
+  if (w.input_norm.length < checked_product({hidden, 2}, "Qwen layer") ||
+      w.post_attention_norm.length < checked_product({hidden, 2}, "Qwen layer") ||
+      w.q_norm.length < checked_product({D, 2}, "Qwen layer") || w.k_norm.length < checked_product({D, 2}, "Qwen layer"))
+    fail(ANIMA_E_OUT_OF_BOUNDS, "Qwen layer norm weight buffer is too short");
   auto need = [&](const anima_qweight& q, int64_t r, int64_t c, const char* nm) {
     if (q.rows != r || q.columns != c) fail(ANIMA_E_INVALID_SHAPE, std::string("invalid Qwen matrix ") + nm);
   };
@@ -620,13 +807,15 @@ void QwenLayerExecutor::encode(const anima_qwen_layer_weights& w, const anima_qw
   half_t* norm = static_cast<half_t*>(norm_b.ptr);
 
   // Attention branch (:244-282).
-  launch_rmsnorm_half(residual, static_cast<const half_t*>(w.input_norm), norm, hidden, rows, a.eps, stream);
+  launch_rmsnorm_half(residual, static_cast<const half_t*>(w.input_norm.ptr), norm, hidden, rows, a.eps, stream);
   {
     const anima_qweight* ws3[3] = {&w.q, &w.k, &w.v};
     const anima_buffer outs[3] = {q_b, k_b, v_b};
     linear_.encode_group(norm_b, ws3, outs, 3, rows, ANIMA_FAMILY_ATTENTION_PROJECTION);
   }
-  anima_qk_prologue pro{w.q_norm, w.k_norm, a.eps, a.rope, S, 1, 1};
+  anima_qk_prologue pro{};
+  pro.q_norm_weight = w.q_norm; pro.k_norm_weight = w.k_norm; pro.eps = a.eps;
+  pro.rope = a.rope; pro.rope_tokens = S; pro.rope_q = 1; pro.rope_k = 1;
   anima_attention_args att{};
   att.query = q_b; att.key = k_b; att.value = v_b; att.output = att_b;
   att.heads = H; att.key_value_heads = Hkv; att.head_dim = D; att.query_count = S; att.key_count = S;
@@ -637,7 +826,8 @@ void QwenLayerExecutor::encode(const anima_qwen_layer_weights& w, const anima_qw
                          residual, nullptr);
 
   // MLP branch (:284-302): gate/up -> SwiGLU (into the gate buffer) -> down.
-  launch_rmsnorm_half(residual, static_cast<const half_t*>(w.post_attention_norm), norm, hidden, rows, a.eps, stream);
+  launch_rmsnorm_half(residual, static_cast<const half_t*>(w.post_attention_norm.ptr), norm, hidden, rows, a.eps,
+                      stream);
   {
     const anima_qweight* ws2[2] = {&w.gate, &w.up};
     const anima_buffer outs[2] = {gate_b, up_b};

@@ -162,6 +162,14 @@ class LinearExecutor {
   // and returns false.  Without epi it always encodes and returns true.
   bool encode_group(anima_buffer input, const anima_qweight* const* weights, const anima_buffer* outputs, int count,
                     int64_t input_rows, int32_t family, const GemmEpilogueArgs* epi = nullptr);
+  // encode() followed by the per-head RMSNorm of the output (rmsnorm_heads_half,
+  // AnimaKernels.metal:660-689) over heads of head_dim columns with the fp16 weight
+  // norm_w: in the ping-pong GEMM's output stage when it takes the shape and
+  // head_dim is 128, else as a second, in-place pass.  norm_w's range is the
+  // caller's to check.
+  void encode_head_rmsnorm(anima_buffer input, int64_t input_offset, const anima_qweight& weight, anima_buffer output,
+                           int64_t output_offset, int64_t input_rows, int32_t family, const half_t* norm_w,
+                           int64_t head_dim, float eps);
   anima_ctx* context() const { return ctx_; }
 
  private:

@@ -1,7 +1,9 @@
 // Host side of the linear executor: LinearExecutor.validate
 // (AnimaXS/Runtime/Metal/LinearExecutor.swift:412-438) and dispatch.
+#include <cmath>
 #include <string>
 
+#include "attention.hpp"
 #include "linear.hpp"
 
 namespace anima {
@@ -181,6 +183,32 @@ bool LinearExecutor::encode_fused(anima_buffer input, int64_t input_offset, cons
   }
   launch_pingpong(p, w.storage, ctx_->stream);
   return true;
+}
+
+void LinearExecutor::encode_head_rmsnorm(anima_buffer input, int64_t input_offset, const anima_qweight& weight,
+                                         anima_buffer output, int64_t output_offset, int64_t input_rows,
+                                         int32_t family, const half_t* norm_w, int64_t head_dim, float eps) {
+  if (!(head_dim > 0 && weight.rows > 0 && weight.rows % head_dim == 0))
+    fail(ANIMA_E_INVALID_SHAPE, "per-head RMSNorm requires weight rows to be a multiple of head_dim");
+  if (head_dim > 512) fail(ANIMA_E_UNSUPPORTED, "per-head RMSNorm supports head_dim <= 512");
+  if (!(eps >= 0.f && std::isfinite(eps))) fail(ANIMA_E_INVALID_ARGUMENT, "RMSNorm epsilon must be finite and >= 0");
+  if (!norm_w) fail(ANIMA_E_INVALID_ARGUMENT, "per-head RMSNorm weight pointer is null");
+  if (head_dim == 128 && input_offset == 0 && output_offset == 0) {
+    const anima_qweight* ws1[1] = {&weight};
+    const GemmEpilogueArgs epi[1] = {{GEMM_QK_NORM, norm_w, eps}};
+    if (encode_group(input, ws1, &output, 1, input_rows, family, epi)) return;
+  }
+  encode(input, input_offset, weight, output, output_offset, input_rows, family);
+  // In place on the [rows, weight.rows] output just written (ranges checked by encode()):
+  // every element is read and rewritten by the same lane.
+  DeviceGuard guard(ctx_);
+  PrologueParams pp{};
+  half_t* y = reinterpret_cast<half_t*>(byte_ptr_mut(output, output_offset));
+  pp.in = y; pp.in_tok = weight.rows; pp.in_head = head_dim; pp.in_batch = input_rows * weight.rows;
+  pp.out = y; pp.out_tok = weight.rows; pp.out_head = head_dim; pp.out_batch = input_rows * weight.rows;
+  pp.batch = 1; pp.rows = (int)input_rows; pp.heads = (int)(weight.rows / head_dim); pp.D = (int)head_dim;
+  pp.norm_w = norm_w; pp.eps = eps; pp.rope = nullptr;
+  launch_prologue(pp, ctx_->stream);
 }
 
 void encode_matvec(anima_ctx* ctx, const anima_qweight& weight, anima_buffer input, int64_t input_offset,

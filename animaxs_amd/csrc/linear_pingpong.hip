@@ -657,7 +657,9 @@ void launch_pingpong_group(const GemmParams* ps, int count, int storage, hipStre
     const GemmParams& p = ps[0];
     const int64_t n = (int64_t)p.M * p.N;
     float* res = p.epilogue == GEMM_RESIDUAL_ADD ? p.residual : nullptr;
-    const int vec = (res ? aligned16(res) : aligned8(p.y)) ? 1 : 0;
+    // The vector form reads split s at part + s*n + i0 as 16 bytes: aligned for every
+    // split only when n is a multiple of 4.
+    const int vec = (n % 4 == 0 && aligned16(p.part) && (res ? aligned16(res) : aligned8(p.y))) ? 1 : 0;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, stream, p.part, p.y, res,
                        n, p.ksplit, vec);
     ANIMA_HIP(hipGetLastError());

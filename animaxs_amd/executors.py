@@ -32,10 +32,15 @@ from ._abi import AnimaError, call
 __all__ = [
     "AnimaError", "Context", "AttentionExecutor", "LinearExecutor", "QuantizedLinearWeightBuffers",
     "QKPrologue", "QuantDecoders", "DitRoPE", "qwen_rope", "DiTBlockExecutor", "BlockOps", "as_buffer",
+    "CrossKVCache", "WeightStreamer", "QwenLayerExecutor",
 ]
 
 
 def as_buffer(x: Any) -> _abi.Buffer:
+    """A device buffer for the C ABI.  Tensors must be contiguous and on the GPU: the
+    length is ``numel * element_size`` from ``data_ptr``, which is the tensor's real
+    extent only for a contiguous layout (an expanded or strided view would claim bytes
+    it does not own), and a host pointer must never reach a kernel."""
     if x is None:
         return _abi.Buffer(None, 0)
     if isinstance(x, _abi.Buffer):
@@ -43,6 +48,10 @@ def as_buffer(x: Any) -> _abi.Buffer:
     if isinstance(x, tuple):
         return _abi.Buffer(C.c_void_p(int(x[0])), int(x[1]))
     if hasattr(x, "data_ptr"):
+        if getattr(x, "is_cuda", False) is not True:
+            raise TypeError("device buffers must be GPU tensors (got a host tensor)")
+        if not x.is_contiguous():
+            raise TypeError("device buffers must be contiguous tensors (got a strided or expanded view)")
         return _abi.Buffer(C.c_void_p(x.data_ptr()), int(x.numel() * x.element_size()))
     raise TypeError(f"cannot use {type(x)!r} as a device buffer")
 
@@ -97,7 +106,9 @@ _BACKENDS = {"auto": _abi.ATTN_AUTO, "flash": _abi.ATTN_FLASH, "generic": _abi.A
 
 @dataclass
 class QKPrologue:
-    """Fused per-head RMSNorm (+ split-half RoPE) applied to Q and K."""
+    """Fused per-head RMSNorm (+ split-half RoPE) applied to Q and K.  ``k_rope`` is an
+    optional separate table for the keys (the LLM adapter's cross attention rotates its
+    context keys with the context positions, LLMAdapterMetal.swift:336-340)."""
     q_norm_weight: Any = None
     k_norm_weight: Any = None
     eps: float = 1e-6
@@ -105,11 +116,13 @@ class QKPrologue:
     rope_tokens: int = 0
     rope_q: bool = True
     rope_k: bool = True
+    k_rope: Any = None
+    k_rope_tokens: int = 0
 
     def to_c(self) -> _abi.QKPrologue:
-        return _abi.QKPrologue(_ptr(self.q_norm_weight), _ptr(self.k_norm_weight), float(self.eps),
-                               _ptr(self.rope), int(self.rope_tokens), int(bool(self.rope_q)),
-                               int(bool(self.rope_k)))
+        return _abi.QKPrologue(as_buffer(self.q_norm_weight), as_buffer(self.k_norm_weight), float(self.eps),
+                               as_buffer(self.rope), int(self.rope_tokens), int(bool(self.rope_q)),
+                               int(bool(self.rope_k)), as_buffer(self.k_rope), int(self.k_rope_tokens))
 
 
 class AttentionExecutor:
@@ -265,6 +278,16 @@ class LinearExecutor:
              as_buffer(output), int(output_offset), int(input_rows), _FAMILY[family], _EPILOGUE[epilogue],
              as_buffer(residual), as_buffer(gate))
 
+    def encode_head_rmsnorm(self, input, weight: QuantizedLinearWeightBuffers, output, input_rows: int,
+                            norm_weight, head_dim: int = 128, eps: float = 1e-6, input_offset: int = 0,
+                            output_offset: int = 0, family: str = "attentionProjection") -> None:
+        """encode() followed by rmsnorm_heads_half on the output (the cross-attention Q /
+        context-K projections of DiTBlockExecutor.swift:1103-1161)."""
+        w = weight.to_c()
+        call("anima_linear_encode_head_rmsnorm", self._h, as_buffer(input), int(input_offset), C.byref(w),
+             as_buffer(output), int(output_offset), int(input_rows), _FAMILY[family], as_buffer(norm_weight),
+             int(head_dim), float(eps))
+
     def execute(self, input, weight: QuantizedLinearWeightBuffers, output, input_rows: int,
                 input_offset: int = 0, output_offset: int = 0, family: str = "other") -> None:
         w = weight.to_c()
@@ -409,11 +432,79 @@ class BlockOps:
         call("anima_add_f32_encode", self.context.handle, as_buffer(destination), as_buffer(source), int(count))
 
 
+class CrossKVCache:
+    """CrossKVCache (DiTBlockExecutor.swift:19-43): per-block cross-attention K/V of the
+    fixed context, reused exactly by every sampler step of one generation."""
+
+    def __init__(self, context: Context, blocks: int, context_tokens: int = 512, dim: int = 2048):
+        h = C.c_void_p()
+        call("anima_cross_kv_cache_create", context.handle, int(blocks), int(context_tokens), int(dim), C.byref(h))
+        self._h = h
+        self.blocks = blocks
+
+    @property
+    def handle(self) -> C.c_void_p:
+        return self._h
+
+    def reset(self) -> None:
+        call("anima_cross_kv_cache_reset", self._h)
+
+    def is_ready(self, block: int) -> bool:
+        r = C.c_int32()
+        call("anima_cross_kv_cache_is_ready", self._h, int(block), C.byref(r))
+        return bool(r.value)
+
+    def bytes(self) -> int:
+        n = C.c_int64()
+        call("anima_cross_kv_cache_bytes", self._h, C.byref(n))
+        return n.value
+
+    def close(self):
+        if self._h:
+            call("anima_cross_kv_cache_destroy", self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class WeightStreamer:
+    """WeightStreamer (WeightStreamer.swift:87-213): ``slots`` device slots of ``capacity``
+    bytes filled from host block ranges on a copy stream."""
+
+    def __init__(self, context: Context, capacity: int, slots: int = 2):
+        h = C.c_void_p()
+        call("anima_weight_streamer_create", context.handle, int(capacity), int(slots), C.byref(h))
+        self._h = h
+        self.capacity = capacity
+        self.slots = slots
+
+    @property
+    def handle(self) -> C.c_void_p:
+        return self._h
+
+    def close(self):
+        if self._h:
+            call("anima_weight_streamer_destroy", self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class DiTBlockExecutor:
-    """One DiT block (DiTBlockExecutor.execute, :155-282); fp32 residual updated in place."""
+    """One DiT block (DiTBlockExecutor.execute, :155-282); fp32 residual updated in place.
+    ``forward`` is DitForward.execute (DitForward.swift:78-112) over a list of blocks."""
 
     NAMES = ("self_q", "self_k", "self_v", "self_o", "cross_q", "cross_k", "cross_v", "cross_o", "mlp1", "mlp2",
              "mod_self_w1", "mod_self_w2", "mod_cross_w1", "mod_cross_w2", "mod_mlp_w1", "mod_mlp_w2")
+    NORMS = ("self_q_norm", "self_k_norm", "cross_q_norm", "cross_k_norm")
 
     def __init__(self, context: Context):
         h = C.c_void_p()
@@ -421,18 +512,51 @@ class DiTBlockExecutor:
         self._h = h
         self.context = context
 
-    def encode(self, weights: dict, norms: dict, residual, emb, adaln_lora, context_tokens_buf, rope,
-               tokens: int, dim: int = 2048, heads: int = 16, head_dim: int = 128, context_tokens: int = 512,
-               context_dim: int = 1024, mlp_hidden: int = 8192, eps: float = 1e-6) -> None:
+    @classmethod
+    def weights_struct(cls, weights: dict, norms: dict) -> _abi.DitBlockWeights:
         w = _abi.DitBlockWeights()
-        for n in self.NAMES:
+        for n in cls.NAMES:
             setattr(w, n, weights[n].to_c())
-        for n in ("self_q_norm", "self_k_norm", "cross_q_norm", "cross_k_norm"):
-            setattr(w, n, _ptr(norms[n]))
-        a = _abi.DitBlockArgs(as_buffer(residual), as_buffer(emb), as_buffer(adaln_lora), as_buffer(context_tokens_buf),
-                              _ptr(rope), int(tokens), int(dim), int(heads), int(head_dim), int(context_tokens),
-                              int(context_dim), int(mlp_hidden), float(eps))
-        call("anima_dit_block_encode", self._h, C.byref(w), C.byref(a))
+        for n in cls.NORMS:
+            setattr(w, n, as_buffer(norms[n]))
+        return w
+
+    @staticmethod
+    def args_struct(residual, emb, adaln_lora, context_tokens_buf, rope, tokens: int, dim: int = 2048,
+                    heads: int = 16, head_dim: int = 128, context_tokens: int = 512, context_dim: int = 1024,
+                    mlp_hidden: int = 8192, eps: float = 1e-6) -> _abi.DitBlockArgs:
+        return _abi.DitBlockArgs(as_buffer(residual), as_buffer(emb), as_buffer(adaln_lora),
+                                 as_buffer(context_tokens_buf), as_buffer(rope), int(tokens), int(dim), int(heads),
+                                 int(head_dim), int(context_tokens), int(context_dim), int(mlp_hidden), float(eps))
+
+    def encode(self, weights: dict, norms: dict, residual, emb, adaln_lora, context_tokens_buf, rope,
+               tokens: int, cache: Optional[CrossKVCache] = None, block_index: int = 0, **shape) -> None:
+        w = self.weights_struct(weights, norms)
+        a = self.args_struct(residual, emb, adaln_lora, context_tokens_buf, rope, tokens, **shape)
+        if cache is None:
+            call("anima_dit_block_encode", self._h, C.byref(w), C.byref(a))
+        else:
+            call("anima_dit_block_encode_cached", self._h, C.byref(w), C.byref(a), cache.handle, int(block_index))
+
+    def forward(self, blocks: list, residual, emb, adaln_lora, context_tokens_buf, rope, tokens: int,
+                cache: Optional[CrossKVCache] = None, **shape) -> None:
+        """``blocks`` is a list of (weights, norms) pairs, run in order over the residual."""
+        arr = (_abi.DitBlockWeights * len(blocks))(*[self.weights_struct(w, n) for w, n in blocks])
+        a = self.args_struct(residual, emb, adaln_lora, context_tokens_buf, rope, tokens, **shape)
+        call("anima_dit_forward_encode", self._h, arr, len(blocks), C.byref(a), cache.handle if cache else None)
+
+    def forward_streamed(self, streamer: WeightStreamer, templates: list, host_ranges: list, residual, emb,
+                         adaln_lora, context_tokens_buf, rope, tokens: int, cache: Optional[CrossKVCache] = None,
+                         **shape) -> None:
+        """``templates[i]`` is a DitBlockWeights whose device pointers hold byte offsets into
+        ``host_ranges[i]`` (an (address, length) pair of host memory)."""
+        n = len(templates)
+        arr = (_abi.DitBlockWeights * n)(*templates)
+        ptrs = (C.c_void_p * n)(*[C.c_void_p(int(r[0])) for r in host_ranges])
+        lens = (C.c_int64 * n)(*[int(r[1]) for r in host_ranges])
+        a = self.args_struct(residual, emb, adaln_lora, context_tokens_buf, rope, tokens, **shape)
+        call("anima_dit_forward_encode_streamed", self._h, streamer.handle, arr, C.cast(ptrs, C.c_void_p),
+             C.cast(lens, C.c_void_p), n, C.byref(a), cache.handle if cache else None)
 
     def close(self):
         if self._h:
@@ -465,13 +589,13 @@ class QwenLayerExecutor:
         for n in self.NAMES:
             setattr(w, n, weights[n].to_c())
         for n in ("input_norm", "post_attention_norm", "q_norm", "k_norm"):
-            setattr(w, n, _ptr(norms[n]))
+            setattr(w, n, as_buffer(norms[n]))
         keep = None
         kl = None
         if key_lengths is not None:
             keep = np.ascontiguousarray(np.asarray(key_lengths, dtype=np.int32))
             kl = C.c_void_p(keep.ctypes.data)
-        a = _abi.QwenLayerArgs(as_buffer(residual), _ptr(rope), kl, int(batch), int(tokens), int(hidden),
+        a = _abi.QwenLayerArgs(as_buffer(residual), as_buffer(rope), kl, int(batch), int(tokens), int(hidden),
                                int(heads), int(kv_heads), int(head_dim), int(intermediate), float(eps))
         call("anima_qwen_layer_encode", self._h, C.byref(w), C.byref(a))
         del keep

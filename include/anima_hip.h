@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ANIMA_HIP_ABI_VERSION 2
+#define ANIMA_HIP_ABI_VERSION 3
 
 /* Status codes.  The reference throws AnimapkError.validation(String)
  * (Runtime/Animapk/MappedFile.swift:14) for every failure; the codes split that
@@ -126,18 +126,23 @@ anima_status anima_attention_destroy(anima_attention* attn);
 
 /* Fused per-head Q/K prologue: RMSNorm with a shared [head_dim] fp16 weight
  * (rmsnorm_heads_half, AnimaKernels.metal:660-689) and/or split-half RoPE on the
- * pairs (p, p+head_dim/2) from an fp32 [rope_tokens][head_dim/2][2][2] table of
- * [cos,-sin,sin,cos] blocks (rms_rope_split_half, AnimaKernels.metal:696-729).
- * Pointers are device pointers; NULL disables that step.  Query row r uses table
- * row r, key row r uses table row r (rope_tokens >= max(query_count, key_count)). */
+ * pairs (p, p+head_dim/2) from an fp32 [tokens][head_dim/2][2][2] table of
+ * [cos,-sin,sin,cos] blocks (rms_rope_split_half, AnimaKernels.metal:696-729;
+ * rms_rope_adapter64, :733-763).  Each table or weight is a device buffer whose
+ * length is checked before launch; a NULL ptr disables that step.  Query row r
+ * uses row r of `rope`; key row r uses row r of `k_rope` when its ptr is set (the
+ * LLM adapter's cross attention rotates its context keys with the context's own
+ * positions, LLMAdapterMetal.swift:336-340, 383-397), else row r of `rope`. */
 typedef struct anima_qk_prologue {
-  const void* q_norm_weight;   /* fp16 [head_dim] or NULL */
-  const void* k_norm_weight;   /* fp16 [head_dim] or NULL */
+  anima_buffer q_norm_weight;  /* fp16 [head_dim] (ptr NULL: no Q RMSNorm) */
+  anima_buffer k_norm_weight;  /* fp16 [head_dim] (ptr NULL: no K RMSNorm) */
   float eps;                   /* RMSNorm epsilon (DiT and Qwen use 1e-6) */
-  const float* rope;           /* fp32 table or NULL (no RoPE, e.g. cross attention) */
-  int64_t rope_tokens;
+  anima_buffer rope;           /* fp32 [rope_tokens][head_dim/2][2][2] (ptr NULL: no RoPE) */
+  int64_t rope_tokens;         /* rows of `rope` (>= query_count, and >= key_count when it serves K) */
   int32_t rope_q;              /* apply RoPE to Q (1) */
   int32_t rope_k;              /* apply RoPE to K (1) */
+  anima_buffer k_rope;         /* optional fp32 [k_rope_tokens][head_dim/2][2][2] for K */
+  int64_t k_rope_tokens;       /* rows of `k_rope` (>= key_count) */
 } anima_qk_prologue;
 
 /* AttentionExecutor.encode (AttentionExecutor.swift:122-133).  The first block of
@@ -284,6 +289,19 @@ anima_status anima_linear_encode_group(anima_linear* lin, anima_buffer input, co
                                        const anima_buffer* outputs, int32_t count, int64_t input_rows,
                                        int32_t family);
 
+/* Extension, no reference entry point: a linear followed by the per-head RMSNorm
+ * that DiTBlockExecutor encodes on the cross-attention Q and context-K projections
+ * (linear.encode + encodeRMSHeads / rmsnorm_heads_half, DiTBlockExecutor.swift:
+ * 1103-1161, AnimaKernels.metal:660-689): output[r, h*head_dim + d] =
+ * half(y[d] * rsqrt(mean_d(y^2) + eps) * norm_weight[d]) with y = half(linear(input))
+ * restricted to head h.  weight.rows must be a multiple of head_dim; norm_weight is
+ * fp16 [head_dim].  The tiled GEMM applies the norm in its output stage for
+ * head_dim 128; otherwise the GEMM runs, then the norm in place. */
+anima_status anima_linear_encode_head_rmsnorm(anima_linear* lin, anima_buffer input, int64_t input_offset,
+                                              const anima_qweight* weight, anima_buffer output,
+                                              int64_t output_offset, int64_t input_rows, int32_t family,
+                                              anima_buffer norm_weight, int64_t head_dim, float eps);
+
 /* M=1 fp32 matvec w4_matvec_f32 / w8_matvec_f32 / fp16_matvec_f32
  * (AnimaKernels.metal:804-933; DiTQuantizedWeightFactory.matvecKernel,
  * LinearExecutor.swift:520-528): output_f32[N] = deq(W)[N,K] . input_f32[K]. */
@@ -356,8 +374,8 @@ typedef struct anima_dit_block_weights {
   anima_qweight mlp1, mlp2;
   /* modulation W1 [256, dim] and W2 [3*dim, 256] per branch (fp16/W4/W8) */
   anima_qweight mod_self_w1, mod_self_w2, mod_cross_w1, mod_cross_w2, mod_mlp_w1, mod_mlp_w2;
-  const void* self_q_norm; const void* self_k_norm;   /* fp16 [head_dim] */
-  const void* cross_q_norm; const void* cross_k_norm; /* fp16 [head_dim] */
+  anima_buffer self_q_norm, self_k_norm;    /* fp16 [head_dim] each, required */
+  anima_buffer cross_q_norm, cross_k_norm;  /* fp16 [head_dim] each, required */
 } anima_dit_block_weights;
 
 typedef struct anima_dit_block_args {
@@ -365,7 +383,7 @@ typedef struct anima_dit_block_args {
   anima_buffer emb;            /* fp32 [dim] timestep embedding */
   anima_buffer adaln_lora;     /* fp32 [3*dim] */
   anima_buffer context;        /* fp16 [context_tokens, context_dim] */
-  const float* rope;           /* device fp32 [tokens][64][2][2] */
+  anima_buffer rope;           /* fp32 [tokens][head_dim/2][2][2] (anima_rope_dit3d) */
   int64_t tokens, dim, heads, head_dim, context_tokens, context_dim, mlp_hidden;
   float eps;
 } anima_dit_block_args;
@@ -375,6 +393,62 @@ anima_status anima_dit_block_create(anima_ctx* ctx, anima_dit_block** out);
 anima_status anima_dit_block_destroy(anima_dit_block* blk);
 anima_status anima_dit_block_encode(anima_dit_block* blk, const anima_dit_block_weights* w,
                                     const anima_dit_block_args* args);
+
+/* CrossKVCache (DiTBlockExecutor.swift:19-43, used at :1110-1161): the cross-
+ * attention K (after its per-head RMSNorm) and V of every block, computed from the
+ * fixed context the first time a block runs and reused, exactly, by every later
+ * sampler step of the same generation.  One device allocation of
+ * blocks * 2 * context_tokens * dim fp16 owned by the cache; the attention reads
+ * the cached rows in place (the reference copies them back into scratch).  The
+ * cache belongs to one prompt: call reset when the context changes. */
+typedef struct anima_cross_kv_cache anima_cross_kv_cache;
+anima_status anima_cross_kv_cache_create(anima_ctx* ctx, int64_t blocks, int64_t context_tokens, int64_t dim,
+                                         anima_cross_kv_cache** out);
+anima_status anima_cross_kv_cache_destroy(anima_cross_kv_cache* cache);
+/* Every block misses again on its next run (a new prompt). */
+anima_status anima_cross_kv_cache_reset(anima_cross_kv_cache* cache);
+anima_status anima_cross_kv_cache_is_ready(const anima_cross_kv_cache* cache, int64_t block, int32_t* ready);
+anima_status anima_cross_kv_cache_bytes(const anima_cross_kv_cache* cache, int64_t* bytes);
+
+/* anima_dit_block_encode as block `block_index` of a forward that shares `cache`
+ * (NULL: no cache, identical to anima_dit_block_encode).  On a miss the block
+ * projects the context into the cache slot and marks it ready; on a hit it skips
+ * the context K/V projections and their norm.  Hit and miss give identical bits. */
+anima_status anima_dit_block_encode_cached(anima_dit_block* blk, const anima_dit_block_weights* w,
+                                           const anima_dit_block_args* args, anima_cross_kv_cache* cache,
+                                           int64_t block_index);
+
+/* DitForward.execute (DitForward.swift:78-112): blocks[0..block_count) in order over
+ * the residual, weights resident in device memory (the whole W4 DiT is ~1 GB, so on
+ * this part every block stays in HBM and nothing is streamed).  cache may be NULL. */
+anima_status anima_dit_forward_encode(anima_dit_block* blk, const anima_dit_block_weights* blocks,
+                                      int64_t block_count, const anima_dit_block_args* args,
+                                      anima_cross_kv_cache* cache);
+
+/* WeightStreamer (WeightStreamer.swift:87-213) for callers that keep the packed
+ * blocks in host memory: `slots` (1..4) device slots of `capacity` bytes and a copy
+ * stream.  Block i's host range is copied into slot i % slots on the copy stream
+ * while earlier blocks compute; an event per slot makes the compute stream wait
+ * for the copy, and the copy for the last block that read the slot, so a slot is
+ * never overwritten in flight (the reference's markInFlight/complete, enforced on
+ * the device instead of by host waits).  Host ranges should be pinned
+ * (hipHostMalloc) for the copies to overlap with compute. */
+typedef struct anima_weight_streamer anima_weight_streamer;
+anima_status anima_weight_streamer_create(anima_ctx* ctx, int64_t capacity, int32_t slots,
+                                          anima_weight_streamer** out);
+anima_status anima_weight_streamer_destroy(anima_weight_streamer* streamer);
+
+/* DitForward.execute with streamed weights.  templates[i] describes block i with
+ * every device pointer (qweight packed/scale/zero ptr, norm ptr) holding a byte
+ * offset from the start of host_ranges[i] instead of an address, and lengths
+ * ignored: the library rebases them onto the slot the range lands in
+ * (DiTQuantizedWeightFactory.makeMatrix binds ring + tensor offset the same way,
+ * LinearExecutor.swift:467-518).  range_bytes[i] <= the streamer's capacity. */
+anima_status anima_dit_forward_encode_streamed(anima_dit_block* blk, anima_weight_streamer* streamer,
+                                               const anima_dit_block_weights* templates,
+                                               const void* const* host_ranges, const int64_t* range_bytes,
+                                               int64_t block_count, const anima_dit_block_args* args,
+                                               anima_cross_kv_cache* cache);
 
 /* ------------------------------------------------------------------------- */
 /* Qwen encoder layer: QwenLayerExecutor.execute (QwenEncoderMetal.swift:232-304)  */
@@ -394,15 +468,15 @@ anima_status anima_add_half_into_float_encode(anima_ctx* ctx, anima_buffer resid
 
 typedef struct anima_qwen_layer_weights {
   anima_qweight q, k, v, o, gate, up, down;  /* W8 in the reference; W4/W8/FP16 accepted */
-  const void* input_norm;            /* fp16 [hidden] */
-  const void* post_attention_norm;   /* fp16 [hidden] */
-  const void* q_norm;                /* fp16 [head_dim] */
-  const void* k_norm;                /* fp16 [head_dim] */
+  anima_buffer input_norm;           /* fp16 [hidden], required */
+  anima_buffer post_attention_norm;  /* fp16 [hidden], required */
+  anima_buffer q_norm;               /* fp16 [head_dim], required */
+  anima_buffer k_norm;               /* fp16 [head_dim], required */
 } anima_qwen_layer_weights;
 
 typedef struct anima_qwen_layer_args {
   anima_buffer residual;        /* fp32 [batch][tokens][hidden], updated in place */
-  const float* rope;            /* device fp32 [tokens][head_dim/2][2][2] (anima_rope_neox) */
+  anima_buffer rope;            /* fp32 [tokens][head_dim/2][2][2] (anima_rope_neox) */
   const int32_t* key_lengths;   /* host, per sequence, 1..tokens; NULL = every token valid */
   int64_t batch, tokens, hidden, heads, kv_heads, head_dim, intermediate;
   float eps;

@@ -143,9 +143,12 @@ BLOCK_LINEARS = [
 
 
 def dit_block(S: int = 4096, ctx_tokens: int = 512, ctx_dim: int = 1024,
-              hidden: int = 8192, dim: int = DIM) -> dict:
-    """Workload 5 (``S`` may be reduced for fast tests; it must be a square grid)."""
+              hidden: int = 8192, dim: int = DIM, seed: int | None = None) -> dict:
+    """Workload 5 (``S`` may be reduced for fast tests; it must be a square grid).
+    ``seed`` replaces the workload seed (other blocks of a multi-block forward)."""
     g = _gen(5)
+    if seed is not None:
+        g.manual_seed(seed)
     side = int(round(S ** 0.5))
     assert side * side == S
     d = {

@@ -217,13 +217,154 @@ def _qwen_weights(hidden=64, qdim=128, kvdim=64, inter=96, bad=None):
 
 def test_qwen_layer_validation(ctx):
     layer = animaxs_amd.QwenLayerExecutor(ctx)
-    norms_ = {n: FAKE for n in ("input_norm", "post_attention_norm", "q_norm", "k_norm")}
+    norms_ = {"input_norm": buf(64 * 2), "post_attention_norm": buf(64 * 2), "q_norm": buf(64 * 2),
+              "k_norm": buf(64 * 2)}
+    rope = buf(4 * 64 * 8)
     kw = dict(batch=2, tokens=4, hidden=64, heads=2, kv_heads=1, head_dim=64, intermediate=96)
-    expect(lambda: layer.encode(_qwen_weights(), norms_, buf(2 * 4 * 64 * 4 - 4), FAKE, **kw),
+    expect(lambda: layer.encode(_qwen_weights(), norms_, buf(2 * 4 * 64 * 4 - 4), rope, **kw),
            _abi.E_OUT_OF_BOUNDS, "invalid Qwen layer input buffers")
-    expect(lambda: layer.encode(_qwen_weights(bad="down"), norms_, buf(2 * 4 * 64 * 4), FAKE, **kw),
+    expect(lambda: layer.encode(_qwen_weights(bad="down"), norms_, buf(2 * 4 * 64 * 4), rope, **kw),
            _abi.E_INVALID_SHAPE, "invalid Qwen matrix down")
-    expect(lambda: layer.encode(_qwen_weights(), norms_, buf(2 * 4 * 64 * 4), FAKE, **dict(kw, kv_heads=3)),
+    expect(lambda: layer.encode(_qwen_weights(), norms_, buf(2 * 4 * 64 * 4), rope, **dict(kw, kv_heads=3)),
            _abi.E_INVALID_SHAPE, "invalid Qwen layer shape")
     expect(lambda: layer.encode(_qwen_weights(), norms_, buf(2 * 4 * 64 * 4), None, **kw),
            _abi.E_INVALID_ARGUMENT, "requires a RoPE table")
+    expect(lambda: layer.encode(_qwen_weights(), norms_, buf(2 * 4 * 64 * 4), buf(4 * 64 * 8 - 4), **kw),
+           _abi.E_OUT_OF_BOUNDS, "RoPE table is shorter")
+    for n in norms_:
+        short = dict(norms_, **{n: buf(norms_[n][1] - 2)})
+        expect(lambda: layer.encode(_qwen_weights(), short, buf(2 * 4 * 64 * 4), rope, **kw),
+               _abi.E_OUT_OF_BOUNDS, "norm weight buffer is too short")
+        null = dict(norms_, **{n: None})
+        expect(lambda: layer.encode(_qwen_weights(), null, buf(2 * 4 * 64 * 4), rope, **kw),
+               _abi.E_INVALID_ARGUMENT, "norm weight pointer is null")
+
+
+# --------------------------------------------------------------------------------------
+# Q/K prologue buffers (lengths checked before launch).
+# --------------------------------------------------------------------------------------
+
+def test_prologue_buffer_lengths(ctx):
+    ex = animaxs_amd.AttentionExecutor(ctx)
+    P = animaxs_amd.QKPrologue
+    D = 64
+    expect(lambda: ex.encode(**attn_kw(prologue=P(q_norm_weight=buf(D * 2 - 2)))), _abi.E_OUT_OF_BOUNDS,
+           "Q RMSNorm weight holds fewer than head_dim")
+    expect(lambda: ex.encode(**attn_kw(prologue=P(k_norm_weight=buf(D * 2 - 2)))), _abi.E_OUT_OF_BOUNDS,
+           "K RMSNorm weight holds fewer than head_dim")
+    # 4 tokens of [32][2][2] fp32 = 4 * 64 * 8 bytes
+    expect(lambda: ex.encode(**attn_kw(prologue=P(rope=buf(4 * D * 8 - 4), rope_tokens=4))), _abi.E_OUT_OF_BOUNDS,
+           "RoPE table buffer is shorter than rope_tokens rows")
+    expect(lambda: ex.encode(**attn_kw(prologue=P(rope=buf(3 * D * 8), rope_tokens=3))), _abi.E_OUT_OF_BOUNDS,
+           "RoPE table has fewer rows than query_count")
+    expect(lambda: ex.encode(**attn_kw(key_count=6, prologue=P(rope=buf(4 * D * 8), rope_tokens=4, rope_q=False))),
+           _abi.E_OUT_OF_BOUNDS, "RoPE table has fewer rows than key_count")
+    # separate K table (the adapter's cross attention): its own row count and length
+    expect(lambda: ex.encode(**attn_kw(key_count=6, prologue=P(rope=buf(4 * D * 8), rope_tokens=4,
+                                                              k_rope=buf(5 * D * 8), k_rope_tokens=5))),
+           _abi.E_OUT_OF_BOUNDS, "K RoPE table has fewer rows than key_count")
+    expect(lambda: ex.encode(**attn_kw(key_count=6, prologue=P(rope=buf(4 * D * 8), rope_tokens=4,
+                                                              k_rope=buf(6 * D * 8 - 4), k_rope_tokens=6))),
+           _abi.E_OUT_OF_BOUNDS, "K RoPE table buffer is shorter")
+    expect(lambda: ex.encode(**attn_kw(prologue=P(eps=float("nan")))), _abi.E_INVALID_ARGUMENT, "epsilon")
+
+
+def test_linear_head_rmsnorm_validation(ctx):
+    lin = animaxs_amd.LinearExecutor(ctx)
+    x, y = buf(4 * 64 * 2), buf(4 * 256 * 2)
+    w = w4(rows=256, cols=64)
+    expect(lambda: lin.encode_head_rmsnorm(x, w, y, 4, buf(128 * 2 - 2), head_dim=128), _abi.E_OUT_OF_BOUNDS,
+           "per-head RMSNorm weight buffer range is out of bounds")
+    expect(lambda: lin.encode_head_rmsnorm(x, w, y, 4, None, head_dim=128), _abi.E_INVALID_ARGUMENT,
+           "pointer is null")
+    expect(lambda: lin.encode_head_rmsnorm(x, w4(rows=200, cols=64), y, 4, buf(256), head_dim=128),
+           _abi.E_INVALID_SHAPE, "multiple of head_dim")
+    expect(lambda: lin.encode_head_rmsnorm(x, w, y, 4, buf(256), head_dim=0), _abi.E_INVALID_SHAPE,
+           "head_dim must be positive")
+    expect(lambda: lin.encode_head_rmsnorm(x, w, y, 4, buf(256), head_dim=128, eps=-1.0),
+           _abi.E_INVALID_ARGUMENT, "epsilon")
+
+
+# --------------------------------------------------------------------------------------
+# DiT block: every pointer and range is checked before any launch.
+# --------------------------------------------------------------------------------------
+
+def _block_case(S=4, dim=256, heads=2, hd=128, T=3, C=128, hidden=512, lora=16):
+    shapes = {"self_q": (dim, dim), "self_k": (dim, dim), "self_v": (dim, dim), "self_o": (dim, dim),
+              "cross_q": (dim, dim), "cross_k": (dim, C), "cross_v": (dim, C), "cross_o": (dim, dim),
+              "mlp1": (hidden, dim), "mlp2": (dim, hidden),
+              "mod_self_w1": (lora, dim), "mod_cross_w1": (lora, dim), "mod_mlp_w1": (lora, dim),
+              "mod_self_w2": (3 * dim, lora), "mod_cross_w2": (3 * dim, lora), "mod_mlp_w2": (3 * dim, lora)}
+    weights = {n: w4(rows=r, cols=c) for n, (r, c) in shapes.items()}
+    norms_ = {n: buf(hd * 2) for n in ("self_q_norm", "self_k_norm", "cross_q_norm", "cross_k_norm")}
+    args = dict(residual=buf(S * dim * 4), emb=buf(dim * 4), adaln_lora=buf(3 * dim * 4),
+                context_tokens_buf=buf(T * C * 2), rope=buf(S * hd * 8))
+    shape = dict(tokens=S, dim=dim, heads=heads, head_dim=hd, context_tokens=T, context_dim=C, mlp_hidden=hidden)
+    return weights, norms_, args, shape
+
+
+def test_dit_block_rejects_null_and_short_buffers(ctx):
+    blk = animaxs_amd.DiTBlockExecutor(ctx)
+    weights, norms_, args, shape = _block_case()
+
+    def run(w=weights, n=norms_, a=args, **over):
+        return lambda: blk.encode(w, n, a["residual"], a["emb"], a["adaln_lora"], a["context_tokens_buf"],
+                                  a["rope"], **dict(shape, **over))
+
+    for name in norms_:
+        expect(run(n=dict(norms_, **{name: None})), _abi.E_INVALID_ARGUMENT, "norm pointer is null")
+        expect(run(n=dict(norms_, **{name: buf(128 * 2 - 2)})), _abi.E_OUT_OF_BOUNDS,
+               "norm buffer range is out of bounds")
+    for name, what in (("residual", "residual"), ("emb", "emb"), ("adaln_lora", "adaln_lora"),
+                       ("context_tokens_buf", "context"), ("rope", "RoPE table")):
+        expect(run(a=dict(args, **{name: (0, args[name][1])})), _abi.E_INVALID_ARGUMENT,
+               f"DiT block {what} pointer is null")
+        expect(run(a=dict(args, **{name: buf(args[name][1] - 4)})), _abi.E_OUT_OF_BOUNDS,
+               f"DiT block {what} buffer range is out of bounds")
+    expect(run(w=dict(weights, mlp2=w4(rows=256, cols=448))), _abi.E_INVALID_SHAPE, "mlp2 shape mismatch")
+    expect(run(w=dict(weights, self_v=w4(rows=256, cols=256, packed=100))), _abi.E_OUT_OF_BOUNDS,
+           "buffer range is out of bounds")
+    expect(run(heads=3), _abi.E_INVALID_SHAPE, "heads * head_dim == dim")
+
+
+def test_dit_forward_validates_every_block_before_launch(ctx):
+    blk = animaxs_amd.DiTBlockExecutor(ctx)
+    weights, norms_, args, shape = _block_case()
+    bad = dict(weights, cross_o=w4(rows=256, cols=256, scale=2))
+    a = args
+    expect(lambda: blk.forward([(weights, norms_), (weights, norms_), (bad, norms_)], a["residual"], a["emb"],
+                               a["adaln_lora"], a["context_tokens_buf"], a["rope"], **shape),
+           _abi.E_OUT_OF_BOUNDS, "buffer range is out of bounds")
+    expect(lambda: blk.forward([], a["residual"], a["emb"], a["adaln_lora"], a["context_tokens_buf"], a["rope"],
+                               **shape), _abi.E_INVALID_SHAPE, "at least one block")
+
+
+def test_cache_and_streamer_argument_checks(ctx):
+    expect(lambda: animaxs_amd.CrossKVCache(ctx, 0, 512, 2048), _abi.E_INVALID_SHAPE, "invalid cross K/V cache shape")
+    expect(lambda: animaxs_amd.WeightStreamer(ctx, 1 << 20, 5), _abi.E_INVALID_ARGUMENT,
+           "weight slot count must be in 1...4")
+    expect(lambda: animaxs_amd.WeightStreamer(ctx, 0, 2), _abi.E_INVALID_SHAPE, "capacity must be positive")
+
+
+def test_as_buffer_rejects_host_and_strided_tensors():
+    import torch
+    with pytest.raises(TypeError, match="GPU tensors"):
+        animaxs_amd.as_buffer(torch.zeros(4))
+    # a stride-0 expanded view claims more bytes than it owns; checked after the device test,
+    # so use a fake object that reports a CUDA tensor which is not contiguous
+    class View:
+        is_cuda = True
+
+        def data_ptr(self):
+            return FAKE
+
+        def is_contiguous(self):
+            return False
+
+        def numel(self):
+            return 1 << 20
+
+        def element_size(self):
+            return 2
+    with pytest.raises(TypeError, match="contiguous"):
+        animaxs_amd.as_buffer(View())

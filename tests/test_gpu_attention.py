@@ -270,3 +270,29 @@ def test_validation_errors_do_not_launch(ctx):
     with pytest.raises(AnimaError) as e:
         ex.execute(query=buf, key=buf, value=buf, output=buf, heads=4, query_count=8, key_count=8, head_dim=8)
     assert e.value.status == animaxs_amd._abi.E_OUT_OF_BOUNDS
+
+
+@pytest.mark.parametrize("Tq,Tk", [(300, 512), (77, 200), (256, 256)])
+def test_llm_adapter_attention_head_dim_64_separate_key_rope(ctx, Tq, Tk):
+    """LLM-adapter attention (LLMAdapterMetal.swift:360-405, rms_rope_adapter64
+    AnimaKernels.metal:733-763): 16 heads x head_dim 64 over hidden 1024, per-head RMSNorm with
+    weights per side, and RoPE theta 1e4 over 32 pairs where the queries (target tokens) use the
+    target table and the keys (context tokens, a different count) their own context table --
+    the K-side table of the prologue.  Token-major [tokens, 1024] rows, no transposes."""
+    H, D = 16, 64
+    g = torch.Generator().manual_seed(Tq * 1000 + Tk)
+    q = (torch.randn(1, Tq, H, D, generator=g) * 2).half()
+    k = (torch.randn(1, Tk, H, D, generator=g) * 2).half()
+    v = torch.randn(1, Tk, H, D, generator=g).half()
+    qw = (torch.rand(D, generator=g) * 0.4 + 0.8).half()
+    kw = (torch.rand(D, generator=g) * 0.4 + 0.8).half()
+    rq = orope.neox_rope_table(Tq, 1.0e4, head_dim=D)
+    rk = orope.neox_rope_table(Tk, 1.0e4, head_dim=D)
+    lib_rq = animaxs_amd.qwen_rope(Tq, head_dim=D, theta=1.0e4)   # the library's own table builder
+    assert np.abs(lib_rq - rq.numpy()).max() < 2e-6
+    pro = QKPrologue(dev(qw), dev(kw), 1e-6, dev(rq), Tq, True, True, k_rope=dev(rk), k_rope_tokens=Tk)
+    print(f"ADAPTER Tq={Tq} Tk={Tk}", flush=True)
+    o = _run(ctx, dev(q), dev(k), dev(v), layout=("tokenMajor", H * D), heads=H, Sq=Tq, Sk=Tk, D=D,
+             out_shape=(1, Tq, H, D), prologue=pro)
+    ref = oatt.sdpa(oatt.qk_prologue(q, qw, 1e-6, rq).half().float(), oatt.qk_prologue(k, kw, 1e-6, rk).half().float(), v)
+    assert_attention_close(o, ref, label=f"adapter D64 Tq{Tq} Tk{Tk}")

@@ -502,3 +502,47 @@ def test_linear_group_equals_separate_encodes(ctx, storage, M, Ns, K):
     torch.cuda.synchronize()
     for r, o in zip(refs, outs):
         assert torch.equal(r.view(torch.int16), o.view(torch.int16))
+
+
+@pytest.mark.parametrize("storage,M,N,K,hd", [(0, 300, 384, 512, 128), (1, 1000, 2048, 1024, 128),
+                                              (0, 4096 + 40, 2048, 2048, 128), (0, 48, 384, 512, 128),
+                                              (0, 300, 384, 512, 64), (2, 100, 256, 256, 128)])
+def test_linear_head_rmsnorm_matches_encode_then_norm(ctx, storage, M, N, K, hd):
+    """anima_linear_encode_head_rmsnorm: the tiled GEMM's per-head RMSNorm output stage (M > 64,
+    W4/W8, head_dim 128; ragged M, N = 384 leaves a 256-column tile half used) and the in-place
+    second pass (small M, head_dim 64, fp16 storage) against plain encode followed by the oracle's
+    per-head RMSNorm (rmsnorm_heads_half, AnimaKernels.metal:660-689) of those fp16 outputs: within
+    one fp16 ulp (the sum of squares is reduced in another order)."""
+    from oracle import norms
+    w = _affine_weight(storage, N, K, seed=11 * M + N + K + storage + hd)
+    qw, keep = device_weight(w)
+    g = torch.Generator().manual_seed(M + N + hd)
+    x = dev(torch.randn(M, K, generator=g).half())
+    nw = (torch.rand(hd, generator=g) * 0.4 + 0.8).half()
+    lin = LinearExecutor(ctx)
+    print(f"HEAD_RMSNORM storage={storage} M={M} N={N} K={K} hd={hd}", flush=True)
+    y0 = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    lin.encode(x, qw, y0, M)
+    y = torch.full((M, N), float("nan"), dtype=torch.float16, device="cuda")
+    lin.encode_head_rmsnorm(x, qw, y, M, dev(nw), head_dim=hd, eps=1e-6)
+    torch.cuda.synchronize()
+    ref = norms.rms_norm(y0.cpu().float().reshape(M, N // hd, hd), nw, 1e-6).reshape(M, N)
+    got = y.cpu().float()
+    assert torch.isfinite(got).all()
+    err = (got - ref).abs()
+    ulp = torch.clamp(ref.abs(), min=2.0 ** -14) * 2.0 ** -10
+    print(f"HEAD_RMSNORM max_err={float(err.max()):.3e} max_err/ulp={float((err / ulp).max()):.2f}", flush=True)
+    assert bool((err <= ulp * 1.01).all())
+
+
+def test_split_k_merge_with_odd_element_count(ctx):
+    """M*N odd (101 x 1001, K = 2048: four tiles, so the GEMM splits K in two): the split-K
+    merge must take its element-wise path, whose reads of split s >= 1 are then not
+    16-byte aligned."""
+    M, N, K = 101, 1001, 2048
+    d = inputs.small_m_gemm(M, N, K, seed=77)
+    qw, keep = device_weight(d["w"])
+    y = torch.full((M, N), float("nan"), dtype=torch.float16, device="cuda")
+    LinearExecutor(ctx).execute(dev(d["x"]), qw, y, M)
+    torch.cuda.synchronize()
+    _check_gemm(y, _gemm_ref(d["x"], d["w"]), f"split-K odd M{M} N{N} K{K}")
