@@ -127,6 +127,7 @@ SIGNATURES = {
     "anima_attention_destroy": (_S, [_P]),
     "anima_attention_encode": (_S, [_P, C.POINTER(AttentionArgs)]),
     "anima_attention_execute": (_S, [_P, C.POINTER(AttentionArgs)]),
+    "anima_attention_encode_noalloc": (_S, [_P, C.POINTER(AttentionArgs)]),
     "anima_attention_max_score_scratch_bytes": (_S, [_P, _I64, _I64, C.POINTER(_I64)]),
     "anima_attention_workspace_bytes": (_S, [_P, C.POINTER(_I64)]),
     "anima_linear_create": (_S, [_P, C.POINTER(LinearConfig), _PP]),

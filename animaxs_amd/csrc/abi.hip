@@ -82,6 +82,10 @@ anima_status anima_attention_encode(anima_attention* attn, const anima_attention
   return guarded([&] { require(attn, "attention")->impl.encode(*require(args, "attention args")); });
 }
 
+anima_status anima_attention_encode_noalloc(anima_attention* attn, const anima_attention_args* args) {
+  return guarded([&] { require(attn, "attention")->impl.encode_noalloc(*require(args, "attention args")); });
+}
+
 anima_status anima_attention_execute(anima_attention* attn, const anima_attention_args* args) {
   return guarded([&] {
     require(attn, "attention")->impl.encode(*require(args, "attention args"));

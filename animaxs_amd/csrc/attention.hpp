@@ -65,11 +65,15 @@ class AttentionExecutor {
  public:
   AttentionExecutor(anima_ctx* ctx, const anima_attention_config& cfg);
   void encode(const anima_attention_args& a);
+  // encode() with its workspace taken from the library's static per-device scratch
+  // (at most 64 MiB) instead of the executor's allocations: no hipMalloc/hipFree.
+  void encode_noalloc(const anima_attention_args& a);
   int64_t maximum_score_scratch_bytes(int64_t key_count, int64_t query_count) const;
   int64_t workspace_bytes() const { return ws_.capacity() + split_ws_.capacity(); }
   anima_ctx* context() const { return ctx_; }
 
  private:
+  void encode_impl(const anima_attention_args& a, bool no_alloc);
   anima_ctx* ctx_;
   anima_attention_config cfg_;
   Workspace ws_;

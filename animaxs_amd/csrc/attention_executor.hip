@@ -2,6 +2,7 @@
 // AttentionExecutor.validate (AnimaXS/Runtime/Metal/AttentionExecutor.swift:778-847)
 // plus the batch / key-length / prologue extensions, and kernel dispatch.
 #include <cmath>
+#include <mutex>
 #include <string>
 
 #include "attention.hpp"
@@ -30,7 +31,42 @@ int64_t AttentionExecutor::maximum_score_scratch_bytes(int64_t key_count, int64_
 
 static int64_t round_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
-void AttentionExecutor::encode(const anima_attention_args& a) {
+// ---------------------------------------------------------------------------
+// Static workspace of anima_attention_encode_noalloc, for callers that cannot
+// allocate (code under graph capture, tight serving loops).  Every GPU the library
+// runs on holds one copy until the process ends.  Each call uses it from offset 0:
+// K prologue rows, then Q prologue rows, then key-split partial rows, all written by
+// the call's own kernels before they are read (nothing has to start at zero).  Calls
+// that overlap on one GPU share it and race.
+// ---------------------------------------------------------------------------
+constexpr int64_t NOALLOC_SCRATCH_BYTES = int64_t(64) << 20;
+static __device__ __align__(256) char scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static std::mutex g_scratch_mutex;
+static char* g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+// Device address of `scratch` on `device` (which must be current): resolved once per
+// device with hipGetSymbolAddress.  The array's own name is a host-side stand-in,
+// never a device address, so only this pointer reaches kernels.
+static char* noalloc_scratch(int device) {
+  if (device < 0 || device >= NOALLOC_MAX_DEVICES)
+    fail(ANIMA_E_UNSUPPORTED, "allocation-free attention supports device indices below 64");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[device]) {
+    void* ptr = nullptr;
+    ANIMA_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (!ptr) fail(ANIMA_E_DEVICE, "hipGetSymbolAddress returned a null scratch address");
+    g_scratch_ptr[device] = static_cast<char*>(ptr);
+  }
+  return g_scratch_ptr[device];
+}
+
+void AttentionExecutor::encode(const anima_attention_args& a) { encode_impl(a, false); }
+
+void AttentionExecutor::encode_noalloc(const anima_attention_args& a) { encode_impl(a, true); }
+
+void AttentionExecutor::encode_impl(const anima_attention_args& a, bool no_alloc) {
   const int layout = a.layout < 0 ? cfg_.layout : a.layout;
   if (layout != ANIMA_LAYOUT_HEAD_MAJOR && layout != ANIMA_LAYOUT_TOKEN_MAJOR)
     fail(ANIMA_E_INVALID_ARGUMENT, "unknown attention layout");
@@ -191,33 +227,20 @@ void AttentionExecutor::encode(const anima_attention_args& a) {
 
   const int64_t k_ws = need_k_pro ? round_up(checked_product({B, kvh, Sk, D, 2}, "attention"), 256) : 0;
   const int64_t q_ws = need_q_pro ? round_up(checked_product({B, H, Sq, D, 2}, "attention"), 256) : 0;
-  DeviceGuard guard(ctx_);
-  hipStream_t stream = ctx_->stream;
-  char* ws = (k_ws + q_ws) > 0 ? static_cast<char*>(ws_.get(k_ws + q_ws, stream)) : nullptr;
 
+  // The whole plan is fixed before anything is launched: the prologues write dense
+  // head-major rows, so the flash kernel reads those strides; the key-split decision
+  // depends on them.
+  const half_t* k_in = kp;
+  const half_t* q_in = qp;
+  const int64_t k_in_tok = k_tok, k_in_head = k_head, k_in_batch = k_batch;
+  const int64_t q_in_tok = q_tok, q_in_head = q_head, q_in_batch = q_batch;
   if (need_k_pro) {
-    PrologueParams pp{};
-    pp.in = kp; pp.in_tok = k_tok; pp.in_head = k_head; pp.in_batch = k_batch;
-    pp.out = reinterpret_cast<half_t*>(ws);
-    pp.out_tok = D; pp.out_head = Sk * D; pp.out_batch = kvh * Sk * D;
-    pp.batch = (int)B; pp.rows = (int)Sk; pp.heads = (int)kvh; pp.D = (int)D;
-    pp.norm_w = k_norm; pp.eps = eps; pp.rope = rope_k;
-    launch_prologue(pp, stream);
-    kp = pp.out;
     k_tok = D; k_head = Sk * D; k_batch = kvh * Sk * D;
   }
   if (need_q_pro) {
-    PrologueParams pp{};
-    pp.in = qp; pp.in_tok = q_tok; pp.in_head = q_head; pp.in_batch = q_batch;
-    pp.out = reinterpret_cast<half_t*>(ws + k_ws);
-    pp.out_tok = D; pp.out_head = Sq * D; pp.out_batch = H * Sq * D;
-    pp.batch = (int)B; pp.rows = (int)Sq; pp.heads = (int)H; pp.D = (int)D;
-    pp.norm_w = q_norm; pp.eps = eps; pp.rope = rope_q;
-    launch_prologue(pp, stream);
-    qp = pp.out;
     q_tok = D; q_head = Sq * D; q_batch = H * Sq * D;
   }
-
   p.q = qp; p.k = kp; p.v = vp; p.o = op;
   p.q_tok = q_tok; p.q_head = q_head; p.q_batch = q_batch;
   p.k_tok = k_tok; p.k_head = k_head; p.k_batch = k_batch;
@@ -236,11 +259,49 @@ void AttentionExecutor::encode(const anima_attention_args& a) {
     p.q_norm_w = q_norm;
     p.rope = rope_q;
   }
+  const int splits = use_flash ? flash_kv_splits(p, (int)D, (int)B, cfg_.flash_rows) : 1;
+  const int64_t part = splits > 1 ? round_up(flash_split_bytes(p, (int)D, (int)B, splits), 256) : 0;
+
+  DeviceGuard guard(ctx_);
+  hipStream_t stream = ctx_->stream;
+  char* ws = nullptr;
+  char* pw = nullptr;
+  if (no_alloc) {
+    const int64_t total = k_ws + q_ws + part;
+    if (total > NOALLOC_SCRATCH_BYTES)
+      fail(ANIMA_E_UNSUPPORTED, "attention needs " + std::to_string(total) +
+                                    " bytes of workspace; the allocation-free entry point holds at most " +
+                                    std::to_string(NOALLOC_SCRATCH_BYTES) + " bytes (use anima_attention_encode)");
+    char* base = noalloc_scratch(ctx_->device);
+    ws = base;
+    pw = base + k_ws + q_ws;
+  } else {
+    if (k_ws + q_ws > 0) ws = static_cast<char*>(ws_.get(k_ws + q_ws, stream));
+    if (part > 0) pw = static_cast<char*>(split_ws_.get(part, stream));
+  }
+
+  if (need_k_pro) {
+    PrologueParams pp{};
+    pp.in = k_in; pp.in_tok = k_in_tok; pp.in_head = k_in_head; pp.in_batch = k_in_batch;
+    pp.out = reinterpret_cast<half_t*>(ws);
+    pp.out_tok = D; pp.out_head = Sk * D; pp.out_batch = kvh * Sk * D;
+    pp.batch = (int)B; pp.rows = (int)Sk; pp.heads = (int)kvh; pp.D = (int)D;
+    pp.norm_w = k_norm; pp.eps = eps; pp.rope = rope_k;
+    launch_prologue(pp, stream);
+    p.k = pp.out;
+  }
+  if (need_q_pro) {
+    PrologueParams pp{};
+    pp.in = q_in; pp.in_tok = q_in_tok; pp.in_head = q_in_head; pp.in_batch = q_in_batch;
+    pp.out = reinterpret_cast<half_t*>(ws + k_ws);
+    pp.out_tok = D; pp.out_head = Sq * D; pp.out_batch = H * Sq * D;
+    pp.batch = (int)B; pp.rows = (int)Sq; pp.heads = (int)H; pp.D = (int)D;
+    pp.norm_w = q_norm; pp.eps = eps; pp.rope = rope_q;
+    launch_prologue(pp, stream);
+    p.q = pp.out;
+  }
   if (use_flash) {
-    const int splits = flash_kv_splits(p, (int)D, (int)B, cfg_.flash_rows);
     if (splits > 1) {
-      const int64_t part = flash_split_bytes(p, (int)D, (int)B, splits);
-      char* pw = static_cast<char*>(split_ws_.get(part, stream));
       p.kv_splits = splits;
       p.part_o = reinterpret_cast<float*>(pw);
       p.part_ml = reinterpret_cast<float*>(pw + checked_product({(int64_t)splits, B, H, Sq, D, 4}, "attention"));

@@ -194,6 +194,13 @@ class AttentionExecutor:
         call("anima_attention_encode", self._h, C.byref(a))
         del keep
 
+    def encode_noalloc(self, **kw) -> None:
+        """encode() with the workspace taken from the library's static per-device scratch
+        (at most 64 MiB): makes no device allocation (anima_attention_encode_noalloc)."""
+        a, keep = self._args(**kw)
+        call("anima_attention_encode_noalloc", self._h, C.byref(a))
+        del keep
+
     def execute(self, **kw) -> None:
         """AttentionExecutor.execute (AttentionExecutor.swift:751-776): encode + wait."""
         a, keep = self._args(**kw)

@@ -178,6 +178,16 @@ typedef struct anima_attention_args {
 
 anima_status anima_attention_encode(anima_attention* attn, const anima_attention_args* args);
 anima_status anima_attention_execute(anima_attention* attn, const anima_attention_args* args);
+/* No counterpart in the reference: anima_attention_encode for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments, validation, kernels and results; the
+ * workspace (K/Q prologue rows, key-split partial rows) comes from a static per-device
+ * array of at most 64 MiB instead of the executor's own allocations, and the call
+ * makes no hipMalloc, hipFree or other allocating call.  A request whose workspace
+ * exceeds 64 MiB fails with ANIMA_E_UNSUPPORTED before anything is launched.  Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams,
+ * two threads) race. */
+anima_status anima_attention_encode_noalloc(anima_attention* attn, const anima_attention_args* args);
 /* AttentionExecutor.maximumScoreScratchBytes (AttentionExecutor.swift:112-120):
  * the score scratch the reference's query-tiled path would need (fp16 legacy /
  * fp32 scores) for min(tile_rows, query_count) x key_count.  The flash kernels
