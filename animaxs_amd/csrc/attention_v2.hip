@@ -11,8 +11,8 @@
 //       G(j)  MFMA phase: QK^T of tile j and PV of tile j-1 on the matrix cores,
 //             as one fixed sequence of MFMAs whose LDS fragment reads run a few
 //             MFMAs ahead;
-//       X(j)  VALU phase: the tile copies (below), masking, row max, the (rare)
-//             O rescale, exp2, fp16 P and the fp32 row sums of tile j.
+//       X(j)  VALU phase: the tile copies (below), masking, exp2, fp16 P and the
+//             fp32 row sums of tile j (row max and O rescale only when needed).
 //     Phases are separated by workgroup barriers, and group 1 runs one phase
 //     behind group 0 (one extra barrier at the start, group 0 one at the end), so
 //     in every barrier interval one wave of each SIMD issues MFMAs while the
@@ -30,9 +30,11 @@
 //     distinct banks (64 banks x 4 B); padding instead of an XOR swizzle keeps
 //     every fragment address "per-lane base + immediate".  V^T fragments come
 //     straight from the row-major V tile with ds_read_b64_tr_b16.
-//   * Exps use the running max; a row max that grows by more than 2^8 rescales O
-//     and the row sums first (wave-uniform branch).  Four LDS stages: tile j is
-//     read by QK while tile j-1 is read by PV and tile j+2 is written.
+//   * Exps use the running max without computing the tile's row max: a lane's
+//     share of the tile's row sum above 2^15 (or not finite) sends the wave to the
+//     exact path (row max, O / row-sum rescale, exps again), which the first tile
+//     always takes.  Four LDS stages: tile j is read by QK while tile j-1 is read
+//     by PV and tile j+2 is written.
 //   * Everything (Q, O accumulators, scores, row sums) lives in the 256 VGPRs a
 //     wave gets at 2 waves/SIMD.
 #include <type_traits>
@@ -45,7 +47,7 @@ constexpr int F2_WAVES = 8;
 constexpr int F2_NT = 64 * F2_WAVES;
 constexpr int F2_BN = 64;
 constexpr int F2_STAGES = 4;
-constexpr float F2_RESCALE_THRESHOLD = 8.0f;
+constexpr float F2_LAZY_LIMIT = 32768.f;   // largest tile row-sum share the fast path accepts
 constexpr int F2_READ_AHEAD = 4;    // MFMA operand fragments read from LDS ahead of their MFMA
 static_assert(FLASH_V2_ROWS == 32 * F2_WAVES, "one 32-row block per wave");
 
@@ -204,25 +206,40 @@ void flash_attention_v2_kernel(FlashParams p) {
   }
   const uint32_t loff_k = (uint32_t)(crow * KROW + cch * 8) * 2u;
   const uint32_t loff_v = (uint32_t)(crow * VROW + cch * 8) * 2u;
-  // Valid bytes of tile j from its first row (the last valid row ends at column D).
-  auto tile_bytes = [&](int j, uint32_t tok2) __attribute__((always_inline)) -> int {
-    const int rows = kend - j * F2_BN;
-    return rows <= 0 ? 0 : rows >= F2_BN ? (int)(F2_BN * tok2) : (int)((uint32_t)(rows - 1) * tok2 + D * 2);
+  // Valid bytes of a tile from its first row: the descriptor of tile j spans from the
+  // tile's first row to the end (column D) of the last key row in use, so rows past
+  // kend read as zeros.  The loop loads tiles 4, 5, 6, ... in order, so it keeps one
+  // running base pointer and one remaining-byte count per tensor and advances them by
+  // a tile per load (scalar adds) instead of recomputing base + j * 64 * row_stride.
+  const int64_t kstep = (int64_t)F2_BN * ktok2, vstep = (int64_t)F2_BN * vtok2;
+  const int64_t kbytes = kend > 0 ? (int64_t)(kend - 1) * ktok2 + D * 2 : 0;
+  const int64_t vbytes = kend > 0 ? (int64_t)(kend - 1) * vtok2 + D * 2 : 0;
+  auto clamp_bytes = [](int64_t rem) __attribute__((always_inline)) -> int {
+    return rem <= 0 ? 0 : (rem >= 0x7fffffff ? 0x7fffffff : (int)rem);
   };
 
-  // Copies go global -> VGPR -> LDS: load_tile fetches this thread's chunks of tile
-  // j into staging buffer j % 2, store_seg writes copy r into a stage two tile
+  // Copies go global -> VGPR -> LDS: load_tile fetches this thread's chunks of a tile
+  // into staging buffer j % 2, store_seg writes copy r into a stage two tile
   // periods later (two buffers keep two tiles in flight).
   u32x4 stg2[2][NCP];
-  auto load_tile = [&](int j, auto bufc) __attribute__((always_inline)) {
+  auto load_at = [&](const char* kt, int nk, const char* vt, int nv, auto bufc) __attribute__((always_inline)) {
     u32x4 (&stg)[NCP] = stg2[decltype(bufc)::value];
-    const char* kt = reinterpret_cast<const char*>(kbase) + (int64_t)j * F2_BN * ktok2;
-    const char* vt = reinterpret_cast<const char*>(vbase) + (int64_t)j * F2_BN * vtok2;
-    const int nk = tile_bytes(j, ktok2), nv = tile_bytes(j, vtok2);
 #pragma unroll
     for (int r = 0; r < CPT; ++r) stg[r] = load16_bounded(kt, nk, goff_k[r]);
 #pragma unroll
     for (int r = 0; r < CPT; ++r) stg[CPT + r] = load16_bounded(vt, nv, goff_v[r]);
+  };
+  auto load_tile = [&](int j, auto bufc) __attribute__((always_inline)) {
+    load_at(reinterpret_cast<const char*>(kbase) + j * kstep, clamp_bytes(kbytes - j * kstep),
+            reinterpret_cast<const char*>(vbase) + j * vstep, clamp_bytes(vbytes - j * vstep), bufc);
+  };
+  const char* k_next = reinterpret_cast<const char*>(kbase) + 4 * kstep;
+  const char* v_next = reinterpret_cast<const char*>(vbase) + 4 * vstep;
+  int64_t k_rem = kbytes - 4 * kstep, v_rem = vbytes - 4 * vstep;
+  auto load_next = [&](auto bufc) __attribute__((always_inline)) {
+    load_at(k_next, clamp_bytes(k_rem), v_next, clamp_bytes(v_rem), bufc);
+    k_next += kstep; v_next += vstep;
+    k_rem -= kstep; v_rem -= vstep;
   };
   auto store_seg = [&](int r, auto st, auto bufc) __attribute__((always_inline)) {
     u32x4 (&stg)[NCP] = stg2[decltype(bufc)::value];
@@ -280,12 +297,6 @@ void flash_attention_v2_kernel(FlashParams p) {
     return half8v{lo_h[0], lo_h[1], lo_h[2], lo_h[3], hi_h[0], hi_h[1], hi_h[2], hi_h[3]};
   };
 
-  // fp16 probability of one score with the running max msub of the latest X phase.
-  float msub = 0.f;
-  auto exp_p = [&](float sc) __attribute__((always_inline)) -> half_t {
-    return (half_t)fast_exp2(fmaf(sc, c2, -msub));
-  };
-
   // G(j): S = K_j Q^T, O += V_{j-1}^T P_{j-1}; the probabilities of keys 32..63 of
   // tile j-1 are computed under the first (key half 0) QK MFMAs, before QK
   // overwrites those scores.
@@ -338,14 +349,14 @@ void flash_attention_v2_kernel(FlashParams p) {
 
   // X(j): the tile copies (tile j+2, staged in registers during X(j-2), goes to
   // LDS; the loads of tile j+4 start into the buffer it leaves), then P = fp16(exp2(S*c - m)) with the
-  // running max m, rescaling O first when a row's max grew by more than 2^8.  The
+  // running max m (updated, with the O rescale, only on the exact path above).  The
   // copies sit in the VALU phase so that their LDS writes never queue ahead of
   // the fragment reads of this wave's MFMA phase.
   auto x_phase = [&](int j, auto st) __attribute__((always_inline)) {
     using SW = std::integral_constant<int, (decltype(st)::value + 2) % F2_STAGES>;
     using BUF = std::integral_constant<int, decltype(st)::value % 2>;
     store_tile(SW{}, BUF{});   // tile j+2
-    load_tile(j + 4, BUF{});   // all zeros past the last tile
+    load_next(BUF{});          // tile j+4 (all zeros past the last tile)
     const int k0 = j * F2_BN;
     if ((k0 + F2_BN > kv_len) || (p.causal && k0 + F2_BN - 1 > wq0)) {
 #pragma unroll
@@ -356,34 +367,46 @@ void flash_attention_v2_kernel(FlashParams p) {
           if (kidx >= kv_len || (p.causal && kidx > qi)) S[h][e] = -INFINITY;
         }
     }
-    // NaN-propagating maximum (v_maximum3_f32, no operand canonicalisation) as a
-    // shallow tree: 32 scores -> 8 partial maxima -> 1.
-    auto mx = [](float a, float b) __attribute__((always_inline)) { return __builtin_elementwise_maximum(a, b); };
-    float part[8];
+    // Exponentials against the running max m_run (log2 units), fp16 P and this lane's
+    // fp32 row-sum share of the tile.  The row max is not computed on this path: a
+    // tile sum <= 2^15 bounds every p by 2^15, well inside fp16, and the sum is
+    // needed anyway.  Only when a lane's sum exceeds that (the first tile, where m_run
+    // is -inf, or a row max that grew by about 15) or is not finite does the wave take
+    // the exact path: the row max, the O / row-sum rescale, then the exponentials again.
+    auto exps = [&](float msub) __attribute__((always_inline)) -> float {
+      float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) part[i] = mx(mx(S[i >> 2][4 * (i & 3)], S[i >> 2][4 * (i & 3) + 1]),
-                                            mx(S[i >> 2][4 * (i & 3) + 2], S[i >> 2][4 * (i & 3) + 3]));
-    float mloc = mx(mx(mx(part[0], part[1]), mx(part[2], part[3])), mx(mx(part[4], part[5]), mx(part[6], part[7])));
-    mloc = xlane32_max(mloc) * c2;
-    if (__any(mloc > m_run + F2_RESCALE_THRESHOLD)) {
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float pe = fast_exp2(fmaf(S[h][e], c2, -msub));
+          P[h][e >> 3][e & 7] = (half_t)pe;
+          ls[e & 3] += pe;
+        }
+      return (ls[0] + ls[1]) + (ls[2] + ls[3]);
+    };
+    float tsum = exps(m_run);
+    if (__any(!(tsum <= F2_LAZY_LIMIT))) {
+      // NaN-propagating maximum (v_maximum3_f32, no operand canonicalisation) as a
+      // shallow tree: 32 scores -> 8 partial maxima -> 1.
+      auto mx = [](float a, float b) __attribute__((always_inline)) { return __builtin_elementwise_maximum(a, b); };
+      float part[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) part[i] = mx(mx(S[i >> 2][4 * (i & 3)], S[i >> 2][4 * (i & 3) + 1]),
+                                              mx(S[i >> 2][4 * (i & 3) + 2], S[i >> 2][4 * (i & 3) + 3]));
+      float mloc = mx(mx(mx(part[0], part[1]), mx(part[2], part[3])), mx(mx(part[4], part[5]), mx(part[6], part[7])));
+      mloc = xlane32_max(mloc) * c2;
       const float mnew = fmaxf(m_run, mloc);
-      const float alpha = (mnew == -INFINITY) ? 1.f : fast_exp2(m_run - mnew);
-      lrow *= alpha;
+      if (mnew > m_run) {
+        const float alpha = (m_run == -INFINITY) ? 1.f : fast_exp2(m_run - mnew);
+        lrow *= alpha;
 #pragma unroll
-      for (int c = 0; c < OB; ++c) acc[c] *= alpha;
-      m_run = mnew;
-    }
-    msub = (m_run == -INFINITY) ? 0.f : m_run;
-    float ls[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float pe = fast_exp2(fmaf(S[h][e], c2, -msub));
-        P[h][e >> 3][e & 7] = (half_t)pe;
-        ls[e & 3] += pe;
+        for (int c = 0; c < OB; ++c) acc[c] *= alpha;
+        m_run = mnew;
       }
-    lrow += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+      tsum = exps((m_run == -INFINITY) ? 0.f : m_run);
+    }
+    lrow += tsum;
     asm volatile("" ::"v"(P[0][0]), "v"(P[0][1]), "v"(P[1][0]), "v"(P[1][1]));
   };
 
