@@ -7,13 +7,15 @@ reference's Swift operator surface in Python over that ABI (``executors``).
 
 from ._abi import AnimaError, LIB_PATH, load  # noqa: F401
 from .executors import (  # noqa: F401
-    AttentionExecutor, BlockOps, Context, CrossKVCache, DiTBlockExecutor, DitRoPE, LinearExecutor, QKPrologue,
-    QuantDecoders, QuantizedLinearWeightBuffers, QwenLayerExecutor, WeightStreamer, as_buffer, qwen_rope,
+    AttentionExecutor, BlockOps, Context, CrossKVCache, DiTBlockExecutor, DiTFinalLayerExecutor,
+    DiTPreparationExecutor, DitRoPE, EulerSampler, LatentOps, LinearExecutor, QKPrologue, QuantDecoders,
+    QuantizedLinearWeightBuffers, QwenLayerExecutor, WeightStreamer, as_buffer, qwen_rope,
 )
 
 __all__ = [
     "AnimaError", "LIB_PATH", "load", "AttentionExecutor", "BlockOps", "Context", "CrossKVCache",
-    "DiTBlockExecutor", "WeightStreamer",
+    "DiTBlockExecutor", "WeightStreamer", "DiTPreparationExecutor", "DiTFinalLayerExecutor", "EulerSampler",
+    "LatentOps",
     "DitRoPE", "LinearExecutor", "QKPrologue", "QuantDecoders", "QuantizedLinearWeightBuffers",
     "QwenLayerExecutor", "as_buffer", "qwen_rope",
 ]

@@ -110,6 +110,25 @@ class QwenLayerArgs(C.Structure):
                 ("eps", C.c_float)]
 
 
+class DitPrepareWeights(C.Structure):
+    _fields_ = [("x_embed", QWeight), ("t_embed1", QWeight), ("t_embed2", QWeight), ("t_norm", Buffer)]
+
+
+class DitPrepareArgs(C.Structure):
+    _fields_ = [("latent", Buffer), ("height", C.c_int64), ("width", C.c_int64), ("sigma", C.c_float),
+                ("residual", Buffer), ("emb", Buffer), ("adaln_lora", Buffer), ("dim", C.c_int64),
+                ("eps", C.c_float)]
+
+
+class DitFinalWeights(C.Structure):
+    _fields_ = [("mod_w1", QWeight), ("mod_w2", QWeight), ("proj", QWeight)]
+
+
+class DitFinalArgs(C.Structure):
+    _fields_ = [("residual", Buffer), ("emb", Buffer), ("adaln_lora", Buffer), ("velocity", Buffer),
+                ("height", C.c_int64), ("width", C.c_int64), ("dim", C.c_int64), ("eps", C.c_float)]
+
+
 # name -> (restype, argtypes)
 _P = C.c_void_p
 _PP = C.POINTER(C.c_void_p)
@@ -173,6 +192,17 @@ SIGNATURES = {
     "anima_weight_streamer_destroy": (_S, [_P]),
     "anima_linear_encode_head_rmsnorm": (_S, [_P, Buffer, _I64, C.POINTER(QWeight), Buffer, _I64, _I64, _I32,
                                               Buffer, _I64, C.c_float]),
+    "anima_patchify17_encode": (_S, [_P, Buffer, _I64, _I64, _I64, Buffer]),
+    "anima_unpatchify16_encode": (_S, [_P, Buffer, _I64, _I64, Buffer]),
+    "anima_unpatchify_velocity16_encode": (_S, [_P, Buffer, _I64, _I64, Buffer]),
+    "anima_flow_velocity_to_denoised_encode": (_S, [_P, Buffer, Buffer, Buffer, C.c_float, _I64]),
+    "anima_euler_step_encode": (_S, [_P, Buffer, Buffer, Buffer, C.c_float, C.c_float, _I64]),
+    "anima_dit_prepare_create": (_S, [_P, _PP]),
+    "anima_dit_prepare_destroy": (_S, [_P]),
+    "anima_dit_prepare_encode": (_S, [_P, C.POINTER(DitPrepareWeights), C.POINTER(DitPrepareArgs)]),
+    "anima_dit_final_create": (_S, [_P, _PP]),
+    "anima_dit_final_destroy": (_S, [_P]),
+    "anima_dit_final_encode": (_S, [_P, C.POINTER(DitFinalWeights), C.POINTER(DitFinalArgs)]),
 }
 
 _lib = None

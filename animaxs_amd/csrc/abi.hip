@@ -1,11 +1,13 @@
 // extern "C" entry points of libanima_hip (include/anima_hip.h).  Each converts
 // exceptions into an anima_status and the thread-local last-error message; no
 // entry point launches anything before its arguments validate.
+#include <cmath>
 #include <string>
 
 #include "attention.hpp"
 #include "block.hpp"
 #include "context.hpp"
+#include "dit_io.hpp"
 #include "linear.hpp"
 
 namespace anima {
@@ -438,6 +440,129 @@ anima_status anima_weight_streamer_create(anima_ctx* ctx, int64_t capacity, int3
 
 anima_status anima_weight_streamer_destroy(anima_weight_streamer* streamer) {
   return guarded([&] { delete streamer; });
+}
+
+// ---------------------------------------------------------------- DiT input / output and sampler
+
+static void check_sampler(const anima_buffer& b, int64_t count, const char* message) {
+  if (!b.ptr) fail(ANIMA_E_INVALID_ARGUMENT, message);
+  if (checked_product({count, 4}, "sampler") > b.length) fail(ANIMA_E_OUT_OF_BOUNDS, message);
+}
+
+static int64_t latent_floats(int64_t channels, int64_t height, int64_t width, const char* who) {
+  (void)patch_tokens(height, width, who);
+  return checked_product({channels, height, width}, who);
+}
+
+anima_status anima_patchify17_encode(anima_ctx* ctx, anima_buffer input, int64_t channels, int64_t height,
+                                     int64_t width, anima_buffer tokens) {
+  return guarded([&] {
+    require(ctx, "context");
+    if (channels != 16 && channels != 17) fail(ANIMA_E_INVALID_SHAPE, "patchify17 reads 16 or 17 channels");
+    const int64_t n = latent_floats(channels, height, width, "patchify17");
+    check_elementwise(input, n, 4, "patchify17 input");
+    check_elementwise(tokens, checked_product({height / 2, width / 2, 68}, "patchify17"), 4, "patchify17 tokens");
+    DeviceGuard g(ctx);
+    launch_patchify17(static_cast<const float*>(input.ptr), (int)channels, height, width,
+                      static_cast<float*>(tokens.ptr), ctx->stream);
+  });
+}
+
+anima_status anima_unpatchify16_encode(anima_ctx* ctx, anima_buffer tokens, int64_t height, int64_t width,
+                                       anima_buffer output) {
+  return guarded([&] {
+    require(ctx, "context");
+    const int64_t n = latent_floats(16, height, width, "unpatchify16");
+    check_elementwise(tokens, checked_product({height / 2, width / 2, 68}, "unpatchify16"), 4, "unpatchify16 tokens");
+    check_elementwise(output, n, 4, "unpatchify16 output");
+    DeviceGuard g(ctx);
+    launch_unpatchify16(static_cast<const float*>(tokens.ptr), height, width, static_cast<float*>(output.ptr),
+                        ctx->stream);
+  });
+}
+
+anima_status anima_unpatchify_velocity16_encode(anima_ctx* ctx, anima_buffer tokens, int64_t height, int64_t width,
+                                                anima_buffer output) {
+  return guarded([&] {
+    require(ctx, "context");
+    const int64_t n = latent_floats(16, height, width, "unpatchify_velocity16");
+    check_elementwise(tokens, n, 4, "unpatchify_velocity16 tokens");  // [T, 64] holds 16*H*W values
+    check_elementwise(output, n, 4, "unpatchify_velocity16 output");
+    DeviceGuard g(ctx);
+    launch_unpatchify_velocity16(static_cast<const float*>(tokens.ptr), height, width,
+                                 static_cast<float*>(output.ptr), ctx->stream);
+  });
+}
+
+anima_status anima_flow_velocity_to_denoised_encode(anima_ctx* ctx, anima_buffer x, anima_buffer velocity,
+                                                    anima_buffer denoised, float sigma, int64_t count) {
+  return guarded([&] {
+    require(ctx, "context");
+    const char* msg = "invalid FLOW conversion input";
+    if (count <= 0 || !std::isfinite(sigma)) fail(ANIMA_E_INVALID_ARGUMENT, msg);
+    check_sampler(x, count, msg);
+    check_sampler(velocity, count, msg);
+    check_sampler(denoised, count, msg);
+    DeviceGuard g(ctx);
+    launch_flow_denoised(static_cast<const float*>(x.ptr), static_cast<const float*>(velocity.ptr),
+                         static_cast<float*>(denoised.ptr), sigma, count, ctx->stream);
+  });
+}
+
+anima_status anima_euler_step_encode(anima_ctx* ctx, anima_buffer x, anima_buffer denoised, anima_buffer x_next,
+                                     float sigma, float next_sigma, int64_t count) {
+  return guarded([&] {
+    require(ctx, "context");
+    const char* msg = "invalid Euler sampler buffer or sigma";
+    if (count <= 0 || !std::isfinite(sigma) || !(sigma > 0.f) || !std::isfinite(next_sigma))
+      fail(ANIMA_E_INVALID_ARGUMENT, msg);
+    check_sampler(x, count, msg);
+    check_sampler(denoised, count, msg);
+    check_sampler(x_next, count, msg);
+    DeviceGuard g(ctx);
+    launch_euler_step(static_cast<const float*>(x.ptr), static_cast<const float*>(denoised.ptr),
+                      static_cast<float*>(x_next.ptr), sigma, next_sigma, count, ctx->stream);
+  });
+}
+
+anima_status anima_dit_prepare_create(anima_ctx* ctx, anima_dit_prepare** out) {
+  return guarded([&] {
+    require(out, "DiT preparation output");
+    *out = nullptr;
+    *out = new anima_dit_prepare(require(ctx, "context"));
+  });
+}
+
+anima_status anima_dit_prepare_destroy(anima_dit_prepare* prep) {
+  return guarded([&] { delete prep; });
+}
+
+anima_status anima_dit_prepare_encode(anima_dit_prepare* prep, const anima_dit_prepare_weights* w,
+                                      const anima_dit_prepare_args* args) {
+  return guarded([&] {
+    require(prep, "DiT preparation")->impl.encode(*require(w, "DiT preparation weights"),
+                                                  *require(args, "DiT preparation args"));
+  });
+}
+
+anima_status anima_dit_final_create(anima_ctx* ctx, anima_dit_final** out) {
+  return guarded([&] {
+    require(out, "DiT final-layer output");
+    *out = nullptr;
+    *out = new anima_dit_final(require(ctx, "context"));
+  });
+}
+
+anima_status anima_dit_final_destroy(anima_dit_final* fin) {
+  return guarded([&] { delete fin; });
+}
+
+anima_status anima_dit_final_encode(anima_dit_final* fin, const anima_dit_final_weights* w,
+                                    const anima_dit_final_args* args) {
+  return guarded([&] {
+    require(fin, "DiT final layer")->impl.encode(*require(w, "DiT final-layer weights"),
+                                                 *require(args, "DiT final-layer args"));
+  });
 }
 
 }  // extern "C"

@@ -48,8 +48,10 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 
 // dit_layernorm_modulate_to_half (AnimaKernels.metal:477-524):
 // half(((x - mean) * rsqrt(var + eps)) * (1 + scale) + shift), var the mean of the
-// squared deviations.
-template <int V>
+// squared deviations.  With HB (the FinalLayer's fp16 boundaries,
+// DiTFinalLayerExecutor.swift:134-157) the residual is read as float(half(x)) and the
+// normalised value is rounded through fp16 before the modulation.
+template <int V, bool HB>
 __global__ __launch_bounds__(256) void layernorm_modulate_wave_kernel(const float* __restrict__ residual,
                                                                       const float* __restrict__ mod,
                                                                       half_t* __restrict__ out, int n, int rows,
@@ -64,6 +66,10 @@ __global__ __launch_bounds__(256) void layernorm_modulate_wave_kernel(const floa
   for (int e = 0; e < V; ++e) {
     const int c = 4 * (lane + 64 * e);
     v[e] = c < n ? *reinterpret_cast<const floatx4*>(x + c) : floatx4{0.f, 0.f, 0.f, 0.f};
+    if (HB) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[e][u] = (float)(half_t)v[e][u];
+    }
     s += (v[e][0] + v[e][1]) + (v[e][2] + v[e][3]);
   }
   const float mean = wave_sum(s) / (float)n;
@@ -91,12 +97,17 @@ __global__ __launch_bounds__(256) void layernorm_modulate_wave_kernel(const floa
       const floatx4 sh = *reinterpret_cast<const floatx4*>(shift + c);
       half4v h;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) h[u] = f32_to_f16((v[e][u] - mean) * inv * (1.0f + sc[u]) + sh[u]);
+      for (int u = 0; u < 4; ++u) {
+        float nv = (v[e][u] - mean) * inv;
+        if (HB) nv = (float)f32_to_f16(nv);
+        h[u] = f32_to_f16(nv * (1.0f + sc[u]) + sh[u]);
+      }
       *reinterpret_cast<half4v*>(o + c) = h;
     }
   }
 }
 
+template <bool HB>
 __global__ __launch_bounds__(LN_NT) void layernorm_modulate_kernel(const float* __restrict__ residual,
                                                                    const float* __restrict__ mod, half_t* __restrict__ out,
                                                                    int n, float eps, int64_t mod_offset) {
@@ -108,7 +119,7 @@ __global__ __launch_bounds__(LN_NT) void layernorm_modulate_kernel(const float* 
 #pragma unroll
   for (int e = 0; e < LN_MAX_PER_THREAD; ++e) {
     const int i = threadIdx.x + e * LN_NT;
-    v[e] = i < n ? x[i] : 0.f;
+    v[e] = i < n ? (HB ? (float)(half_t)x[i] : x[i]) : 0.f;
     s += v[e];
   }
   const float mean = block_sum(s, red) / (float)n;
@@ -128,7 +139,11 @@ __global__ __launch_bounds__(LN_NT) void layernorm_modulate_kernel(const float* 
 #pragma unroll
   for (int e = 0; e < LN_MAX_PER_THREAD; ++e) {
     const int i = threadIdx.x + e * LN_NT;
-    if (i < n) o[i] = f32_to_f16((v[e] - mean) * inv * (1.0f + scale[i]) + shift[i]);
+    if (i < n) {
+      float nv = (v[e] - mean) * inv;
+      if (HB) nv = (float)f32_to_f16(nv);
+      o[i] = f32_to_f16(nv * (1.0f + scale[i]) + shift[i]);
+    }
   }
 }
 
@@ -332,29 +347,38 @@ static int wave_depth(int64_t n) {
   return 0;
 }
 
-void launch_layernorm_modulate(const float* residual, const float* mod, half_t* out, int64_t n, int64_t rows, float eps,
-                               int64_t mod_offset, hipStream_t stream) {
-  if (n > LN_NT * LN_MAX_PER_THREAD) fail(ANIMA_E_UNSUPPORTED, "layernorm-modulate supports rows of at most 8192");
-  if (rows > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "layernorm-modulate rows exceed int32");
-  if (rows <= 0 || n <= 0) return;
+template <bool HB>
+static void launch_layernorm_modulate_t(const float* residual, const float* mod, half_t* out, int64_t n, int64_t rows,
+                                        float eps, int64_t mod_offset, hipStream_t stream) {
   const int depth = wave_depth(n);
   if (depth && aligned16(residual) && aligned16(mod) && mod_offset % 4 == 0 && aligned8(out)) {
     const dim3 grid((unsigned)((rows + 3) / 4));
     switch (depth) {
-      case 2: hipLaunchKernelGGL(layernorm_modulate_wave_kernel<2>, grid, dim3(256), 0, stream, residual, mod, out,
-                                 (int)n, (int)rows, eps, mod_offset); break;
-      case 4: hipLaunchKernelGGL(layernorm_modulate_wave_kernel<4>, grid, dim3(256), 0, stream, residual, mod, out,
-                                 (int)n, (int)rows, eps, mod_offset); break;
-      case 8: hipLaunchKernelGGL(layernorm_modulate_wave_kernel<8>, grid, dim3(256), 0, stream, residual, mod, out,
-                                 (int)n, (int)rows, eps, mod_offset); break;
-      default: hipLaunchKernelGGL(layernorm_modulate_wave_kernel<16>, grid, dim3(256), 0, stream, residual, mod, out,
-                                  (int)n, (int)rows, eps, mod_offset); break;
+      case 2: hipLaunchKernelGGL((layernorm_modulate_wave_kernel<2, HB>), grid, dim3(256), 0, stream, residual, mod,
+                                 out, (int)n, (int)rows, eps, mod_offset); break;
+      case 4: hipLaunchKernelGGL((layernorm_modulate_wave_kernel<4, HB>), grid, dim3(256), 0, stream, residual, mod,
+                                 out, (int)n, (int)rows, eps, mod_offset); break;
+      case 8: hipLaunchKernelGGL((layernorm_modulate_wave_kernel<8, HB>), grid, dim3(256), 0, stream, residual, mod,
+                                 out, (int)n, (int)rows, eps, mod_offset); break;
+      default: hipLaunchKernelGGL((layernorm_modulate_wave_kernel<16, HB>), grid, dim3(256), 0, stream, residual, mod,
+                                  out, (int)n, (int)rows, eps, mod_offset); break;
     }
   } else {
-    hipLaunchKernelGGL(layernorm_modulate_kernel, dim3((unsigned)rows), dim3(LN_NT), 0, stream, residual, mod, out,
-                       (int)n, eps, mod_offset);
+    hipLaunchKernelGGL((layernorm_modulate_kernel<HB>), dim3((unsigned)rows), dim3(LN_NT), 0, stream, residual, mod,
+                       out, (int)n, eps, mod_offset);
   }
   ANIMA_HIP(hipGetLastError());
+}
+
+void launch_layernorm_modulate(const float* residual, const float* mod, half_t* out, int64_t n, int64_t rows, float eps,
+                               int64_t mod_offset, hipStream_t stream, bool fp16_boundaries) {
+  if (n > LN_NT * LN_MAX_PER_THREAD) fail(ANIMA_E_UNSUPPORTED, "layernorm-modulate supports rows of at most 8192");
+  if (rows > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "layernorm-modulate rows exceed int32");
+  if (rows <= 0 || n <= 0) return;
+  if (fp16_boundaries)
+    launch_layernorm_modulate_t<true>(residual, mod, out, n, rows, eps, mod_offset, stream);
+  else
+    launch_layernorm_modulate_t<false>(residual, mod, out, n, rows, eps, mod_offset, stream);
 }
 void launch_gate_add(float* residual, const half_t* branch, const float* gate, int64_t n, int64_t count,
                      hipStream_t stream) {

@@ -11,8 +11,10 @@
 
 namespace anima {
 
+// fp16_boundaries: the FinalLayer form (float(half(x)) in, the normalised value rounded
+// through fp16 before the modulation).
 void launch_layernorm_modulate(const float* residual, const float* mod, half_t* out, int64_t n, int64_t rows, float eps,
-                               int64_t mod_offset, hipStream_t stream);
+                               int64_t mod_offset, hipStream_t stream, bool fp16_boundaries = false);
 void launch_gate_add(float* residual, const half_t* branch, const float* gate, int64_t n, int64_t count,
                      hipStream_t stream);
 void launch_gelu(half_t* values, int64_t count, hipStream_t stream);

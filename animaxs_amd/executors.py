@@ -10,6 +10,11 @@ tests) read like the reference's own:
   * ``DitRoPE`` / ``qwen_rope``  Runtime/Text/DitRoPE.swift:58-107,
                            Runtime/Metal/QwenEncoderMetal.swift:126-143
   * ``DiTBlockExecutor``   AnimaXS/Runtime/Metal/DiTBlockExecutor.swift:155-282
+  * ``DiTPreparationExecutor`` / ``DiTFinalLayerExecutor``
+                           Runtime/Metal/DiTPreparationExecutor.swift:51-135,
+                           Runtime/Metal/DiTFinalLayerExecutor.swift:75-186
+  * ``EulerSampler`` / ``LatentOps``  Runtime/Sampler/EulerSampler.swift:6-90,
+                           Shaders/AnimaKernels.metal:1191-1297
 
 A "buffer" is anything with ``data_ptr()`` plus ``numel()``/``element_size()``
 (a device tensor), an ``(address, length)`` tuple, or an ``_abi.Buffer``.  The
@@ -32,7 +37,8 @@ from ._abi import AnimaError, call
 __all__ = [
     "AnimaError", "Context", "AttentionExecutor", "LinearExecutor", "QuantizedLinearWeightBuffers",
     "QKPrologue", "QuantDecoders", "DitRoPE", "qwen_rope", "DiTBlockExecutor", "BlockOps", "as_buffer",
-    "CrossKVCache", "WeightStreamer", "QwenLayerExecutor",
+    "CrossKVCache", "WeightStreamer", "QwenLayerExecutor", "LatentOps", "EulerSampler", "DiTPreparationExecutor",
+    "DiTFinalLayerExecutor",
 ]
 
 
@@ -568,6 +574,121 @@ class DiTBlockExecutor:
     def close(self):
         if self._h:
             call("anima_dit_block_destroy", self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class LatentOps:
+    """The latent-layout and sampler kernels of AnimaKernels.metal: patchify17 (:1225-1246),
+    unpatchify16 (:1251-1268), unpatchify_velocity16 (:1276-1297) and
+    flow_velocity_to_denoised_f32 (:1191-1201), fp32 buffers throughout."""
+
+    def __init__(self, context: Context):
+        self.context = context
+
+    def patchify17(self, input, tokens, height: int, width: int, channels: int = 17) -> None:
+        """[channels, H, W] -> [(H/2)*(W/2), 68]; channels 16 appends the zero mask channel."""
+        call("anima_patchify17_encode", self.context.handle, as_buffer(input), int(channels), int(height), int(width),
+             as_buffer(tokens))
+
+    def unpatchify16(self, tokens, output, height: int, width: int) -> None:
+        call("anima_unpatchify16_encode", self.context.handle, as_buffer(tokens), int(height), int(width),
+             as_buffer(output))
+
+    def unpatchify_velocity16(self, tokens, output, height: int, width: int) -> None:
+        call("anima_unpatchify_velocity16_encode", self.context.handle, as_buffer(tokens), int(height), int(width),
+             as_buffer(output))
+
+    def flow_velocity_to_denoised(self, x, velocity, denoised, sigma: float, count: int) -> None:
+        """DiffusionSampler.convertVelocity (DiffusionSampler.swift:380-402)."""
+        call("anima_flow_velocity_to_denoised_encode", self.context.handle, as_buffer(x), as_buffer(velocity),
+             as_buffer(denoised), float(sigma), int(count))
+
+
+class EulerSampler:
+    """EulerSampler (EulerSampler.swift:6-90): the Anima-Turbo 8-step schedule and the fp32
+    Euler update ``x_next = x + (next_sigma - sigma) * (x - denoised) / sigma``."""
+
+    SIGMAS = (1.0, 0.9546938, 0.90035903, 0.8339981, 0.7511211, 0.64468634, 0.50298506, 0.30500895, 0.0)
+
+    def __init__(self, context: Context):
+        self.context = context
+
+    @staticmethod
+    def cpu_step(latent, denoised, sigma: float, next_sigma: float) -> np.ndarray:
+        """EulerSampler.cpuStep (:29-40), a CPU function in the reference as well."""
+        x = np.asarray(latent, np.float32)
+        d = np.asarray(denoised, np.float32)
+        if x.size == 0 or x.shape != d.shape or not np.isfinite(sigma) or not sigma > 0 or not np.isfinite(next_sigma):
+            raise AnimaError(_abi.E_INVALID_ARGUMENT, "invalid Euler sampler input")
+        delta = np.float32(next_sigma) - np.float32(sigma)
+        return x + (x - d) / np.float32(sigma) * delta
+
+    def encode_step(self, latent, denoised, output, sigma: float, next_sigma: float, count: int) -> None:
+        call("anima_euler_step_encode", self.context.handle, as_buffer(latent), as_buffer(denoised),
+             as_buffer(output), float(sigma), float(next_sigma), int(count))
+
+
+class DiTPreparationExecutor:
+    """DiTPreparationExecutor.execute (DiTPreparationExecutor.swift:51-135): latent
+    ``[16, H, W]`` fp32 and sigma -> fp32 residual ``[(H/2)*(W/2), dim]``, timestep
+    embedding ``[dim]`` and AdaLN-LoRA base ``[3*dim]``.  ``weights`` holds
+    ``x_embed`` [dim, 68], ``t_embed1`` [dim, dim], ``t_embed2`` [3*dim, dim]
+    (QuantizedLinearWeightBuffers) and ``t_norm`` (fp16 [dim] device buffer)."""
+
+    def __init__(self, context: Context):
+        h = C.c_void_p()
+        call("anima_dit_prepare_create", context.handle, C.byref(h))
+        self._h = h
+        self.context = context
+
+    def execute(self, weights: dict, latent, sigma: float, residual, embedding, adaln_lora, height: int = 64,
+                width: int = 64, dim: int = 2048, eps: float = 1e-6) -> None:
+        w = _abi.DitPrepareWeights(weights["x_embed"].to_c(), weights["t_embed1"].to_c(), weights["t_embed2"].to_c(),
+                                   as_buffer(weights["t_norm"]))
+        a = _abi.DitPrepareArgs(as_buffer(latent), int(height), int(width), float(sigma), as_buffer(residual),
+                                as_buffer(embedding), as_buffer(adaln_lora), int(dim), float(eps))
+        call("anima_dit_prepare_encode", self._h, C.byref(w), C.byref(a))
+
+    def close(self):
+        if self._h:
+            call("anima_dit_prepare_destroy", self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DiTFinalLayerExecutor:
+    """DiTFinalLayerExecutor.execute (DiTFinalLayerExecutor.swift:75-186, fp16Legacy
+    residual boundary): fp32 residual, embedding and AdaLN-LoRA -> fp32 velocity
+    ``[16, H, W]``.  ``weights`` holds ``mod_w1`` [lora, dim], ``mod_w2`` [2*dim, lora]
+    and ``proj`` [64, dim]."""
+
+    def __init__(self, context: Context):
+        h = C.c_void_p()
+        call("anima_dit_final_create", context.handle, C.byref(h))
+        self._h = h
+        self.context = context
+
+    def execute(self, weights: dict, residual, emb, adaln_lora, velocity, height: int = 64, width: int = 64,
+                dim: int = 2048, eps: float = 1e-6) -> None:
+        w = _abi.DitFinalWeights(weights["mod_w1"].to_c(), weights["mod_w2"].to_c(), weights["proj"].to_c())
+        a = _abi.DitFinalArgs(as_buffer(residual), as_buffer(emb), as_buffer(adaln_lora), as_buffer(velocity),
+                              int(height), int(width), int(dim), float(eps))
+        call("anima_dit_final_encode", self._h, C.byref(w), C.byref(a))
+
+    def close(self):
+        if self._h:
+            call("anima_dit_final_destroy", self._h)
             self._h = C.c_void_p()
 
     def __del__(self):

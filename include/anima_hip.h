@@ -461,6 +461,90 @@ anima_status anima_dit_forward_encode_streamed(anima_dit_block* blk, anima_weigh
                                                anima_cross_kv_cache* cache);
 
 /* ------------------------------------------------------------------------- */
+/* DiT input / output and the sampler update (AnimaKernels.metal:1191-1297).   */
+/* Latents are fp32 [channels][height][width]; tokens are the 2x2 patches in   */
+/* row-major patch order, token t = (height/2 row, width/2 column).             */
+/* ------------------------------------------------------------------------- */
+/* patchify17 (AnimaKernels.metal:1218-1243): tokens[t][c*4 + di*2 + dj] =
+ * input[c][2i+di][2j+dj] for 17 channels.  channels = 17 reads the mask channel
+ * from input; channels = 16 treats it as zeros (the zero padding-mask channel that
+ * DiTPreparationExecutor appends, DiTPreparationExecutor.swift:82-89).  tokens is
+ * fp32 [(height/2)*(width/2)][68]. */
+anima_status anima_patchify17_encode(anima_ctx* ctx, anima_buffer input, int64_t channels, int64_t height,
+                                     int64_t width, anima_buffer tokens);
+/* unpatchify16 (AnimaKernels.metal:1247-1268): the first 16 channels of [T][68]
+ * tokens back to fp32 [16][height][width]. */
+anima_status anima_unpatchify16_encode(anima_ctx* ctx, anima_buffer tokens, int64_t height, int64_t width,
+                                       anima_buffer output);
+/* unpatchify_velocity16 (AnimaKernels.metal:1273-1296): FinalLayer tokens fp32
+ * [T][64] with element (di*2 + dj)*16 + c to fp32 [16][height][width]. */
+anima_status anima_unpatchify_velocity16_encode(anima_ctx* ctx, anima_buffer tokens, int64_t height,
+                                                int64_t width, anima_buffer output);
+/* flow_velocity_to_denoised_f32 (AnimaKernels.metal:1191-1201): denoised = x - sigma * velocity. */
+anima_status anima_flow_velocity_to_denoised_encode(anima_ctx* ctx, anima_buffer x, anima_buffer velocity,
+                                                    anima_buffer denoised, float sigma, int64_t count);
+/* EulerSampler.encodeStep + euler_step_f32 (EulerSampler.swift:43-70,
+ * AnimaKernels.metal:1206-1216): x_next = x + (next_sigma - sigma) * (x - denoised) * (1/sigma);
+ * sigma must be finite and > 0, next_sigma finite. */
+anima_status anima_euler_step_encode(anima_ctx* ctx, anima_buffer x, anima_buffer denoised, anima_buffer x_next,
+                                     float sigma, float next_sigma, int64_t count);
+
+/* DiTPreparationExecutor.execute (DiTPreparationExecutor.swift:51-135) at any even
+ * latent size: patchify the 16-channel latent with a zero mask channel, embed the
+ * patches (x_embedder linear [dim, 68]) into the fp32 residual, and for sigma build
+ * the sinusoidal timestep t (cos / sin halves, dit_source_oracle Timesteps), emb =
+ * RMSNorm(t) * t_norm and adaln_lora = t_embed2 . SiLU(t_embed1 . t). */
+typedef struct anima_dit_prepare_weights {
+  anima_qweight x_embed;    /* [dim, 68] */
+  anima_qweight t_embed1;   /* [dim, dim] */
+  anima_qweight t_embed2;   /* [3*dim, dim] */
+  anima_buffer t_norm;      /* fp16 [dim] */
+} anima_dit_prepare_weights;
+
+typedef struct anima_dit_prepare_args {
+  anima_buffer latent;      /* fp32 [16][height][width] */
+  int64_t height, width;    /* even */
+  float sigma;              /* finite */
+  anima_buffer residual;    /* out fp32 [(height/2)*(width/2)][dim] */
+  anima_buffer emb;         /* out fp32 [dim] */
+  anima_buffer adaln_lora;  /* out fp32 [3*dim] */
+  int64_t dim;              /* even */
+  float eps;                /* RMSNorm epsilon (1e-6) */
+} anima_dit_prepare_args;
+
+typedef struct anima_dit_prepare anima_dit_prepare;
+anima_status anima_dit_prepare_create(anima_ctx* ctx, anima_dit_prepare** out);
+anima_status anima_dit_prepare_destroy(anima_dit_prepare* prep);
+anima_status anima_dit_prepare_encode(anima_dit_prepare* prep, const anima_dit_prepare_weights* w,
+                                      const anima_dit_prepare_args* args);
+
+/* DiTFinalLayerExecutor.execute (DiTFinalLayerExecutor.swift:75-186, W4 fp16
+ * boundary): modulation = mod_w2 . (mod_w1 . SiLU(emb)) + adaln_lora[0 : 2*dim]
+ * split into (shift, scale); x = half(residual); n = half(LayerNorm(x)) with fp32
+ * statistics; y = half(n * (1 + scale) + shift); velocity = unpatchify_velocity16(
+ * float(half(proj . y))). */
+typedef struct anima_dit_final_weights {
+  anima_qweight mod_w1;     /* [lora, dim] */
+  anima_qweight mod_w2;     /* [2*dim, lora] */
+  anima_qweight proj;       /* [64, dim] */
+} anima_dit_final_weights;
+
+typedef struct anima_dit_final_args {
+  anima_buffer residual;    /* fp32 [(height/2)*(width/2)][dim] */
+  anima_buffer emb;         /* fp32 [dim] */
+  anima_buffer adaln_lora;  /* fp32 [>= 2*dim]; its first 2*dim values are added */
+  anima_buffer velocity;    /* out fp32 [16][height][width] */
+  int64_t height, width, dim;
+  float eps;                /* LayerNorm epsilon (1e-6) */
+} anima_dit_final_args;
+
+typedef struct anima_dit_final anima_dit_final;
+anima_status anima_dit_final_create(anima_ctx* ctx, anima_dit_final** out);
+anima_status anima_dit_final_destroy(anima_dit_final* fin);
+anima_status anima_dit_final_encode(anima_dit_final* fin, const anima_dit_final_weights* w,
+                                    const anima_dit_final_args* args);
+
+/* ------------------------------------------------------------------------- */
 /* Qwen encoder layer: QwenLayerExecutor.execute (QwenEncoderMetal.swift:232-304)  */
 /* for a batch of right-padded sequences, fp32 residual updated in place.        */
 /* ------------------------------------------------------------------------- */

@@ -13,7 +13,7 @@ known answers, closed forms, brute force) is listed in ``PINNING`` below and
 exercised by ``tests/test_oracle_*.py``.
 """
 
-from . import quant, rope, norms, attention, inputs, blocks  # noqa: F401
+from . import quant, rope, norms, attention, inputs, blocks, dit_io  # noqa: F401
 
 # function -> the independent checks that pin it (see tests/test_oracle_*.py)
 PINNING = {
@@ -49,6 +49,20 @@ PINNING = {
         "(:64-88); GQA 0,0,1,1 (:90-111, GqaHeadMappingTests.swift:23-89); "
         "tiny 2x3 case (DiTBlockTests.swift:117-147); additive finfo.min/4 mask "
         "equivalence (scripts/qwen_comfy_oracle.py:233-248)"),
+    "dit_io.timestep_sinusoid": (
+        "known answers of AnimaXSTests/TimestepEmbedderTests.swift:18-34 (cos/sin first 8 "
+        "at sigma 1) and DiTInputTests.swift:67-73; fp64 closed form at every schedule sigma"),
+    "dit_io.patchify17 / unpatchify16 / unpatchify_velocity16": (
+        "markers of DiTInputTests.swift:14-52; hand-computed entries of the 4x6 input of "
+        "MetalExecutionTests.swift:548-592; round trip; equality with the reshape/permute "
+        "form of scripts/dit_source_oracle.py:367-382"),
+    "dit_io.euler_step / flow_to_denoised": (
+        "hand-computed values of the MetalExecutionTests.swift:680-710 vectors; next_sigma = 0 "
+        "returns denoised; flow then Euler equals x + dsigma * velocity"),
+    "dit_io.prepare / final_layer": (
+        "closed forms with identity projections (emb = raw / sqrt(0.5 + eps), "
+        "adaln = SiLU(raw)); final layer on alternating-sign rows with exact fp16 "
+        "shift/scale outputs (detects a shift/scale swap and layout errors)"),
     "blocks.dit_block": (
         "composition of pinned parts following scripts/dit_block0_oracle.py:327-391; "
         "zero-gate identity and zero-weight invariants"),

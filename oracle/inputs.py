@@ -212,6 +212,28 @@ def qwen_layer(B: int = 4, S: int = 512, hidden: int = 1024, heads: int = 16, kv
     return d
 
 
+def dit_io(H: int = 64, W: int = 64, dim: int = DIM, lora: int = 256, seed: int = 1007,
+           storage: str = "w4") -> dict:
+    """The DiT preparation and final-layer inputs at a [16, H, W] latent: W4 (or W8 for
+    ``storage="w8"``) x_embedder [dim, 68], t_embedder linears [dim, dim] / [3*dim, dim],
+    final modulation [lora, dim] / [2*dim, lora] and projection [64, dim]; fp16 t_norm
+    ~U(0.8, 1.2); fp32 latent ~N(0, 1), residual ~N(0, 4), emb / adaln ~N(0, 1)."""
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    T = (H // 2) * (W // 2)
+    mk = symmetric_w4 if storage == "w4" else symmetric_w8
+    return {
+        "latent": torch.randn(16, H, W, generator=g, dtype=torch.float32),
+        "residual": torch.randn(T, dim, generator=g, dtype=torch.float32) * 2.0,
+        "emb": torch.randn(dim, generator=g, dtype=torch.float32),
+        "adaln": torch.randn(3 * dim, generator=g, dtype=torch.float32),
+        "t_norm": _uniform(g, 0.8, 1.2, dim).half(),
+        "w": {"x_embed": mk(g, dim, 68), "t_embed1": mk(g, dim, dim), "t_embed2": mk(g, 3 * dim, dim),
+              "mod_w1": mk(g, lora, dim), "mod_w2": mk(g, 2 * dim, lora), "proj": mk(g, 64, dim)},
+        "H": H, "W": W, "dim": dim, "eps": 1e-6,
+    }
+
+
 def small_m_gemm(M: int, N: int, K: int, seed: int = 1006) -> dict:
     """Small-M W4 GEMM sweep inputs: X ~N(0,1) fp16 [M,K], symmetric W4 [N,K]."""
     g = torch.Generator(device="cpu")

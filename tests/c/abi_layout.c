@@ -106,6 +106,23 @@ int main(void) {
   FIELD(anima_qwen_layer_args, tokens); FIELD(anima_qwen_layer_args, hidden); FIELD(anima_qwen_layer_args, heads);
   FIELD(anima_qwen_layer_args, kv_heads); FIELD(anima_qwen_layer_args, head_dim);
   FIELD(anima_qwen_layer_args, intermediate); FIELD(anima_qwen_layer_args, eps);
+
+  SIZE(anima_dit_prepare_weights);
+  FIELD(anima_dit_prepare_weights, x_embed); FIELD(anima_dit_prepare_weights, t_embed1);
+  FIELD(anima_dit_prepare_weights, t_embed2); FIELD(anima_dit_prepare_weights, t_norm);
+
+  SIZE(anima_dit_prepare_args);
+  FIELD(anima_dit_prepare_args, latent); FIELD(anima_dit_prepare_args, height); FIELD(anima_dit_prepare_args, width);
+  FIELD(anima_dit_prepare_args, sigma); FIELD(anima_dit_prepare_args, residual); FIELD(anima_dit_prepare_args, emb);
+  FIELD(anima_dit_prepare_args, adaln_lora); FIELD(anima_dit_prepare_args, dim); FIELD(anima_dit_prepare_args, eps);
+
+  SIZE(anima_dit_final_weights);
+  FIELD(anima_dit_final_weights, mod_w1); FIELD(anima_dit_final_weights, mod_w2); FIELD(anima_dit_final_weights, proj);
+
+  SIZE(anima_dit_final_args);
+  FIELD(anima_dit_final_args, residual); FIELD(anima_dit_final_args, emb); FIELD(anima_dit_final_args, adaln_lora);
+  FIELD(anima_dit_final_args, velocity); FIELD(anima_dit_final_args, height); FIELD(anima_dit_final_args, width);
+  FIELD(anima_dit_final_args, dim); FIELD(anima_dit_final_args, eps);
   printf("\n},\n\"rejections\": [\n");
 
   /* Requests that must fail validation, through the C entry points. */
@@ -161,6 +178,17 @@ int main(void) {
   anima_weight_streamer* st = NULL;
   rejection("streamer_slots", anima_weight_streamer_create(ctx, 1 << 20, 9, &st));
   rejection("rope_dit3d_shape", anima_rope_dit3d(0, 1, 1, NULL));
+  rejection("euler_sigma", anima_euler_step_encode(ctx, big, big, big, 0.0f, 0.5f, 4));
+  rejection("patchify_odd", anima_patchify17_encode(ctx, big, 17, 3, 4, big));
+  anima_dit_prepare* prep = NULL;
+  rejection("prepare_create", anima_dit_prepare_create(ctx, &prep));
+  anima_dit_prepare_weights pw;
+  memset(&pw, 0, sizeof pw);
+  anima_dit_prepare_args pa;
+  memset(&pa, 0, sizeof pa);
+  pa.sigma = 1.0f / 0.0f;
+  rejection("prepare_sigma", anima_dit_prepare_encode(prep, &pw, &pa));
+  anima_dit_prepare_destroy(prep);
 
   anima_linear_destroy(lin);
   anima_attention_destroy(attn);

@@ -30,6 +30,10 @@ STRUCTS = {
     "anima_dit_block_args": _abi.DitBlockArgs,
     "anima_qwen_layer_weights": _abi.QwenLayerWeights,
     "anima_qwen_layer_args": _abi.QwenLayerArgs,
+    "anima_dit_prepare_weights": _abi.DitPrepareWeights,
+    "anima_dit_prepare_args": _abi.DitPrepareArgs,
+    "anima_dit_final_weights": _abi.DitFinalWeights,
+    "anima_dit_final_args": _abi.DitFinalArgs,
 }
 
 
@@ -69,7 +73,7 @@ def test_every_struct_field_matches_ctypes(report):
 
 def test_rejections_through_the_c_entry_points(report):
     got = {name: (status, msg) for name, status, msg in report["rejections"]}
-    ok = {"ctx_create", "attention_create", "linear_create"}
+    ok = {"ctx_create", "attention_create", "linear_create", "prepare_create"}
     for name in ok:
         assert got[name][0] == _abi.OK, (name, got[name])
     want = {
@@ -87,6 +91,9 @@ def test_rejections_through_the_c_entry_points(report):
         "cache_shape": (_abi.E_INVALID_SHAPE, "invalid cross K/V cache shape"),
         "streamer_slots": (_abi.E_INVALID_ARGUMENT, "weight slot count must be in 1...4"),
         "rope_dit3d_shape": (_abi.E_INVALID_SHAPE, ""),
+        "euler_sigma": (_abi.E_INVALID_ARGUMENT, "invalid Euler sampler buffer or sigma"),
+        "patchify_odd": (_abi.E_INVALID_SHAPE, "even height and width"),
+        "prepare_sigma": (_abi.E_INVALID_ARGUMENT, "invalid DiT preparation input"),
     }
     for name, (status, fragment) in want.items():
         st, msg = got[name]

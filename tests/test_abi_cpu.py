@@ -368,3 +368,86 @@ def test_as_buffer_rejects_host_and_strided_tensors():
             return 2
     with pytest.raises(TypeError, match="contiguous"):
         animaxs_amd.as_buffer(View())
+
+
+def test_latent_and_sampler_kernel_checks(ctx):
+    """patchify/unpatchify shapes and ranges; EulerSampler.encodeStep / convertVelocity
+    rejections (EulerSampler.swift:47-51, DiffusionSampler.swift:380-385)."""
+    ops, eu = animaxs_amd.LatentOps(ctx), animaxs_amd.EulerSampler(ctx)
+    expect(lambda: ops.patchify17(buf(17 * 16 * 4), buf(4 * 68 * 4), 3, 4), _abi.E_INVALID_SHAPE, "even height")
+    expect(lambda: ops.patchify17(buf(15 * 16 * 4), buf(4 * 68 * 4), 4, 4, channels=15), _abi.E_INVALID_SHAPE,
+           "16 or 17 channels")
+    expect(lambda: ops.patchify17(buf(17 * 16 * 4 - 4), buf(4 * 68 * 4), 4, 4), _abi.E_OUT_OF_BOUNDS,
+           "patchify17 input buffer range")
+    expect(lambda: ops.patchify17(buf(16 * 16 * 4), buf(4 * 68 * 4 - 4), 4, 4, channels=16), _abi.E_OUT_OF_BOUNDS,
+           "patchify17 tokens buffer range")
+    expect(lambda: ops.unpatchify16(buf(4 * 68 * 4), buf(16 * 16 * 4 - 4), 4, 4), _abi.E_OUT_OF_BOUNDS,
+           "unpatchify16 output")
+    expect(lambda: ops.unpatchify_velocity16(buf(4 * 64 * 4 - 4), buf(16 * 16 * 4), 4, 4), _abi.E_OUT_OF_BOUNDS,
+           "unpatchify_velocity16 tokens")
+    expect(lambda: ops.patchify17(buf(1 << 40), buf(1 << 40), 1 << 20, 1 << 20), _abi.E_INVALID_SHAPE, "too large")
+    msg = "invalid Euler sampler buffer or sigma"
+    for s, ns, n in ((0.0, 0.5, 8), (-1.0, 0.5, 8), (float("nan"), 0.5, 8), (1.0, float("inf"), 8), (1.0, 0.5, 0)):
+        expect(lambda: eu.encode_step(buf(32), buf(32), buf(32), s, ns, n), _abi.E_INVALID_ARGUMENT, msg)
+    expect(lambda: eu.encode_step(buf(32), buf(28), buf(32), 1.0, 0.5, 8), _abi.E_OUT_OF_BOUNDS, msg)
+    expect(lambda: eu.encode_step(buf(32), buf(32), (0, 32), 1.0, 0.5, 8), _abi.E_INVALID_ARGUMENT, msg)
+    fmsg = "invalid FLOW conversion input"
+    expect(lambda: ops.flow_velocity_to_denoised(buf(32), buf(32), buf(32), float("nan"), 8), _abi.E_INVALID_ARGUMENT,
+           fmsg)
+    expect(lambda: ops.flow_velocity_to_denoised(buf(32), buf(31), buf(32), 0.5, 8), _abi.E_OUT_OF_BOUNDS, fmsg)
+
+
+def _io_weights(dim=256, lora=32):
+    return {"x_embed": w4(rows=dim, cols=68), "t_embed1": w4(rows=dim, cols=dim), "t_embed2": w4(rows=3 * dim, cols=dim),
+            "t_norm": buf(dim * 2), "mod_w1": w4(rows=lora, cols=dim), "mod_w2": w4(rows=2 * dim, cols=lora),
+            "proj": w4(rows=64, cols=dim)}
+
+
+def test_dit_preparation_validation(ctx):
+    """DiTPreparationExecutor.execute guards (DiTPreparationExecutor.swift:55-61, :297-323)."""
+    prep = animaxs_amd.DiTPreparationExecutor(ctx)
+    w = _io_weights()
+    H = W = 8
+    a = dict(latent=buf(16 * H * W * 4), residual=buf(16 * 256 * 4), embedding=buf(256 * 4), adaln_lora=buf(768 * 4))
+
+    def run(w=w, sigma=0.5, **over):
+        kw = dict(a, height=H, width=W, dim=256)
+        kw.update(over)
+        return lambda: prep.execute(w, kw.pop("latent"), sigma, kw.pop("residual"), kw.pop("embedding"),
+                                    kw.pop("adaln_lora"), **kw)
+
+    for s in (float("nan"), float("inf")):
+        expect(run(sigma=s), _abi.E_INVALID_ARGUMENT, "invalid DiT preparation input")
+    expect(run(height=6, width=7), _abi.E_INVALID_SHAPE, "even height and width")
+    expect(run(dim=255), _abi.E_INVALID_SHAPE, "hidden width must be even")
+    expect(run(dim=8194), _abi.E_INVALID_SHAPE, "at most 8192")
+    expect(run(w=dict(w, x_embed=w4(rows=256, cols=64))), _abi.E_INVALID_SHAPE, "x_embedder must be [256, 68]")
+    expect(run(w=dict(w, t_embed2=w4(rows=512, cols=256))), _abi.E_INVALID_SHAPE, "linear_2 must be [768, 256]")
+    expect(run(w=dict(w, t_norm=buf(510))), _abi.E_OUT_OF_BOUNDS, "t_embedding_norm buffer is too small")
+    expect(run(w=dict(w, t_norm=None)), _abi.E_INVALID_ARGUMENT, "t_embedding_norm pointer is null")
+    for name, what in (("latent", "latent"), ("residual", "residual"), ("embedding", "embedding"),
+                       ("adaln_lora", "adaln_lora")):
+        expect(run(**{name: buf(a[name][1] - 4)}), _abi.E_OUT_OF_BOUNDS, f"DiT preparation {what} buffer is too small")
+        expect(run(**{name: (0, a[name][1])}), _abi.E_INVALID_ARGUMENT, f"DiT preparation {what} pointer is null")
+
+
+def test_dit_final_layer_validation(ctx):
+    """DiTFinalLayerExecutor.validate / FinalWeights (DiTFinalLayerExecutor.swift:382-420)."""
+    fin = animaxs_amd.DiTFinalLayerExecutor(ctx)
+    w = _io_weights()
+    H = W = 8
+    a = dict(residual=buf(16 * 256 * 4), emb=buf(256 * 4), adaln_lora=buf(512 * 4), velocity=buf(16 * H * W * 4))
+
+    def run(w=w, **over):
+        kw = dict(a, height=H, width=W, dim=256)
+        kw.update(over)
+        return lambda: fin.execute(w, kw.pop("residual"), kw.pop("emb"), kw.pop("adaln_lora"), kw.pop("velocity"),
+                                   **kw)
+
+    expect(run(w=dict(w, mod_w1=w4(rows=32, cols=128))), _abi.E_INVALID_SHAPE, "must have dim columns")
+    expect(run(w=dict(w, mod_w2=w4(rows=512, cols=16))), _abi.E_INVALID_SHAPE, "adaln_modulation.2 must be [512, 32]")
+    expect(run(w=dict(w, proj=w4(rows=16, cols=256))), _abi.E_INVALID_SHAPE, "linear must be [64, 256]")
+    expect(run(height=9), _abi.E_INVALID_SHAPE, "even height and width")
+    expect(run(eps=float("nan")), _abi.E_INVALID_ARGUMENT, "epsilon")
+    for name in a:
+        expect(run(**{name: buf(a[name][1] - 4)}), _abi.E_OUT_OF_BOUNDS, "buffer is too small")
