@@ -6,6 +6,7 @@ reference's Swift operator surface in Python over that ABI (``executors``).
 """
 
 from ._abi import AnimaError, LIB_PATH, load  # noqa: F401
+from .animapk import AnimapkExecutionRange, AnimapkFile, AnimapkTensor, DiTBlockLocator  # noqa: F401
 from .executors import (  # noqa: F401
     AttentionExecutor, BlockOps, Context, CrossKVCache, DiTBlockExecutor, DiTFinalLayerExecutor,
     DiTPreparationExecutor, DitRoPE, EulerSampler, LatentOps, LinearExecutor, QKPrologue, QuantDecoders,
@@ -15,7 +16,7 @@ from .executors import (  # noqa: F401
 __all__ = [
     "AnimaError", "LIB_PATH", "load", "AttentionExecutor", "BlockOps", "Context", "CrossKVCache",
     "DiTBlockExecutor", "WeightStreamer", "DiTPreparationExecutor", "DiTFinalLayerExecutor", "EulerSampler",
-    "LatentOps",
+    "LatentOps", "AnimapkFile", "AnimapkTensor", "AnimapkExecutionRange", "DiTBlockLocator",
     "DitRoPE", "LinearExecutor", "QKPrologue", "QuantDecoders", "QuantizedLinearWeightBuffers",
     "QwenLayerExecutor", "as_buffer", "qwen_rope",
 ]

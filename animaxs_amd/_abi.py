@@ -14,10 +14,11 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libanima_hip.so"
 
 # anima_status
-OK, E_INVALID_SHAPE, E_OUT_OF_BOUNDS, E_OVERFLOW, E_MISALIGNED, E_UNSUPPORTED, E_DEVICE, E_INVALID_ARGUMENT = range(8)
+(OK, E_INVALID_SHAPE, E_OUT_OF_BOUNDS, E_OVERFLOW, E_MISALIGNED, E_UNSUPPORTED, E_DEVICE, E_INVALID_ARGUMENT,
+ E_FORMAT, E_IO) = range(10)
 STATUS_NAMES = {
     0: "OK", 1: "INVALID_SHAPE", 2: "OUT_OF_BOUNDS", 3: "OVERFLOW", 4: "MISALIGNED",
-    5: "UNSUPPORTED", 6: "DEVICE", 7: "INVALID_ARGUMENT",
+    5: "UNSUPPORTED", 6: "DEVICE", 7: "INVALID_ARGUMENT", 8: "FORMAT", 9: "IO",
 }
 
 # enums
@@ -129,6 +130,28 @@ class DitFinalArgs(C.Structure):
                 ("height", C.c_int64), ("width", C.c_int64), ("dim", C.c_int64), ("eps", C.c_float)]
 
 
+class PackInfo(C.Structure):
+    _fields_ = [("version", C.c_int32), ("component", C.c_int32), ("alignment", C.c_int64),
+                ("tensor_count", C.c_int64), ("json_offset", C.c_int64), ("json_size", C.c_int64),
+                ("table_offset", C.c_int64), ("table_bytes", C.c_int64), ("payload_offset", C.c_int64),
+                ("file_size", C.c_int64), ("record_size", C.c_int32), ("quant_group", C.c_int32),
+                ("quant_scheme", C.c_char_p), ("component_name", C.c_char_p)]
+
+
+class PackTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("storage", C.c_int32), ("rank", C.c_int32), ("shape", C.c_int64 * 8),
+                ("blob_offset", C.c_int64), ("blob_size", C.c_int64), ("data_offset", C.c_int64),
+                ("data_size", C.c_int64), ("scale_offset", C.c_int64), ("scale_size", C.c_int64),
+                ("zero_offset", C.c_int64), ("zero_size", C.c_int64), ("block_index", C.c_int64),
+                ("crc32", C.c_uint32), ("has_crc32", C.c_int32), ("logical_dtype", C.c_char_p),
+                ("quantization_format", C.c_char_p)]
+
+
+class PackRange(C.Structure):
+    _fields_ = [("logical_index", C.c_int64), ("file_offset", C.c_int64), ("length", C.c_int64),
+                ("tensor_count", C.c_int64), ("host", C.c_void_p)]
+
+
 # name -> (restype, argtypes)
 _P = C.c_void_p
 _PP = C.POINTER(C.c_void_p)
@@ -203,6 +226,21 @@ SIGNATURES = {
     "anima_dit_final_create": (_S, [_P, _PP]),
     "anima_dit_final_destroy": (_S, [_P]),
     "anima_dit_final_encode": (_S, [_P, C.POINTER(DitFinalWeights), C.POINTER(DitFinalArgs)]),
+    "anima_pack_open": (_S, [C.c_char_p, _PP]),
+    "anima_pack_close": (_S, [_P]),
+    "anima_pack_get_info": (_S, [_P, C.POINTER(PackInfo)]),
+    "anima_pack_tensor_at": (_S, [_P, _I64, C.POINTER(PackTensor)]),
+    "anima_pack_find": (_S, [_P, C.c_char_p, C.POINTER(PackTensor)]),
+    "anima_pack_crc32_mismatch_count": (_S, [_P, C.POINTER(C.c_int64)]),
+    "anima_pack_bytes": (_S, [_P, _I64, _I64, C.POINTER(C.c_void_p)]),
+    "anima_pack_execution_ranges": (_S, [_P, C.c_char_p, _I64, C.POINTER(PackRange)]),
+    "anima_pack_dit_block": (_S, [_P, _I64, C.POINTER(DitBlockWeights), C.POINTER(PackRange)]),
+    "anima_pack_dit_prepare": (_S, [_P, _I64, C.POINTER(DitPrepareWeights), C.POINTER(PackRange)]),
+    "anima_pack_dit_final": (_S, [_P, _I64, C.POINTER(DitFinalWeights), C.POINTER(PackRange)]),
+    "anima_dit_block_weights_rebase": (_S, [C.POINTER(DitBlockWeights), _P, _I64, C.POINTER(DitBlockWeights)]),
+    "anima_dit_prepare_weights_rebase": (_S, [C.POINTER(DitPrepareWeights), _P, _I64,
+                                              C.POINTER(DitPrepareWeights)]),
+    "anima_dit_final_weights_rebase": (_S, [C.POINTER(DitFinalWeights), _P, _I64, C.POINTER(DitFinalWeights)]),
 }
 
 _lib = None

@@ -13,6 +13,7 @@
 #include "attention.hpp"
 #include "block.hpp"
 #include "linear.hpp"
+#include "pack.hpp"
 
 namespace anima {
 
@@ -643,34 +644,6 @@ void DitBlockExecutor::forward(const anima_dit_block_weights* blocks, int64_t co
 
 // Rebase one template buffer (ptr holds a byte offset into the block's range) onto
 // the slot the range was copied to.
-static anima_buffer rebase(const anima_buffer& t, char* base, int64_t range_bytes, const char* what) {
-  const uintptr_t off = reinterpret_cast<uintptr_t>(t.ptr);
-  if (off > (uintptr_t)range_bytes)
-    fail(ANIMA_E_OUT_OF_BOUNDS, std::string("streamed ") + what + " offset lies outside its block range");
-  return anima_buffer{base + off, range_bytes - (int64_t)off};
-}
-
-static anima_qweight rebase(const anima_qweight& t, char* base, int64_t range_bytes, const char* what) {
-  anima_qweight q = t;
-  q.packed = rebase(t.packed, base, range_bytes, what);
-  q.scale = rebase(t.scale, base, range_bytes, what);
-  q.zero = rebase(t.zero, base, range_bytes, what);
-  return q;
-}
-
-static anima_dit_block_weights rebase(const anima_dit_block_weights& t, char* base, int64_t range_bytes) {
-  anima_dit_block_weights w = t;
-  anima_qweight* dst[] = {&w.self_q, &w.self_k, &w.self_v, &w.self_o, &w.cross_q, &w.cross_k, &w.cross_v, &w.cross_o,
-                          &w.mlp1, &w.mlp2, &w.mod_self_w1, &w.mod_self_w2, &w.mod_cross_w1, &w.mod_cross_w2,
-                          &w.mod_mlp_w1, &w.mod_mlp_w2};
-  for (anima_qweight* q : dst) *q = rebase(*q, base, range_bytes, "weight");
-  w.self_q_norm = rebase(t.self_q_norm, base, range_bytes, "norm weight");
-  w.self_k_norm = rebase(t.self_k_norm, base, range_bytes, "norm weight");
-  w.cross_q_norm = rebase(t.cross_q_norm, base, range_bytes, "norm weight");
-  w.cross_k_norm = rebase(t.cross_k_norm, base, range_bytes, "norm weight");
-  return w;
-}
-
 void DitBlockExecutor::forward_streamed(WeightStreamer& st, const anima_dit_block_weights* templates,
                                         const void* const* ranges, const int64_t* range_bytes, int64_t count,
                                         const anima_dit_block_args& a, CrossKVCache* cache) {
@@ -683,7 +656,7 @@ void DitBlockExecutor::forward_streamed(WeightStreamer& st, const anima_dit_bloc
     if (!ranges[i]) fail(ANIMA_E_INVALID_ARGUMENT, "streamed block range pointer is null");
     if (range_bytes[i] <= 0 || range_bytes[i] > st.capacity())
       fail(ANIMA_E_OUT_OF_BOUNDS, "execution range does not fit the weight slot");
-    check(rebase(templates[i], st.slot((int)(i % st.slots())), range_bytes[i]), a, cache, i);
+    check(rebase_block(templates[i], st.slot((int)(i % st.slots())), range_bytes[i]), a, cache, i);
   }
   DeviceGuard guard(ctx_);
   // DitForward.loopStep (DitForward.swift:21-35): with two or more slots block i runs from
@@ -701,7 +674,7 @@ void DitBlockExecutor::forward_streamed(WeightStreamer& st, const anima_dit_bloc
       st.load(ns, ranges[i + 1], range_bytes[i + 1]);
     }
     st.acquire(s);
-    encode(rebase(templates[i], st.slot(s), range_bytes[i]), a, cache, i);
+    encode(rebase_block(templates[i], st.slot(s), range_bytes[i]), a, cache, i);
     st.release(s);
   }
 }

@@ -526,7 +526,11 @@ class DiTBlockExecutor:
         self.context = context
 
     @classmethod
-    def weights_struct(cls, weights: dict, norms: dict) -> _abi.DitBlockWeights:
+    def weights_struct(cls, weights, norms: Optional[dict] = None) -> _abi.DitBlockWeights:
+        """A dict of QuantizedLinearWeightBuffers plus a dict of norm buffers, or a ready
+        ``_abi.DitBlockWeights`` (for example a rebased pack template), passed through."""
+        if isinstance(weights, _abi.DitBlockWeights):
+            return weights
         w = _abi.DitBlockWeights()
         for n in cls.NAMES:
             setattr(w, n, weights[n].to_c())
@@ -553,8 +557,10 @@ class DiTBlockExecutor:
 
     def forward(self, blocks: list, residual, emb, adaln_lora, context_tokens_buf, rope, tokens: int,
                 cache: Optional[CrossKVCache] = None, **shape) -> None:
-        """``blocks`` is a list of (weights, norms) pairs, run in order over the residual."""
-        arr = (_abi.DitBlockWeights * len(blocks))(*[self.weights_struct(w, n) for w, n in blocks])
+        """``blocks`` is a list of (weights, norms) pairs or of ``_abi.DitBlockWeights``, run in
+        order over the residual."""
+        structs = [b if isinstance(b, _abi.DitBlockWeights) else self.weights_struct(*b) for b in blocks]
+        arr = (_abi.DitBlockWeights * len(blocks))(*structs)
         a = self.args_struct(residual, emb, adaln_lora, context_tokens_buf, rope, tokens, **shape)
         call("anima_dit_forward_encode", self._h, arr, len(blocks), C.byref(a), cache.handle if cache else None)
 
@@ -649,8 +655,11 @@ class DiTPreparationExecutor:
 
     def execute(self, weights: dict, latent, sigma: float, residual, embedding, adaln_lora, height: int = 64,
                 width: int = 64, dim: int = 2048, eps: float = 1e-6) -> None:
-        w = _abi.DitPrepareWeights(weights["x_embed"].to_c(), weights["t_embed1"].to_c(), weights["t_embed2"].to_c(),
-                                   as_buffer(weights["t_norm"]))
+        if isinstance(weights, _abi.DitPrepareWeights):
+            w = weights
+        else:
+            w = _abi.DitPrepareWeights(weights["x_embed"].to_c(), weights["t_embed1"].to_c(),
+                                       weights["t_embed2"].to_c(), as_buffer(weights["t_norm"]))
         a = _abi.DitPrepareArgs(as_buffer(latent), int(height), int(width), float(sigma), as_buffer(residual),
                                 as_buffer(embedding), as_buffer(adaln_lora), int(dim), float(eps))
         call("anima_dit_prepare_encode", self._h, C.byref(w), C.byref(a))
@@ -681,7 +690,10 @@ class DiTFinalLayerExecutor:
 
     def execute(self, weights: dict, residual, emb, adaln_lora, velocity, height: int = 64, width: int = 64,
                 dim: int = 2048, eps: float = 1e-6) -> None:
-        w = _abi.DitFinalWeights(weights["mod_w1"].to_c(), weights["mod_w2"].to_c(), weights["proj"].to_c())
+        if isinstance(weights, _abi.DitFinalWeights):
+            w = weights
+        else:
+            w = _abi.DitFinalWeights(weights["mod_w1"].to_c(), weights["mod_w2"].to_c(), weights["proj"].to_c())
         a = _abi.DitFinalArgs(as_buffer(residual), as_buffer(emb), as_buffer(adaln_lora), as_buffer(velocity),
                               int(height), int(width), int(dim), float(eps))
         call("anima_dit_final_encode", self._h, C.byref(w), C.byref(a))

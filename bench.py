@@ -42,6 +42,8 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="skip the per-workload table")
     ap.add_argument("--profile-block", action="store_true",
                     help="only run the S=4096 DiT block (--block-steps times), for a rocprofv3 kernel trace")
+    ap.add_argument("--profile-step", action="store_true",
+                    help="only the 1024px sampler step (for a kernel trace of the whole step)")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="only launch the dominant flash kernel (--warmup + --steps times) and a 256 MiB "
                          "calibration copy, for rocprofv3 counter passes; prints no JSON")
@@ -155,6 +157,11 @@ def main():
         ms = time_block(torch, A, ctx, stream, args)
         print(f"# profile-block: DiT block S4096 {ms:.3f} ms", file=sys.stderr)
         return
+    if args.profile_step:
+        st_ms, first_ms, fwd_ms, finite = time_sampler_step(torch, A, ctx, stream, args)
+        print(f"# profile-step: sampler step 1024px {st_ms:.3f} ms (first {first_ms:.3f} ms, 28-block forward "
+              f"{fwd_ms:.3f} ms, velocity finite {finite})", file=sys.stderr)
+        return
 
     # ---------------- headline: S=4096 self-attention with fused norm+RoPE ----------------
     sets, qw, kw = gen_attention_inputs(torch, 4)
@@ -228,6 +235,14 @@ def main():
         qwen = time_qwen_layer(torch, A, ctx, stream, args)
         extra["qwen_layer_b4_s512"] = qwen
         print(f"# Qwen layer B4 S512: {qwen}", file=sys.stderr, flush=True)
+        st_ms, first_ms, fwd_ms, finite = time_sampler_step(torch, A, ctx, stream, args)
+        extra["sampler_step_1024px"] = {
+            "ms": round(st_ms, 3), "first_step_ms": round(first_ms, 3), "forward_28_blocks_ms": round(fwd_ms, 3),
+            "ms_per_block": round(fwd_ms / 28, 4), "generation_8_steps_ms": round(first_ms + 7 * st_ms, 2),
+            "velocity_finite": finite,
+            "includes": "DiT preparation + 28 W4 blocks (cross K/V cached after step 1) + final layer + "
+                        "flow-to-denoised + Euler; weights resident"}
+        print(f"# sampler step 1024px: {extra['sampler_step_1024px']}", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -396,6 +411,84 @@ def time_block(torch, A, ctx, stream, args):
         blk.encode(weights, norms, residual, emb, adaln, ctxt, rope, tokens=S)
 
     return time_region(torch, stream, step, args.block_steps, 2)
+
+
+def time_sampler_step(torch, A, ctx, stream, args, blocks=28):
+    """One denoising step of the 1024px configuration (DiffusionSampler.swift:212-250):
+    DiTPreparation on the [16, 128, 128] latent (4096 tokens) -> 28 DiT blocks (all ten
+    linears W4, cross-attention K/V from the cache) -> final layer -> flow-to-denoised ->
+    Euler.  Returns (ms per step with the cache filled, ms of the first step that fills
+    it, ms of the 28-block forward alone, velocity finite)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1008)
+    dim, hidden, T, C, side = 2048, 8192, 512, 1024, 128
+    keep = []
+
+    def w4(n, k):
+        st, gr = (k + 1) // 2, (k + 63) // 64
+        p = torch.randint(0, 256, (n, st), device="cuda", generator=g, dtype=torch.uint8)
+        sc = (0.005 + 0.015 * torch.rand(n, gr, device="cuda", generator=g)).half()
+        z = (-8 * sc.float()).half()
+        keep.extend([p, sc, z])
+        return A.QuantizedLinearWeightBuffers(0, p, sc, z, n, k, st)
+
+    def f16(n, k):
+        w = (0.02 * torch.randn(n, k, device="cuda", generator=g)).half()
+        keep.append(w)
+        return A.QuantizedLinearWeightBuffers(2, w, w, w, n, k, k)
+
+    shapes = {"self_q": (dim, dim), "self_k": (dim, dim), "self_v": (dim, dim), "self_o": (dim, dim),
+              "cross_q": (dim, dim), "cross_k": (dim, C), "cross_v": (dim, C), "cross_o": (dim, dim),
+              "mlp1": (hidden, dim), "mlp2": (dim, hidden)}
+    block_list = []
+    for _ in range(blocks):
+        weights = {n: w4(*sh) for n, sh in shapes.items()}
+        for br in ("self", "cross", "mlp"):
+            weights[f"mod_{br}_w1"] = f16(256, dim)
+            weights[f"mod_{br}_w2"] = f16(3 * dim, 256)
+        norms = {n: (0.8 + 0.4 * torch.rand(128, device="cuda", generator=g)).half()
+                 for n in ("self_q_norm", "self_k_norm", "cross_q_norm", "cross_k_norm")}
+        block_list.append((weights, norms))
+    pw = {"x_embed": w4(dim, 68), "t_embed1": w4(dim, dim), "t_embed2": w4(3 * dim, dim),
+          "t_norm": (0.8 + 0.4 * torch.rand(dim, device="cuda", generator=g)).half()}
+    fw = {"mod_w1": w4(256, dim), "mod_w2": w4(2 * dim, 256), "proj": w4(64, dim)}
+    latent = torch.randn(16, side, side, device="cuda", generator=g)
+    ctxt = torch.randn(T, C, device="cuda", generator=g).half()
+    rope = torch.from_numpy(A.DitRoPE.generate(1, SIDE, SIDE)).cuda()
+    residual = torch.empty(S, dim, device="cuda")
+    emb = torch.empty(dim, device="cuda")
+    adaln = torch.empty(3 * dim, device="cuda")
+    vel = torch.empty(16, side, side, device="cuda")
+    den, nxt = torch.empty_like(vel), torch.empty_like(vel)
+    prep, fin, blk = A.DiTPreparationExecutor(ctx), A.DiTFinalLayerExecutor(ctx), A.DiTBlockExecutor(ctx)
+    ops, eu = A.LatentOps(ctx), A.EulerSampler(ctx)
+    cache = A.CrossKVCache(ctx, blocks)
+    sig = A.EulerSampler.SIGMAS
+    n = vel.numel()
+
+    def step(i):
+        s, ns = sig[i % 8], sig[i % 8 + 1]
+        prep.execute(pw, latent, s, residual, emb, adaln, height=side, width=side)
+        blk.forward(block_list, residual, emb, adaln, ctxt, rope, tokens=S, cache=cache)
+        fin.execute(fw, residual, emb, adaln, vel, height=side, width=side)
+        ops.flow_velocity_to_denoised(latent, vel, den, s, n)
+        eu.encode_step(latent, den, nxt, s, ns, n)
+
+    def forward_only(i):
+        blk.forward(block_list, residual, emb, adaln, ctxt, rope, tokens=S, cache=cache)
+
+    # the first step projects every block's context K/V into the cache
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    step(0)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    first_ms = e0.elapsed_time(e1)
+    finite = bool(torch.isfinite(vel).all())
+    ms = time_region(torch, stream, step, args.block_steps, 1)
+    fwd = time_region(torch, stream, forward_only, args.block_steps, 1)
+    return ms, first_ms, fwd, finite
 
 
 def time_qwen_layer(torch, A, ctx, stream, args):

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ANIMA_HIP_ABI_VERSION 3
+#define ANIMA_HIP_ABI_VERSION 4
 
 /* Status codes.  The reference throws AnimapkError.validation(String)
  * (Runtime/Animapk/MappedFile.swift:14) for every failure; the codes split that
@@ -46,7 +46,9 @@ typedef enum anima_status {
   ANIMA_E_MISALIGNED = 4,      /* offsets / strides violate the alignment contract */
   ANIMA_E_UNSUPPORTED = 5,     /* valid request this backend refuses (loudly) */
   ANIMA_E_DEVICE = 6,          /* HIP runtime error */
-  ANIMA_E_INVALID_ARGUMENT = 7 /* null handle / unknown enum value */
+  ANIMA_E_INVALID_ARGUMENT = 7, /* null handle / unknown enum value */
+  ANIMA_E_FORMAT = 8,          /* a .animapk header, JSON or layout violates ANMA v1 */
+  ANIMA_E_IO = 9               /* a file could not be opened or mapped */
 } anima_status;
 
 /* Thread-local message of the last failure on this thread ("" after success). */
@@ -543,6 +545,103 @@ anima_status anima_dit_final_create(anima_ctx* ctx, anima_dit_final** out);
 anima_status anima_dit_final_destroy(anima_dit_final* fin);
 anima_status anima_dit_final_encode(anima_dit_final* fin, const anima_dit_final_weights* w,
                                     const anima_dit_final_args* args);
+
+/* ------------------------------------------------------------------------- */
+/* .animapk (ANMA v1) packs: AnimapkFile (Runtime/Animapk/AnimapkFile.swift:15-185), */
+/* AnimapkHeader (AnimapkHeader.swift:5-69), the tensor_meta JSON          */
+/* (AnimapkTensor.swift:90-173) and the execution ranges of                */
+/* AnimapkRangeLocator.swift:38-261.  The file is mapped read-only on the  */
+/* host; every name and pointer the calls return stays valid until         */
+/* anima_pack_close.                                                       */
+/* ------------------------------------------------------------------------- */
+typedef struct anima_pack anima_pack;
+
+typedef struct anima_pack_info {
+  int32_t version;           /* 1 */
+  int32_t component;         /* header code: 1 dit, 2 te, 3 vae */
+  int64_t alignment;         /* 16384 */
+  int64_t tensor_count;
+  int64_t json_offset, json_size;
+  int64_t table_offset, table_bytes;
+  int64_t payload_offset;
+  int64_t file_size;
+  int32_t record_size;       /* 128 */
+  int32_t quant_group;       /* JSON quant.group, -1 when absent */
+  const char* quant_scheme;  /* JSON quant.scheme, NULL when absent */
+  const char* component_name;/* JSON component ("dit", "te", "vae") */
+} anima_pack_info;
+
+/* One tensor_meta entry.  Offsets: blob_* are absolute file offsets; data_*,
+ * scale_* and zero_* are relative to the blob (scale/zero -1 when absent). */
+typedef struct anima_pack_tensor {
+  const char* name;
+  int32_t storage;           /* ANIMA_STORAGE_* from storage_dtype ("w4" ... "fp32") */
+  int32_t rank;              /* <= 8 */
+  int64_t shape[8];
+  int64_t blob_offset, blob_size;
+  int64_t data_offset, data_size;
+  int64_t scale_offset, scale_size;
+  int64_t zero_offset, zero_size;
+  int64_t block_index;       /* -1 when absent */
+  uint32_t crc32;
+  int32_t has_crc32;
+  const char* logical_dtype;
+  const char* quantization_format;  /* NULL when absent */
+} anima_pack_tensor;
+
+/* A contiguous file range holding every blob of one execution unit (a DiT block,
+ * the final layer, the preparation tensors): AnimapkExecutionRange. */
+typedef struct anima_pack_range {
+  int64_t logical_index;
+  int64_t file_offset;       /* 16 KiB aligned */
+  int64_t length;
+  int64_t tensor_count;
+  const void* host;          /* the mapped bytes of [file_offset, file_offset + length) */
+} anima_pack_range;
+
+/* AnimapkFile.init: header, JSON, per-tensor and table cross-match validation
+ * (ANIMA_E_FORMAT with the reference's message on a violation, ANIMA_E_IO when
+ * the file cannot be opened or mapped). */
+anima_status anima_pack_open(const char* path, anima_pack** out);
+anima_status anima_pack_close(anima_pack* pack);
+anima_status anima_pack_get_info(const anima_pack* pack, anima_pack_info* out);
+/* Tensors in JSON order (index 0 .. tensor_count-1), or by full name
+ * (ANIMA_E_INVALID_ARGUMENT "missing tensor <name>" when absent). */
+anima_status anima_pack_tensor_at(const anima_pack* pack, int64_t index, anima_pack_tensor* out);
+anima_status anima_pack_find(const anima_pack* pack, const char* name, anima_pack_tensor* out);
+/* AnimapkFile.crc32MismatchCount: tensors whose data CRC-32 (zlib) differs from
+ * the JSON value (tensors without one count as matching). */
+anima_status anima_pack_crc32_mismatch_count(const anima_pack* pack, int64_t* out);
+/* AnimapkFile.bytes(in:): the mapped bytes of an absolute file range. */
+anima_status anima_pack_bytes(const anima_pack* pack, int64_t offset, int64_t length, const void** out);
+/* AnimapkRangeBuilder.executionRanges: for i < count the range of every tensor
+ * named "<prefix><i>." ..., in logical order; physical ranges must not overlap. */
+anima_status anima_pack_execution_ranges(const anima_pack* pack, const char* prefix, int64_t count,
+                                         anima_pack_range* out);
+
+/* Weight templates of one execution unit: every anima_qweight has packed /
+ * scale / zero = {NULL, range length} with *_offset relative to the range start
+ * (DiTQuantizedWeightFactory.makeMatrix, LinearExecutor.swift:467-518), and every
+ * norm buffer {(void*)offset, bytes}.  anima_dit_forward_encode_streamed takes
+ * block templates as they are; the *_rebase calls turn a template into device
+ * weights once the range has been copied to `base`. */
+/* DiT block i (BlockWeights, DiTBlockExecutor.swift:1864-1917: 20 tensors). */
+anima_status anima_pack_dit_block(const anima_pack* pack, int64_t block, anima_dit_block_weights* tmpl,
+                                  anima_pack_range* range);
+/* DiTPreparationLocator + DiTPreparationWeights (DiTPreparationExecutor.swift:297-323). */
+anima_status anima_pack_dit_prepare(const anima_pack* pack, int64_t dim, anima_dit_prepare_weights* tmpl,
+                                    anima_pack_range* range);
+/* DiTFinalLayerLocator + FinalWeights (DiTFinalLayerExecutor.swift:394-420). */
+anima_status anima_pack_dit_final(const anima_pack* pack, int64_t dim, anima_dit_final_weights* tmpl,
+                                  anima_pack_range* range);
+/* Template -> weights in a device copy of the range at `base` (range_bytes long);
+ * an offset outside the range fails with ANIMA_E_OUT_OF_BOUNDS. */
+anima_status anima_dit_block_weights_rebase(const anima_dit_block_weights* tmpl, void* base, int64_t range_bytes,
+                                            anima_dit_block_weights* out);
+anima_status anima_dit_prepare_weights_rebase(const anima_dit_prepare_weights* tmpl, void* base,
+                                              int64_t range_bytes, anima_dit_prepare_weights* out);
+anima_status anima_dit_final_weights_rebase(const anima_dit_final_weights* tmpl, void* base, int64_t range_bytes,
+                                            anima_dit_final_weights* out);
 
 /* ------------------------------------------------------------------------- */
 /* Qwen encoder layer: QwenLayerExecutor.execute (QwenEncoderMetal.swift:232-304)  */

@@ -123,6 +123,25 @@ int main(void) {
   FIELD(anima_dit_final_args, residual); FIELD(anima_dit_final_args, emb); FIELD(anima_dit_final_args, adaln_lora);
   FIELD(anima_dit_final_args, velocity); FIELD(anima_dit_final_args, height); FIELD(anima_dit_final_args, width);
   FIELD(anima_dit_final_args, dim); FIELD(anima_dit_final_args, eps);
+
+  SIZE(anima_pack_info);
+  FIELD(anima_pack_info, version); FIELD(anima_pack_info, component); FIELD(anima_pack_info, alignment);
+  FIELD(anima_pack_info, tensor_count); FIELD(anima_pack_info, json_offset); FIELD(anima_pack_info, json_size);
+  FIELD(anima_pack_info, table_offset); FIELD(anima_pack_info, table_bytes); FIELD(anima_pack_info, payload_offset);
+  FIELD(anima_pack_info, file_size); FIELD(anima_pack_info, record_size); FIELD(anima_pack_info, quant_group);
+  FIELD(anima_pack_info, quant_scheme); FIELD(anima_pack_info, component_name);
+
+  SIZE(anima_pack_tensor);
+  FIELD(anima_pack_tensor, name); FIELD(anima_pack_tensor, storage); FIELD(anima_pack_tensor, rank);
+  FIELD(anima_pack_tensor, shape); FIELD(anima_pack_tensor, blob_offset); FIELD(anima_pack_tensor, blob_size);
+  FIELD(anima_pack_tensor, data_offset); FIELD(anima_pack_tensor, data_size); FIELD(anima_pack_tensor, scale_offset);
+  FIELD(anima_pack_tensor, scale_size); FIELD(anima_pack_tensor, zero_offset); FIELD(anima_pack_tensor, zero_size);
+  FIELD(anima_pack_tensor, block_index); FIELD(anima_pack_tensor, crc32); FIELD(anima_pack_tensor, has_crc32);
+  FIELD(anima_pack_tensor, logical_dtype); FIELD(anima_pack_tensor, quantization_format);
+
+  SIZE(anima_pack_range);
+  FIELD(anima_pack_range, logical_index); FIELD(anima_pack_range, file_offset); FIELD(anima_pack_range, length);
+  FIELD(anima_pack_range, tensor_count); FIELD(anima_pack_range, host);
   printf("\n},\n\"rejections\": [\n");
 
   /* Requests that must fail validation, through the C entry points. */
@@ -189,6 +208,8 @@ int main(void) {
   pa.sigma = 1.0f / 0.0f;
   rejection("prepare_sigma", anima_dit_prepare_encode(prep, &pw, &pa));
   anima_dit_prepare_destroy(prep);
+  anima_pack* pack = NULL;
+  rejection("pack_missing", anima_pack_open("/nonexistent/dir/x.animapk", &pack));
 
   anima_linear_destroy(lin);
   anima_attention_destroy(attn);

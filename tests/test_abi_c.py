@@ -34,6 +34,9 @@ STRUCTS = {
     "anima_dit_prepare_args": _abi.DitPrepareArgs,
     "anima_dit_final_weights": _abi.DitFinalWeights,
     "anima_dit_final_args": _abi.DitFinalArgs,
+    "anima_pack_info": _abi.PackInfo,
+    "anima_pack_tensor": _abi.PackTensor,
+    "anima_pack_range": _abi.PackRange,
 }
 
 
@@ -51,7 +54,7 @@ def report(tmp_path_factory):
 
 
 def test_abi_version(report):
-    assert report["abi_version"] == _abi.load().anima_abi_version() == 3
+    assert report["abi_version"] == _abi.load().anima_abi_version() == 4
 
 
 def test_every_struct_field_matches_ctypes(report):
@@ -94,6 +97,7 @@ def test_rejections_through_the_c_entry_points(report):
         "euler_sigma": (_abi.E_INVALID_ARGUMENT, "invalid Euler sampler buffer or sigma"),
         "patchify_odd": (_abi.E_INVALID_SHAPE, "even height and width"),
         "prepare_sigma": (_abi.E_INVALID_ARGUMENT, "invalid DiT preparation input"),
+        "pack_missing": (_abi.E_IO, "cannot open /nonexistent/dir/x.animapk"),
     }
     for name, (status, fragment) in want.items():
         st, msg = got[name]
