@@ -509,8 +509,13 @@ constexpr int F2_MIN_SPLIT_KEYS = 256;
 constexpr int F2_MAX_SPLITS = 8;
 
 int flash_kv_splits(const FlashParams& p, int D, int batch, int flash_rows) {
-  if (flash_rows != 0 || p.causal || p.key_lengths_dev || p.use_host_lengths || (D != 128 && D != 64)) return 1;
-  const int64_t t256 = (int64_t)((p.Sq + FLASH_V2_ROWS - 1) / FLASH_V2_ROWS) * p.H * batch;
+  if (p.causal || p.key_lengths_dev || p.use_host_lengths) return 1;
+  if (D != 128 && D != 64 && D != 384) return 1;
+  if (D != 384 && flash_rows != 0) return 1;
+  // Query tiles of the kernel that will run: 256 rows (head_dim 64 / 128) or the wide
+  // kernel's 128 rows (head_dim 384, which has no other flash kernel).
+  const int rows = D == 384 ? FLASH_WIDE_ROWS : FLASH_V2_ROWS;
+  const int64_t t256 = (int64_t)((p.Sq + rows - 1) / rows) * p.H * batch;
   if (t256 >= F2_MIN_BLOCKS || t256 <= 0) return 1;
   if (64 * std::max(p.k_tok, p.v_tok) * (int64_t)sizeof(half_t) >= ((int64_t)1 << 31)) return 1;
   int splits = (int)((F2_MIN_BLOCKS + t256 - 1) / t256);
@@ -524,8 +529,34 @@ int64_t flash_split_bytes(const FlashParams& p, int D, int batch, int splits) {
   return checked_product({rows, (int64_t)D + 2, 4}, "attention");
 }
 
+// Head dim 384: the wide kernel, 128 query rows per workgroup, keys split when the query
+// tiles alone cannot cover the chip.
+static void launch_flash_wide_plan(FlashParams p, int D, int batch, hipStream_t stream) {
+  if (32 * std::max(p.k_tok, p.v_tok) * (int64_t)sizeof(half_t) >= ((int64_t)1 << 31))
+    fail(ANIMA_E_INVALID_SHAPE, "wide flash attention requires 32 key rows to span < 2 GiB");
+  p.q_tiles = (p.Sq + FLASH_WIDE_ROWS - 1) / FLASH_WIDE_ROWS;
+  const int64_t tiles = (int64_t)p.q_tiles * p.H * batch;
+  if (tiles <= 0) return;
+  if (p.kv_splits > 1) {
+    if (p.kv_splits != flash_kv_splits(p, D, batch, 0) || !p.part_o || !p.part_ml)
+      fail(ANIMA_E_INVALID_ARGUMENT, "flash key splits do not match the shape");
+    p.nbatch = batch;
+    p.kv_chunk = ((p.Sk + p.kv_splits - 1) / p.kv_splits + 63) / 64 * 64;
+  } else {
+    p.kv_splits = 0;
+  }
+  const int64_t blocks = tiles * (p.kv_splits > 1 ? p.kv_splits : 1);
+  if (blocks > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "attention grid too large");
+  launch_flash_wide(p, D, dim3((unsigned)blocks), stream);
+  if (p.kv_splits > 1) launch_flash_combine(p, D, batch, stream);
+}
+
 void launch_flash(FlashParams p, int D, int batch, int flash_rows, hipStream_t stream) {
-  if (D != 128 && D != 64) fail(ANIMA_E_UNSUPPORTED, "flash attention requires head_dim 64 or 128");
+  if (D == 384) {
+    launch_flash_wide_plan(p, D, batch, stream);
+    return;
+  }
+  if (D != 128 && D != 64) fail(ANIMA_E_UNSUPPORTED, "flash attention requires head_dim 64, 128 or 384");
   const int64_t t256 = (int64_t)((p.Sq + FLASH_V2_ROWS - 1) / FLASH_V2_ROWS) * p.H * batch;
   // The 256-row kernel addresses one 64-key tile with 32-bit byte offsets.
   const bool v2_fits = 64 * std::max(p.k_tok, p.v_tok) * (int64_t)sizeof(half_t) < ((int64_t)1 << 31);

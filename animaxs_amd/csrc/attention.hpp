@@ -56,6 +56,10 @@ int64_t flash_split_bytes(const FlashParams& p, int D, int batch, int splits);
 
 // 256-row flash variant (attention_v2.hip); p.q_tiles counts 256-row tiles.
 constexpr int FLASH_V2_ROWS = 256;
+// Wide-head (head_dim 384) flash kernel (attention_wide.hip): 128 query rows per
+// workgroup, p.q_tiles counts 128-row tiles.
+constexpr int FLASH_WIDE_ROWS = 128;
+void launch_flash_wide(const FlashParams& p, int D, dim3 grid, hipStream_t stream);
 void launch_flash_v2(const FlashParams& p, int D, dim3 grid, hipStream_t stream);
 void launch_flash_combine(const FlashParams& p, int D, int batch, hipStream_t stream);
 void launch_generic(const FlashParams& p, int D, int batch, hipStream_t stream);

@@ -203,7 +203,7 @@ void AttentionExecutor::encode_impl(const anima_attention_args& a, bool no_alloc
     k_tok = D; k_head = Sk * D; k_batch = kvh * Sk * D;
   }
 
-  const bool flash_shape = (D == 64 || D == 128);
+  const bool flash_shape = (D == 64 || D == 128 || D == 384);
   const bool rows_aligned = aligned16(qp) && aligned16(kp) && aligned16(vp) && aligned16(op) && (q_tok % 8 == 0) &&
                             (k_tok % 8 == 0) && (q_head % 8 == 0) && (k_head % 8 == 0) && (q_batch % 8 == 0) &&
                             (k_batch % 8 == 0);
@@ -212,7 +212,7 @@ void AttentionExecutor::encode_impl(const anima_attention_args& a, bool no_alloc
     case ANIMA_ATTENTION_BACKEND_FLASH:
       if (!(flash_shape && rows_aligned))
         fail(ANIMA_E_UNSUPPORTED,
-             "flash attention requires head_dim 64 or 128 and 16-byte-aligned rows, offsets and strides");
+             "flash attention requires head_dim 64, 128 or 384 and 16-byte-aligned rows, offsets and strides");
       use_flash = true;
       break;
     case ANIMA_ATTENTION_BACKEND_GENERIC:
@@ -221,7 +221,8 @@ void AttentionExecutor::encode_impl(const anima_attention_args& a, bool no_alloc
     default:
       use_flash = flash_shape && rows_aligned;
   }
-  const bool q_fusable = use_flash && (!q_norm || aligned16(q_norm)) && (!rope_q || aligned16(rope_q));
+  // The wide (head_dim 384) kernel reads Q as it is; the prologue kernel normalises it.
+  const bool q_fusable = use_flash && D != 384 && (!q_norm || aligned16(q_norm)) && (!rope_q || aligned16(rope_q));
   const bool need_q_pro = (q_norm || rope_q) && !q_fusable;
   const bool need_k_pro = (k_norm || rope_k);
 

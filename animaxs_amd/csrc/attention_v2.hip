@@ -39,7 +39,7 @@
 //     wave gets at 2 waves/SIMD.
 #include <type_traits>
 
-#include "attention.hpp"
+#include "flash_common.hpp"
 
 namespace anima {
 
@@ -50,67 +50,6 @@ constexpr int F2_STAGES = 4;
 constexpr float F2_LAZY_LIMIT = 32768.f;   // largest tile row-sum share the fast path accepts
 constexpr int F2_READ_AHEAD = 4;    // MFMA operand fragments read from LDS ahead of their MFMA
 static_assert(FLASH_V2_ROWS == 32 * F2_WAVES, "one 32-row block per wave");
-
-typedef short short4v __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float xlane32_max(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xlane32_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// Q fragment of one 32-row block (B operand of S^T): lane holds
-// Q[row][16s + 8h + 0..7] with the per-head RMSNorm and split-half RoPE fused.
-template <int D>
-__device__ __forceinline__ void load_q_fragment(const FlashParams& p, int b, int head, int qi, int hh,
-                                                half8v (&qf)[D / 16]) {
-  constexpr int QS = D / 16;
-  const int qrow = qi < p.Sq ? qi : p.Sq - 1;
-  const half_t* qp = p.q + (int64_t)b * p.q_batch + (int64_t)head * p.q_head + (int64_t)qrow * p.q_tok;
-#pragma unroll
-  for (int s = 0; s < QS; ++s) qf[s] = *reinterpret_cast<const half8v*>(qp + 16 * s + 8 * hh);
-  if (p.q_norm_w || p.rope) {
-    float x[QS][8];
-#pragma unroll
-    for (int s = 0; s < QS; ++s)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x[s][i] = (float)qf[s][i];
-    if (p.q_norm_w) {
-      float ss = 0.f;
-#pragma unroll
-      for (int s = 0; s < QS; ++s)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) ss = fmaf(x[s][i], x[s][i], ss);
-      ss = xlane32_sum(ss);
-      const float inv = rsqrtf(ss / (float)D + p.eps);
-#pragma unroll
-      for (int s = 0; s < QS; ++s) {
-        const half8v w = *reinterpret_cast<const half8v*>(p.q_norm_w + 16 * s + 8 * hh);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] * inv * (float)w[i];
-      }
-    }
-    if (p.rope) {
-      const float* rr = p.rope + (int64_t)qrow * (D / 2) * 4;
-#pragma unroll
-      for (int s = 0; s < QS / 2; ++s)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const floatx4 blk = *reinterpret_cast<const floatx4*>(rr + (16 * s + 8 * hh + i) * 4);
-          const float a = x[s][i], bb = x[s + QS / 2][i];
-          x[s][i] = blk[0] * a + blk[1] * bb;
-          x[s + QS / 2][i] = blk[2] * a + blk[0] * bb;
-        }
-    }
-#pragma unroll
-    for (int s = 0; s < QS; ++s)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qf[s][i] = f32_to_f16(x[s][i]);
-  }
-}
 
 template <int D>
 __global__ __launch_bounds__(F2_NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -486,7 +425,9 @@ void flash_attention_v2_kernel(FlashParams p) {
 template <int D>
 __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p, int64_t rows) {
   constexpr int TPR = D / 8;
-  const int64_t row = (int64_t)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
+  constexpr int RPB = 256 / TPR;   // rows per block (threads past RPB * TPR idle)
+  if ((int)threadIdx.x >= RPB * TPR) return;
+  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
   const int t = threadIdx.x % TPR;
   if (row >= rows) return;
   const int qi = (int)(row % p.Sq);
@@ -523,6 +464,8 @@ void launch_flash_combine(const FlashParams& p, int D, int batch, hipStream_t st
   if (blocks > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "attention combine grid too large");
   if (D == 128)
     hipLaunchKernelGGL(flash_combine_kernel<128>, dim3((unsigned)blocks), dim3(256), 0, stream, p, rows);
+  else if (D == 384)
+    hipLaunchKernelGGL(flash_combine_kernel<384>, dim3((unsigned)blocks), dim3(256), 0, stream, p, rows);
   else
     hipLaunchKernelGGL(flash_combine_kernel<64>, dim3((unsigned)blocks), dim3(256), 0, stream, p, rows);
   ANIMA_HIP(hipGetLastError());

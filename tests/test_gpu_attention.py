@@ -296,3 +296,44 @@ def test_llm_adapter_attention_head_dim_64_separate_key_rope(ctx, Tq, Tk):
              out_shape=(1, Tq, H, D), prologue=pro)
     ref = oatt.sdpa(oatt.qk_prologue(q, qw, 1e-6, rq).half().float(), oatt.qk_prologue(k, kw, 1e-6, rk).half().float(), v)
     assert_attention_close(o, ref, label=f"adapter D64 Tq{Tq} Tk{Tk}")
+
+
+# ---------------------------------------------------------------------------
+# Head dim 384: the VAE decoder's mid-block attention (VAEDecoder.swift:396-404): one head,
+# Q/K/V contiguous [positions, 384] blocks, 4096 positions at the 64x64 latent.
+# ---------------------------------------------------------------------------
+def test_vae_attention_head_dim_384_matches_oracle(ctx):
+    S, D = 4096, 384
+    g = torch.Generator().manual_seed(384)
+    q = torch.randn(S, D, generator=g).half()
+    k = torch.randn(S, D, generator=g).half()
+    v = torch.randn(S, D, generator=g).half()
+    print("VAE attention D384 S4096", flush=True)
+    o = _run(ctx, dev(q), dev(k), dev(v), layout="headMajor", heads=1, Sq=S, Sk=S, D=D, out_shape=(S, D))
+    ref = oatt.sdpa(q[None, :, None, :], k[None, :, None, :], v[None, :, None, :])[0, :, 0, :]
+    assert_attention_close(o, ref, label="VAE D384 S4096 (wide flash, 8 key splits)")
+    # the generic kernel, which the reference's shape used before, agrees to the same bar
+    og = _run(ctx, dev(q), dev(k), dev(v), layout="headMajor", heads=1, Sq=S, Sk=S, D=D, out_shape=(S, D),
+              backend="generic")
+    assert_attention_close(og, ref, label="VAE D384 S4096 generic")
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk,causal,lengths", [(1, 1, 300, 777, False, None), (2, 2, 129, 64, False, None),
+                                                      (1, 3, 260, 260, True, None), (2, 1, 200, 450, False, [37, 450]),
+                                                      (1, 1, 1, 33, False, None), (1, 2, 5000, 40, False, None)])
+def test_wide_flash_head_dim_384_ragged(ctx, B, H, Sq, Sk, causal, lengths):
+    """Ragged tiles, batch and heads, causal rows, per-sequence key lengths (no key splits) and the
+    split path (300 x 777: 3 splits); large logits so the lazy running max must rescale."""
+    D = 384
+    g = torch.Generator().manual_seed(B * 100000 + H * 10000 + Sq + Sk)
+    q = (torch.randn(B, Sq, H, D, generator=g) * 4.0).half()    # logits ~N(0, 16^2): the running max
+    k = (torch.randn(B, Sk, H, D, generator=g) * 4.0).half()    # grows past the lazy bound
+    v = torch.randn(B, Sk, H, D, generator=g).half()
+    kw = {}
+    if lengths is not None:
+        kw["key_lengths"] = np.array(lengths, np.int32)
+    print(f"WIDE D384 B{B} H{H} Sq{Sq} Sk{Sk} causal={causal} lengths={lengths}", flush=True)
+    o = _run(ctx, dev(q), dev(k), dev(v), layout=("tokenMajor", H * D), heads=H, Sq=Sq, Sk=Sk, D=D,
+             out_shape=(B, Sq, H, D), batch=B, causal=causal, backend="flash", **kw)
+    ref = oatt.sdpa(q, k, v, causal=causal, key_lengths=lengths)
+    assert_attention_close(o, ref, label=f"wide D384 B{B} H{H} Sq{Sq} Sk{Sk} causal={causal}")
