@@ -7,8 +7,8 @@ fraction of the fp16 dense MFMA peak — plus ms per full DiT block (hidden 2048
 S=4096, 512-token context, all ten linears W4 group-64).
 
 One "step" = one attention call on fresh synthetic inputs already resident in
-HBM (4 rotating input sets, 256 MiB, so the 256 MB Infinity Cache does not hold
-a step's inputs).  Prints ONE JSON line.  The CPU baseline is the repository's
+HBM (8 rotating input sets, 512 MiB, twice the 256 MB Infinity Cache, so it does not
+hold a step's inputs).  Prints ONE JSON line.  The CPU baseline is the repository's
 torch-CPU fp32 oracle timed on the same workload on this host's cores.
 """
 
@@ -34,10 +34,13 @@ SIDE = 64
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--steps", type=int, default=60)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--block-steps", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-table", action="store_true",
+                    help="also time the oracle on all five workloads (C1-C5, incl. ms per DiT block) at all threads "
+                         "and at 4 threads, median of 5 after 1 warm-up (several minutes of CPU work)")
     ap.add_argument("--no-block", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the per-workload table")
     ap.add_argument("--profile-block", action="store_true",
@@ -47,7 +50,63 @@ def parse():
     ap.add_argument("--profile-kernel", action="store_true",
                     help="only launch the dominant flash kernel (--warmup + --steps times) and a 256 MiB "
                          "calibration copy, for rocprofv3 counter passes; prints no JSON")
+    ap.add_argument("--profile-gemm", metavar="M,N,K",
+                    help="only launch the W4 GEMM of this shape over rotating weight sets (> 600 MB), settle + "
+                         "--warmup + --steps times, then the calibration copies; for rocprofv3 counter passes")
+    ap.add_argument("--profile-vae", action="store_true",
+                    help="only the VAE mid-block attention (1 head, head_dim 384, 4096 positions), settle + "
+                         "--warmup + --steps calls; for a rocprofv3 kernel trace")
+    ap.add_argument("--counter-summary", metavar="CSV",
+                    help="no GPU: per-dispatch means of a rocprofv3 --pmc counter_collection.csv, per kernel "
+                         "(last --trace-last dispatches of each) and exit")
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="no GPU: summarise a rocprofv3 kernel_trace.csv (per kernel: dispatches, mean/median/p10/p90 "
+                         "of the last --trace-last dispatches) and exit")
+    ap.add_argument("--trace-last", type=int, default=0, help="with --trace-summary: only the last N dispatches of "
+                    "each kernel (the timed ones; 0 = all)")
     return ap.parse_args()
+
+
+def counter_summary(path, last):
+    """Per kernel: mean / min / max over its last ``last`` dispatches of every counter in a
+    rocprofv3 --pmc counter_collection.csv (one row per dispatch and counter, the value
+    already summed over the counter's instances)."""
+    import csv
+    import numpy as np
+    per = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            k = per.setdefault(r["Kernel_Name"], {})
+            k.setdefault(r["Counter_Name"], []).append((int(r["Dispatch_Id"]), float(r["Counter_Value"])))
+    print("| kernel | counter | dispatches | summarised | mean per dispatch | min | max |")
+    print("|---|---|---|---|---|---|---|")
+    for name, counters in per.items():
+        for cname, v in sorted(counters.items()):
+            v.sort()
+            d = np.array([x[1] for x in (v[-last:] if last else v)])
+            print(f"| `{name[:70]}` | {cname} | {len(v)} | {len(d)} | {d.mean():.1f} | {d.min():.1f} | {d.max():.1f} |")
+
+
+def trace_summary(path, last):
+    """Per-kernel durations from a rocprofv3 --kernel-trace CSV (Kernel_Name,
+    Start_Timestamp, End_Timestamp in ns)."""
+    import csv
+    import numpy as np
+    per = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            per.setdefault(r["Kernel_Name"], []).append((int(r["Start_Timestamp"]),
+                                                         int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    rows = []
+    for name, v in per.items():
+        v.sort()
+        d = np.array([x[1] for x in (v[-last:] if last else v)], dtype=np.float64) / 1e3
+        rows.append((d.sum(), name, len(v), len(d), d.mean(), np.median(d), np.percentile(d, 10), np.percentile(d, 90)))
+    rows.sort(reverse=True)
+    print("| kernel | dispatches | summarised | mean us | median us | p10 us | p90 us |")
+    print("|---|---|---|---|---|---|---|")
+    for _, name, n, k, mean, med, p10, p90 in rows:
+        print(f"| `{name[:90]}` | {n} | {k} | {mean:.2f} | {med:.2f} | {p10:.2f} | {p90:.2f} |")
 
 
 def attn_flops(Sq, Sk, heads=H, batch=B, d=D):
@@ -103,6 +162,25 @@ def time_region(torch, stream, fn, steps, warmup, settle=True):
     return start.elapsed_time(end) / steps  # ms per step
 
 
+def time_calls(torch, stream, fn, calls, warmup, settle=True):
+    """Two timed passes of ``calls`` back-to-back calls after one settle + warm-up:
+    one event pair around the whole pass (the mean, nothing between the calls), then
+    an event after every call (per-call durations: median, p10, p90).  Returns a dict
+    in ms."""
+    import numpy as np
+    mean = time_region(torch, stream, fn, calls, warmup, settle)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(calls + 1)]
+    evs[0].record(stream)
+    for i in range(calls):
+        fn(i)
+        evs[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(calls)])
+    return {"mean_ms": round(mean, 5), "median_ms": round(float(np.median(per)), 5),
+            "p10_ms": round(float(np.percentile(per, 10)), 5), "p90_ms": round(float(np.percentile(per, 90)), 5),
+            "calls": calls}
+
+
 def time_graph(torch, ctx, fn, calls, reps=5):
     """ms per call of ``calls`` back-to-back encodes captured once into a HIP graph and
     replayed ``reps`` times (events on the replay stream)."""
@@ -136,6 +214,12 @@ def time_graph(torch, ctx, fn, calls, reps=5):
 
 def main():
     args = parse()
+    if args.trace_summary:
+        trace_summary(args.trace_summary, args.trace_last)
+        return
+    if args.counter_summary:
+        counter_summary(args.counter_summary, args.trace_last)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the attention/W4 hot path is "
               "benchmarked per GPU and multi-GPU sharding is a design note, not a measured mode.", file=sys.stderr)
@@ -157,6 +241,13 @@ def main():
         ms = time_block(torch, A, ctx, stream, args)
         print(f"# profile-block: DiT block S4096 {ms:.3f} ms", file=sys.stderr)
         return
+    if args.profile_gemm:
+        profile_gemm(torch, A, ctx, stream, args, *(int(x) for x in args.profile_gemm.split(",")))
+        return
+    if args.profile_vae:
+        ms = time_region(torch, stream, vae_attention_call(torch, A, ctx), args.steps, args.warmup)
+        print(f"# profile-vae: {ms * 1e3:.2f} us per call (HIP events, {args.steps} timed calls)", file=sys.stderr)
+        return
     if args.profile_step:
         st_ms, first_ms, fwd_ms, finite = time_sampler_step(torch, A, ctx, stream, args)
         print(f"# profile-step: sampler step 1024px {st_ms:.3f} ms (first {first_ms:.3f} ms, 28-block forward "
@@ -164,7 +255,7 @@ def main():
         return
 
     # ---------------- headline: S=4096 self-attention with fused norm+RoPE ----------------
-    sets, qw, kw = gen_attention_inputs(torch, 4)
+    sets, qw, kw = gen_attention_inputs(torch, 8)
     rope = torch.from_numpy(A.DitRoPE.generate(1, SIDE, SIDE)).cuda()
     pro = A.QKPrologue(qw, kw, 1e-6, rope, S, True, True)
     ex = A.AttentionExecutor(ctx, layout=("tokenMajor", H * D), backend="flash")
@@ -175,9 +266,10 @@ def main():
 
     flops = attn_flops(S, S)
     if not args.profile_kernel:
-        ms = time_region(torch, stream, step, args.steps, args.warmup)
+        step_t = time_calls(torch, stream, step, args.steps, args.warmup)
+        ms = step_t["mean_ms"]
         tflops = flops / (ms * 1e-3) / 1e12
-        print(f"# self-attn S4096 (norm+rope, incl. K prologue): {ms:.4f} ms  {tflops:.1f} TFLOP/s", file=sys.stderr,
+        print(f"# self-attn S4096 (norm+rope, incl. K prologue): {step_t}  {tflops:.1f} TFLOP/s", file=sys.stderr,
               flush=True)
 
     # Dominant kernel alone: the flash kernel with Q norm+RoPE fused and K given already
@@ -204,24 +296,21 @@ def main():
         kms = time_region(torch, stream, kstep, args.steps, args.warmup)
         print(f"# profile-kernel: flash kernel alone {kms:.4f} ms (HIP events, {args.steps} timed launches)",
               file=sys.stderr, flush=True)
-        # calibration: a plain copy of known size (256 MiB read + 256 MiB written)
-        src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
+        calibration_copies(torch)
         print(f"# profile-kernel: settle launches, then {args.warmup} warmup + {args.steps} timed flash launches, "
               "3 x 256 MiB copies", file=sys.stderr)
         return
 
-    kms = time_region(torch, stream, kstep, args.steps, args.warmup)
+    kern_t = time_calls(torch, stream, kstep, args.steps, args.warmup)
+    kms = kern_t["mean_ms"]
     k_tflops = flops / (kms * 1e-3) / 1e12
-    print(f"# flash kernel alone: {kms:.4f} ms  {k_tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    print(f"# flash kernel alone: {kern_t}  {k_tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
 
     roofline = {
         "bound": "mfma", "kernel": "flash_attention_v2_kernel<128>", "achieved": round(k_tflops, 2),
         "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(k_tflops / FP16_PEAK_TFLOPS, 4),
         "traffic": load_traffic(), "flops_per_launch": flops, "avg_launch_ms": round(kms, 5),
+        "launch_timing": kern_t,
     }
 
     extra = {}
@@ -247,10 +336,13 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline()
+        if args.cpu_table:
+            cpu["table"] = cpu_table()
 
     line = {
         "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "step_timing": step_t,
         "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
         "config": {"workload": "dit_self_attention_1024px", "batch": B, "heads": H, "head_dim": D, "seq_len": S,
                    "qk_rmsnorm": True, "rope": "dit3d 1x64x64", "layout": "token-major stride 2048",
@@ -263,6 +355,56 @@ def main():
         "device": dev_name,
     }
     print(json.dumps(line), flush=True)
+
+
+def vae_attention_call(torch, A, ctx, sets=4):
+    """VAE decoder mid-block attention: one head, head_dim 384, 4096 positions (64x64
+    latent), Q/K/V contiguous [4096, 384] fp16 (VAEDecoder.swift:396-404); rotating sets."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1009)
+    vsets = [tuple(torch.randn(4096, 384, device="cuda", generator=g).half() for _ in range(3)) for _ in range(sets)]
+    vo = torch.empty(4096, 384, device="cuda", dtype=torch.float16)
+    exv = A.AttentionExecutor(ctx, layout="headMajor", backend="flash")
+
+    def call(i):
+        q, k, v = vsets[i % sets]
+        exv.encode(query=q, key=k, value=v, output=vo, heads=1, query_count=4096, key_count=4096, head_dim=384)
+    return call
+
+
+def calibration_copies(torch):
+    """A plain device copy of known size (256 MiB read + 256 MiB written), three times:
+    the reference point for the memory-traffic counters."""
+    src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def gemm_weight_sets(torch, A, N, K, min_bytes=600 << 20):
+    """Rotating W4 weight sets (random codes, group-64 scales, zero = -8 * scale) whose
+    total exceeds the 256 MB Infinity Cache."""
+    wbytes = N * K // 2
+    nsets = max(1, min(512, -(-min_bytes // wbytes)))
+    ws = []
+    for _ in range(nsets):
+        p = torch.randint(0, 256, (N, K // 2), device="cuda", dtype=torch.uint8)
+        sc = (0.005 + 0.015 * torch.rand(N, K // 64, device="cuda")).half()
+        z = (-8 * sc.float()).half()
+        ws.append((A.QuantizedLinearWeightBuffers(0, p, sc, z, N, K, K // 2), p, sc, z))
+    return ws
+
+
+def profile_gemm(torch, A, ctx, stream, args, M, N, K):
+    lin = A.LinearExecutor(ctx)
+    ws = gemm_weight_sets(torch, A, N, K)
+    x = torch.randn(M, K, device="cuda").half()
+    y = torch.empty(M, N, device="cuda", dtype=torch.float16)
+    ms = time_region(torch, stream, lambda i: lin.encode(x, ws[i % len(ws)][0], y, M), args.steps, args.warmup)
+    print(f"# profile-gemm M{M} N{N} K{K}: {ms * 1e3:.2f} us per launch (HIP events, {args.steps} timed launches "
+          f"over {len(ws)} weight sets)", file=sys.stderr, flush=True)
+    calibration_copies(torch)
 
 
 def load_traffic():
@@ -287,11 +429,12 @@ def other_workloads(torch, A, ctx, stream, args):
     q, k, v = (torch.randn(1, 1024, H, D, device="cuda", generator=g).half() for _ in range(3))
     o = torch.empty_like(q)
     ex = A.AttentionExecutor(ctx, layout=("tokenMajor", H * D), backend="flash")
-    ms = time_region(torch, stream, lambda i: ex.encode(query=q, key=k, value=v, output=o, heads=H, query_count=1024,
-                                                        key_count=1024, head_dim=D), args.steps, args.warmup)
+    t = time_calls(torch, stream, lambda i: ex.encode(query=q, key=k, value=v, output=o, heads=H, query_count=1024,
+                                                      key_count=1024, head_dim=D), args.steps, args.warmup)
+    ms = t["mean_ms"]
     f = attn_flops(1024, 1024)
     res["self_attention_s1024"] = {"ms": round(ms, 5), "tflops": round(f / ms / 1e9, 2),
-                                   "mfma_frac": round(f / ms / 1e9 / FP16_PEAK_TFLOPS, 4)}
+                                   "mfma_frac": round(f / ms / 1e9 / FP16_PEAK_TFLOPS, 4), "timing": t}
     # workload 3: cross attention B4, 4096 queries, 512 keys, masked, q/k RMSNorm
     g.manual_seed(1003)
     sets = []
@@ -310,14 +453,15 @@ def other_workloads(torch, A, ctx, stream, args):
         ex3.encode(query=q, key=k, value=v, output=o, heads=H, query_count=4096, key_count=512, head_dim=D, batch=4,
                    key_lengths=lengths, prologue=pro)
 
-    ms = time_region(torch, stream, s3, args.steps, args.warmup)
+    t = time_calls(torch, stream, s3, args.steps, args.warmup)
+    ms = t["mean_ms"]
     L = [int(x) for x in lengths]
     f = sum(4.0 * H * 4096 * l * D for l in L)
     byts = 2.0 * (4 * 4096 * H * D * 2) + sum(2.0 * l * H * D * 2 for l in L)
     res["cross_attention_b4_masked"] = {"ms": round(ms, 5), "tflops": round(f / ms / 1e9, 2),
                                         "gbs": round(byts / ms / 1e6, 1), "key_lengths": L,
                                         "hbm_frac": round(byts / ms / 1e6 / HBM_PEAK_GBS, 4),
-                                        "mfma_frac": round(f / ms / 1e9 / FP16_PEAK_TFLOPS, 4)}
+                                        "mfma_frac": round(f / ms / 1e9 / FP16_PEAK_TFLOPS, 4), "timing": t}
     # workload 4: Qwen causal GQA B4 S512, head-major, norm + rope 1e6, right padding
     g.manual_seed(1004)
     qh = torch.randn(4, 16, 512, D, device="cuda", generator=g).half()
@@ -328,15 +472,41 @@ def other_workloads(torch, A, ctx, stream, args):
     lens = torch.randint(8, 513, (4,), generator=torch.Generator().manual_seed(1004)).int().numpy()
     pro4 = A.QKPrologue(nw, nw, 1e-6, rq, 512, True, True)
     ex4 = A.AttentionExecutor(ctx, layout="headMajor", backend="flash")
-    ms = time_region(torch, stream, lambda i: ex4.encode(query=qh, key=kh, value=vh, output=oh, heads=16, query_count=512,
-                                                         key_count=512, head_dim=D, key_value_heads=8, causal=True,
-                                                         batch=4, key_lengths=lens, prologue=pro4),
-                     args.steps, args.warmup)
+    t = time_calls(torch, stream, lambda i: ex4.encode(query=qh, key=kh, value=vh, output=oh, heads=16, query_count=512,
+                                                       key_count=512, head_dim=D, key_value_heads=8, causal=True,
+                                                       batch=4, key_lengths=lens, prologue=pro4),
+                   args.steps, args.warmup)
+    ms = t["mean_ms"]
     pairs = sum(sum(min(i + 1, int(l)) for i in range(512)) for l in lens)
     f = 4.0 * D * 16 * pairs
     byts = (4 * 16 * 512 * D * 2) * 2 + (4 * 8 * 512 * D * 2) * 2
     res["qwen_causal_gqa_b4_s512_per_layer"] = {"ms": round(ms, 5), "tflops": round(f / ms / 1e9, 2),
-                                                "gbs": round(byts / ms / 1e6, 1), "key_lengths": [int(x) for x in lens]}
+                                                "gbs": round(byts / ms / 1e6, 1), "key_lengths": [int(x) for x in lens],
+                                                "timing": t}
+    # VAE decoder mid-block attention: one head, head_dim 384, 4096 positions (64x64 latent),
+    # Q/K/V contiguous [4096, 384] (VAEDecoder.swift:396-404); 4 rotating input sets
+    t = time_calls(torch, stream, vae_attention_call(torch, A, ctx), args.steps, args.warmup)
+    ms = t["mean_ms"]
+    f = attn_flops(4096, 4096, heads=1, d=384)
+    res["vae_attention_hd384_s4096"] = {"ms": round(ms, 5), "tflops": round(f / ms / 1e9, 2),
+                                        "mfma_frac": round(f / ms / 1e9 / FP16_PEAK_TFLOPS, 4), "timing": t}
+    # LLM-adapter attention: 16 heads x head_dim 64 over 512 target tokens, 512 context
+    # tokens, per-head RMSNorm on both sides, separate Q / K RoPE tables (theta 1e4)
+    # (LLMAdapterMetal.swift:360-405)
+    g.manual_seed(1010)
+    qa, ka, va = (torch.randn(1, 512, 16, 64, device="cuda", generator=g).half() for _ in range(3))
+    oa = torch.empty_like(qa)
+    wa = (0.8 + 0.4 * torch.rand(64, device="cuda", generator=g)).half()
+    ra = torch.from_numpy(A.qwen_rope(512, head_dim=64, theta=1.0e4)).cuda()
+    proa = A.QKPrologue(wa, wa, 1e-6, ra, 512, True, True, k_rope=ra, k_rope_tokens=512)
+    exa = A.AttentionExecutor(ctx, layout=("tokenMajor", 1024), backend="flash")
+    t = time_calls(torch, stream, lambda i: exa.encode(query=qa, key=ka, value=va, output=oa, heads=16, query_count=512,
+                                                       key_count=512, head_dim=64, prologue=proa),
+                   args.steps, args.warmup)
+    ms = t["mean_ms"]
+    f = attn_flops(512, 512, heads=16, d=64)
+    res["adapter_attention_hd64_512x512"] = {"ms": round(ms, 5), "tflops": round(f / ms / 1e9, 2),
+                                             "mfma_frac": round(f / ms / 1e9 / FP16_PEAK_TFLOPS, 4), "timing": t}
     # W4 GEMMs.  Small M is HBM-bound on the weight stream: each timed pass rotates
     # over weight sets totalling > 512 MB (so the 256 MB Infinity Cache cannot hold
     # them) and is replayed from a HIP graph, so the figure is the GPU's back-to-back
@@ -345,14 +515,8 @@ def other_workloads(torch, A, ctx, stream, args):
     shapes = [(M, N, K) for M in (1, 16, 64) for (N, K) in ((2048, 2048), (8192, 2048), (2048, 8192))]
     shapes += [(4096, 2048, 2048), (4096, 8192, 2048)]
     for (M, N, K) in shapes:
-        wbytes = N * K // 2
-        nsets = max(1, min(512, -(-(600 << 20) // wbytes)))
-        ws = []
-        for _ in range(nsets):
-            p = torch.randint(0, 256, (N, K // 2), device="cuda", dtype=torch.uint8)
-            sc = (0.005 + 0.015 * torch.rand(N, K // 64, device="cuda")).half()
-            z = (-8 * sc.float()).half()
-            ws.append((A.QuantizedLinearWeightBuffers(0, p, sc, z, N, K, K // 2), p, sc, z))
+        ws = gemm_weight_sets(torch, A, N, K)
+        nsets = len(ws)
         x = torch.randn(M, K, device="cuda").half()
         y = torch.empty(M, N, device="cuda", dtype=torch.float16)
         call = lambda i: lin.encode(x, ws[i % nsets][0], y, M)
@@ -529,46 +693,119 @@ def time_qwen_layer(torch, A, ctx, stream, args):
             "key_lengths": lengths}
 
 
-def cpu_baseline():
-    """The torch-CPU fp32 oracle on the headline workload (all 16 heads, S=4096, norm+RoPE),
-    median of up to 3 timed runs after one warm-up, on this host's torch threads."""
+def _host_info():
+    import subprocess
+    import numpy
     import torch
-    from oracle import attention as oatt
-    from oracle import inputs as oin
-    threads = torch.get_num_threads()
-    d = oin.self_attention(2)
-
-    def run():
-        qq = oatt.qk_prologue(d["q"], d["q_norm_w"], d["eps"], d["rope"])
-        kk = oatt.qk_prologue(d["k"], d["k_norm_w"], d["eps"], d["rope"])
-        return oatt.sdpa(qq, kk, d["v"])
-
-    t0 = time.perf_counter()
-    run()
-    first = time.perf_counter() - t0
-    times = []
-    budget = 30.0
-    spent = first
-    while len(times) < 3 and spent + first < budget:
-        t0 = time.perf_counter()
-        run()
-        dt = time.perf_counter() - t0
-        times.append(dt)
-        spent += dt
-    if not times:
-        times = [first]
-    times.sort()
-    med = times[len(times) // 2]
-    tf = attn_flops(S, S) / med / 1e12
+    model = "?"
     try:
-        model = next((l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")), "?")
-    except OSError:
-        model = "?"
-    print(f"# cpu oracle: {med:.3f} s/call ({tf:.4f} TFLOP/s) on {threads} threads", file=sys.stderr, flush=True)
-    return {"value": round(tf, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"full workload: S=4096 H=16 D=128 self-attention with q/k RMSNorm + DiT RoPE, fp32 torch "
-                      f"oracle, median of {len(times)} run(s) after 1 warm-up",
-            "ms_per_call": round(med * 1e3, 2), "cpu_model": model, "torch": torch.__version__}
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        model = next((l.split(":", 1)[1].strip() for l in out.splitlines() if l.startswith("Model name")), "?")
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "torch": torch.__version__, "numpy": numpy.__version__}
+
+
+def _median_of(fn, runs=5):
+    """Median wall time (s) of ``runs`` calls after one untimed warm-up, and the spread."""
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], times[0], times[-1]
+
+
+def _at_threads(torch, n, fn, runs=5):
+    old = torch.get_num_threads()
+    torch.set_num_threads(n)
+    try:
+        return _median_of(fn, runs)
+    finally:
+        torch.set_num_threads(old)
+
+
+def _oracle_cases():
+    """The five workloads as oracle calls, inputs built once outside the timed runs:
+    C1 S=1024 self-attention, C2 S=4096 self-attention with q/k RMSNorm + DiT RoPE,
+    C3 B4 cross attention 4096x512 with key lengths, C4 Qwen causal GQA B4 S512 with
+    NeoX RoPE and padding, C5 one DiT block at S=4096 (W4 weights dequantised once)."""
+    from oracle import attention as oatt
+    from oracle import blocks as oblk
+    from oracle import inputs as oin
+    cases = {}
+    d1 = oin.self_attention(1)
+    cases["c1_self_attention_s1024"] = (lambda: oatt.sdpa(d1["q"], d1["k"], d1["v"]), attn_flops(1024, 1024))
+    d2 = oin.self_attention(2)
+
+    def c2():
+        qq = oatt.qk_prologue(d2["q"], d2["q_norm_w"], d2["eps"], d2["rope"])
+        kk = oatt.qk_prologue(d2["k"], d2["k_norm_w"], d2["eps"], d2["rope"])
+        return oatt.sdpa(qq, kk, d2["v"])
+    cases["c2_self_attention_s4096_norm_rope"] = (c2, attn_flops(S, S))
+    d3 = oin.cross_attention()
+    L3 = d3["key_lengths"].tolist()
+
+    def c3():
+        qq = oatt.qk_prologue(d3["q"], d3["q_norm_w"], d3["eps"], None)
+        kk = oatt.qk_prologue(d3["k"], d3["k_norm_w"], d3["eps"], None)
+        return oatt.sdpa(qq, kk, d3["v"], key_lengths=L3)
+    cases["c3_cross_attention_b4_masked"] = (c3, sum(4.0 * H * 4096 * l * D for l in L3))
+    d4 = oin.qwen_attention()
+    L4 = d4["key_lengths"].tolist()
+
+    def c4():
+        qq = oatt.qk_prologue(d4["q"], d4["q_norm_w"], d4["eps"], d4["rope"])
+        kk = oatt.qk_prologue(d4["k"], d4["k_norm_w"], d4["eps"], d4["rope"])
+        return oatt.sdpa(qq, kk, d4["v"], causal=True, key_lengths=L4)
+    cases["c4_qwen_causal_gqa_b4_s512"] = (c4, 4.0 * D * 16 * sum(sum(min(i + 1, l) for i in range(512)) for l in L4))
+    d5 = oin.dit_block(S=4096)
+    w5 = oblk.dequant_weights(d5)
+    cases["c5_dit_block_s4096"] = (lambda: oblk.dit_block(d5, boundary="fp16", weights=w5), oblk.block_flops())
+    return cases
+
+
+def cpu_baseline():
+    """The torch-CPU fp32 oracle on the headline workload (all 16 heads, S=4096,
+    norm+RoPE): median of 5 timed runs after one warm-up, on all of this host's torch
+    threads and again on 4 threads (the thread count the reference's own source oracle
+    pins)."""
+    import torch
+    cases = _oracle_cases()
+    fn, fl = cases["c2_self_attention_s4096_norm_rope"]
+    threads = torch.get_num_threads()
+    med, lo, hi = _at_threads(torch, threads, fn)
+    med4, lo4, hi4 = _at_threads(torch, 4, fn)
+    info = _host_info()
+    print(f"# cpu oracle C2: {med:.3f} s/call on {threads} threads, {med4:.3f} s/call on 4 threads ({info})",
+          file=sys.stderr, flush=True)
+    out = {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+           "sample": "full workload: S=4096 H=16 D=128 self-attention with q/k RMSNorm + DiT RoPE, fp32 torch "
+                     "oracle, median of 5 runs after 1 warm-up",
+           "ms_per_call": round(med * 1e3, 2), "ms_min_max": [round(lo * 1e3, 2), round(hi * 1e3, 2)],
+           "threads_4": {"value": round(fl / med4 / 1e12, 5), "ms_per_call": round(med4 * 1e3, 2),
+                         "ms_min_max": [round(lo4 * 1e3, 2), round(hi4 * 1e3, 2)]}}
+    out.update(info)
+    return out
+
+
+def cpu_table():
+    """ms per call of the oracle on C1-C5 (C5 = ms per DiT block) at all threads and at
+    4 threads, median of 5 after 1 warm-up each."""
+    import torch
+    threads = torch.get_num_threads()
+    rows = {}
+    for name, (fn, fl) in _oracle_cases().items():
+        row = {}
+        for n in (threads, 4):
+            med, lo, hi = _at_threads(torch, n, fn)
+            row[f"threads_{n}"] = {"ms": round(med * 1e3, 2), "ms_min_max": [round(lo * 1e3, 2), round(hi * 1e3, 2)],
+                                   "tflops": round(fl / med / 1e12, 5)}
+        rows[name] = row
+        print(f"# cpu oracle {name}: {row}", file=sys.stderr, flush=True)
+    return rows
 
 
 if __name__ == "__main__":
