@@ -65,5 +65,7 @@ PINNING = {
         "shift/scale outputs (detects a shift/scale swap and layout errors)"),
     "blocks.dit_block": (
         "composition of pinned parts following scripts/dit_block0_oracle.py:327-391; "
-        "zero-gate identity and zero-weight invariants"),
+        "zero-gate identity and zero-weight invariants; closed-form blocks (Q = K = 0 with identity "
+        "V/O/MLP projections; a 2x2 grid where only RoPE shapes the softmax) that reject swapped "
+        "shift/scale, another branch's gate, cross K/V from x and a missing Q or K RoPE"),
 }
