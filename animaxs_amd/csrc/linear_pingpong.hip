@@ -233,6 +233,10 @@ void pingpong_gemm_kernel(GemmGroup gp) {
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) wf[t][s][4 * part + e] = h[e];
+    // Pin the result here: the exact redo after the MFMAs overwrites wf, so without
+    // this the compiler sinks the whole one-rounding dequantisation out of the MFMA
+    // sequence into the branch where it survives, after the last MFMA.
+    asm volatile("" : "+v"(wf[t][s]));
   };
   auto dq_step = [&](auto fast_c, auto buf_c, int t, int s) __attribute__((always_inline)) {
     constexpr bool F = decltype(fast_c)::value;
