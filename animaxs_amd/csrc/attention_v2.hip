@@ -192,8 +192,7 @@ void flash_attention_v2_kernel(FlashParams p) {
     for (int r = 0; r < NCP; ++r) store_seg(r, st, bufc);
   };
 
-  half8v qf[QS];
-  load_q_fragment<D>(p, b, head, qi, hh, qf);
+  half8v qf[QS];   // filled in the prologue below, beside the first tile loads
 
   floatx16 acc[OB];
 #pragma unroll
@@ -361,9 +360,17 @@ void flash_attention_v2_kernel(FlashParams p) {
   using S3 = std::integral_constant<int, 3>;
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
+  // Prologue: the loads of tiles 0 and 1, of the Q rows and of the Q norm weight are
+  // all in flight together, so the workgroup pays one memory round trip before its
+  // first MFMA instead of three.
   load_tile(0, B0{});
-  store_tile(S0{}, B0{});
   load_tile(1, B1{});
+  {
+    half8v wn[QS];
+    issue_q_loads<D>(p, b, head, qi, hh, qf, wn);
+    finish_q_fragment<D>(p, qi, hh, qf, wn);
+  }
+  store_tile(S0{}, B0{});
   store_tile(S1{}, B1{});
   load_tile(2, B0{});
   load_tile(3, B1{});
@@ -406,17 +413,31 @@ void flash_attention_v2_kernel(FlashParams p) {
     }
     return;
   }
+  // The fp16 O rows go through LDS so that every global store is a 16-byte piece of a
+  // whole row (D/8 lanes per row).  In registers a lane holds 4-column pieces of one
+  // row, and storing those directly scatters each instruction over 32 rows.  Wave w
+  // uses half of K stage w/2 (32 rows of D+8 halfs), free once both groups are past
+  // their last PV: group 1 finishes its last PV after group 0's final barrier above, so
+  // one more barrier for all waves comes first.
+  barrier();
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (qi < p.Sq) {
-    half_t* op = p.o + (int64_t)b * p.o_batch + (int64_t)head * p.o_head + (int64_t)qi * p.o_tok;
+  half_t* const ost = ((wave >> 1) == 0 ? K0 : (wave >> 1) == 1 ? K1 : (wave >> 1) == 2 ? K2 : K3) +
+                      (wave & 1) * 32 * KROW;
 #pragma unroll
-    for (int c = 0; c < OB; ++c)
+  for (int c = 0; c < OB; ++c)
 #pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        half4v val = {(half_t)(acc[c][4 * e4 + 0] * inv), (half_t)(acc[c][4 * e4 + 1] * inv),
-                      (half_t)(acc[c][4 * e4 + 2] * inv), (half_t)(acc[c][4 * e4 + 3] * inv)};
-        *reinterpret_cast<half4v*>(op + 32 * c + 8 * e4 + 4 * hh) = val;
-      }
+    for (int e4 = 0; e4 < 4; ++e4) {
+      const half4v val = {(half_t)(acc[c][4 * e4 + 0] * inv), (half_t)(acc[c][4 * e4 + 1] * inv),
+                          (half_t)(acc[c][4 * e4 + 2] * inv), (half_t)(acc[c][4 * e4 + 3] * inv)};
+      *reinterpret_cast<half4v*>(ost + c32 * KROW + 32 * c + 8 * e4 + 4 * hh) = val;
+    }
+  constexpr int CPR = D / 8, RPI = 64 / CPR;   // 16-byte chunks per row, rows per store
+  half_t* const obase = p.o + (int64_t)b * p.o_batch + (int64_t)head * p.o_head;
+#pragma unroll
+  for (int i = 0; i < 32 / RPI; ++i) {
+    const int r = i * RPI + lane / CPR, ch = lane % CPR;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(ost + r * KROW + ch * 8);
+    if (wq0 + r < p.Sq) *reinterpret_cast<u32x4*>(obase + (int64_t)(wq0 + r) * p.o_tok + ch * 8) = v;
   }
 }
 
