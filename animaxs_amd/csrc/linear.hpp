@@ -137,6 +137,14 @@ void launch_pingpong_group(const GemmParams* ps, int count, int storage, hipStre
 constexpr int SMALLM_MAX_ROWS = 64;
 bool smallm_supported(const GemmParams& p, int storage);
 void launch_smallm(const GemmParams& p, int storage, hipStream_t stream);
+// Split-K form for W4/W8 (linear_smallm.hip): the number of K slices it runs this GEMM
+// with (0: it does not apply).  With more than one slice the caller passes
+// p.part = [slices][M][N] fp32 and p.ksplit = slices; launch_smallm_splitk adds the
+// slices in order (launch_splitk_reduce) into p.y.
+int smallm_splitk_slices(const GemmParams& p, int storage);
+void launch_smallm_splitk(const GemmParams& p, int storage, hipStream_t stream);
+// y[i] = half(sum_s part[s * count + i]) for i < count, slices added in order.
+void launch_splitk_reduce(const float* part, half_t* y, int64_t count, int ksplit, hipStream_t stream);
 void launch_matvec(const MatvecParams& p, hipStream_t stream);
 // count (1..MV_BATCH) matvecs; one launch when they share storage and lane split.
 void launch_matvec_batch(const MatvecParams* ps, int count, hipStream_t stream);

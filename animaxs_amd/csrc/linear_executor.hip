@@ -106,6 +106,14 @@ void LinearExecutor::encode(anima_buffer input, int64_t input_offset, const anim
     launch_gemm(p, ANIMA_STORAGE_FP16, stream);
     return;
   }
+  const int slices = cfg_.backend == ANIMA_LINEAR_BACKEND_AUTO ? smallm_splitk_slices(p, w.storage) : 0;
+  if (slices > 0) {
+    p.ksplit = slices;
+    if (slices > 1)
+      p.part = static_cast<float*>(ws_.get(checked_product({(int64_t)slices, p.M, p.N, 4}, "LinearExecutor"), stream));
+    launch_smallm_splitk(p, w.storage, stream);
+    return;
+  }
   if (smallm_supported(p, w.storage)) {
     launch_smallm(p, w.storage, stream);
     return;

@@ -674,4 +674,11 @@ void launch_pingpong(const GemmParams& p, int storage, hipStream_t stream) {
   launch_pingpong_group(&p, 1, storage, stream);
 }
 
+void launch_splitk_reduce(const float* part, half_t* y, int64_t count, int ksplit, hipStream_t stream) {
+  const int vec = (count % 4 == 0 && aligned16(part) && aligned8(y)) ? 1 : 0;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((count + 1023) / 1024)), dim3(256), 0, stream, part, y,
+                     static_cast<float*>(nullptr), count, ksplit, vec);
+  ANIMA_HIP(hipGetLastError());
+}
+
 }  // namespace anima

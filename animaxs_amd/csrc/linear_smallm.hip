@@ -407,4 +407,205 @@ void launch_smallm(const GemmParams& g, int storage, hipStream_t stream) {
   ANIMA_HIP(hipGetLastError());
 }
 
+
+// ---------------------------------------------------------------------------
+// Split-K form (W4/W8).  The kernel above gives each 16 weight rows all of X: with
+// 33..64 input rows every wave gathers M x K halfs of X from L2 for 16 x K/2 bytes of
+// weights, and N = 2048 leaves half the chip without a workgroup.  Here:
+//   * a workgroup of SK_WAVES waves owns SK_ROWS weight rows (16 per wave) and one K
+//     slice; the slice of X (all M rows, zero rows up to 16 * MB) is copied into LDS
+//     once with coalesced 16-byte loads, and every wave reads its B fragments there,
+//     so an X byte crosses the CU's memory path once per SK_ROWS weight rows;
+//   * a wave loads all its weight words of the slice at once (one 16-byte load per
+//     lane and chunk for W4, two for W8) and dequantises them chunk by chunk with the
+//     exact rounding of the kernel above (one_rounding_exact, wave-uniform);
+//   * slices are chosen so the grid reaches 256 workgroups; with more than one, each
+//     writes fp32 partial rows [slice][M][N] and launch_splitk_reduce adds them in
+//     slice order (deterministic) and rounds once to fp16.
+// MFMA operand layout as above: A = 16 weight rows x 32 k (lane (r, g) holds row r,
+// k = chunk + 32g + 8t .. +7 of step t), B = X^T with the same k, C lane (r, g) =
+// Y[m = 16mb + r][n = 16w + 4g .. +3].
+// ---------------------------------------------------------------------------
+constexpr int SK_WAVES = 4;
+constexpr int SK_ROWS = 16 * SK_WAVES;
+constexpr int SK_MAX_CHUNKS = 8;              // 128-wide K chunks per slice
+constexpr int64_t SK_MAX_LDS = 160 * 1024;    // X slice bytes per workgroup
+
+template <int STORAGE, int MB, int NCHK>
+__global__ __launch_bounds__(64 * SK_WAVES) void smallm_splitk_kernel(SmallMParams p, float* part, int rgroups) {
+  constexpr int WORDS = SmallMChunk<STORAGE>::WORDS;
+  constexpr int QBITS = STORAGE == ANIMA_STORAGE_W4 ? 4 : 8;
+  constexpr int KS = NCHK * SM_CHUNK;         // K of the slice
+  constexpr int XROW = KS + 8;                // padded LDS row (halfs)
+  constexpr int XCH = KS / 8;                 // 16-byte chunks per X row
+  __shared__ __attribute__((aligned(16))) half_t xs[16 * MB * XROW];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int rg = blockIdx.x % rgroups, slice = blockIdx.x / rgroups;
+  const int k0 = slice * KS;
+  const int nb = rg * SK_ROWS + wave * 16;    // first weight row of this wave
+  // Rows past N re-read row N-1 (computed, never stored).
+  const int n = min(nb + r, p.N - 1);
+  const uint8_t* wrow = p.w + (int64_t)n * p.row_stride;
+
+  uint32_t wv[NCHK][WORDS];
+  half_t sc[NCHK], zc[NCHK];
+#pragma unroll
+  for (int c = 0; c < NCHK; ++c) {
+    const int kl = k0 + c * SM_CHUNK + 32 * g;
+    const int64_t boff = STORAGE == ANIMA_STORAGE_W4 ? kl / 2 : kl;
+    const u32x4* src = reinterpret_cast<const u32x4*>(wrow + boff);
+#pragma unroll
+    for (int v = 0; v < WORDS / 4; ++v) {
+      const u32x4 t4 = __builtin_nontemporal_load(src + v);
+      wv[c][4 * v] = t4[0];
+      wv[c][4 * v + 1] = t4[1];
+      wv[c][4 * v + 2] = t4[2];
+      wv[c][4 * v + 3] = t4[3];
+    }
+    sc[c] = p.scale[(int64_t)n * p.groups + (kl >> 6)];
+    zc[c] = p.zero[(int64_t)n * p.groups + (kl >> 6)];
+  }
+  // The slice of X, 16 loads per thread in flight at a time.  Rows M .. 16 MB - 1 copy
+  // row M - 1: they only feed output columns m >= M, which are never stored.
+  constexpr int PER = 16 * MB * XCH / (64 * SK_WAVES);
+  constexpr int BATCH = PER <= 16 ? PER : (PER % 16 == 0 ? 16 : (PER % 12 == 0 ? 12 : 8));
+  static_assert(PER * 64 * SK_WAVES == 16 * MB * XCH && PER % BATCH == 0, "X copy splits evenly");
+#pragma unroll
+  for (int b0 = 0; b0 < PER; b0 += BATCH) {
+    u32x4 v[BATCH];
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j) {
+      const int i = threadIdx.x + (b0 + j) * 64 * SK_WAVES;
+      const int m = min(i / XCH, p.M - 1), ch = i % XCH;
+      v[j] = *reinterpret_cast<const u32x4*>(p.x + (int64_t)m * p.K + k0 + ch * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j) {
+      const int i = threadIdx.x + (b0 + j) * 64 * SK_WAVES;
+      *reinterpret_cast<u32x4*>(xs + (i / XCH) * XROW + (i % XCH) * 8) = v[j];
+    }
+  }
+  __syncthreads();
+
+  floatx4 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = floatx4{};
+#pragma unroll
+  for (int c = 0; c < NCHK; ++c) {
+    const bool fast = __all(one_rounding_exact<QBITS>(sc[c], zc[c]));
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const half8v a = fast ? dequant_frag<STORAGE, true>(wv[c], t, sc[c], zc[c])
+                            : dequant_frag<STORAGE, false>(wv[c], t, sc[c], zc[c]);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const half8v b = *reinterpret_cast<const half8v*>(xs + (mb * 16 + r) * XROW + c * SM_CHUNK + 32 * g + 8 * t);
+        acc[mb] = mfma16(a, b, acc[mb]);
+      }
+    }
+  }
+
+  const int nc = nb + 4 * g;                  // this lane's first output column
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = mb * 16 + r;
+    if (m >= p.M) continue;
+    if (part) {
+      float* pp = part + ((int64_t)slice * p.M + m) * p.N + nc;
+      if (nc + 3 < p.N && (reinterpret_cast<uintptr_t>(pp) & 15u) == 0) {
+        *reinterpret_cast<floatx4*>(pp) = acc[mb];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (nc + i < p.N) pp[i] = acc[mb][i];
+      }
+    } else {
+      half_t* yp = p.y + (int64_t)m * p.N + nc;
+      if (nc + 3 < p.N && (reinterpret_cast<uintptr_t>(yp) & 7u) == 0) {
+        *reinterpret_cast<half4v*>(yp) =
+            half4v{(half_t)acc[mb][0], (half_t)acc[mb][1], (half_t)acc[mb][2], (half_t)acc[mb][3]};
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (nc + i < p.N) yp[i] = (half_t)acc[mb][i];
+      }
+    }
+  }
+}
+
+int smallm_splitk_slices(const GemmParams& p, int storage) {
+  if (storage != ANIMA_STORAGE_W4 && storage != ANIMA_STORAGE_W8) return 0;
+  if (p.epilogue != GEMM_STORE) return 0;
+  // With up to 32 input rows, or N wide enough for the weight-streaming kernel to give
+  // 256 workgroups of 32 rows, that kernel is faster (it needs no partial rows).
+  if (p.M <= 32 || p.N >= 32 * 256) return 0;
+  if (p.M < 1 || p.M > SMALLM_MAX_ROWS || p.K % SM_CHUNK != 0 || !aligned16(p.x) || !aligned16(p.w) ||
+      p.row_stride % 16 != 0)
+    return 0;
+  const int mb = (p.M + 15) / 16, nch = p.K / SM_CHUNK;
+  const int64_t rgroups = (p.N + SK_ROWS - 1) / SK_ROWS;
+  int best = 0;
+  // The fewest slices that give the grid 256 workgroups (else the most there can be),
+  // each slice 1, 2, 4 or 8 chunks and its X copy within the LDS budget.
+  for (int d = 1; d <= nch; ++d) {
+    if (nch % d != 0) continue;
+    const int ch = nch / d;
+    if (ch > SK_MAX_CHUNKS || (ch & (ch - 1)) != 0) continue;
+    if ((int64_t)16 * mb * (ch * SM_CHUNK + 8) * 2 > SK_MAX_LDS) continue;
+    if (rgroups * d > 0x7fffffff) break;
+    best = d;
+    if (rgroups * d >= 256) break;
+  }
+  return best;
+}
+
+template <int STORAGE, int MB, int NCHK>
+static void launch_splitk_t(const SmallMParams& sp, float* part, int rgroups, int slices, hipStream_t stream) {
+  hipLaunchKernelGGL((smallm_splitk_kernel<STORAGE, MB, NCHK>), dim3((unsigned)(rgroups * slices)),
+                     dim3(64 * SK_WAVES), 0, stream, sp, part, rgroups);
+}
+
+template <int STORAGE, int MB>
+static void launch_splitk_m(const SmallMParams& sp, float* part, int rgroups, int slices, int chunks,
+                            hipStream_t stream) {
+  switch (chunks) {
+    case 1: launch_splitk_t<STORAGE, MB, 1>(sp, part, rgroups, slices, stream); break;
+    case 2: launch_splitk_t<STORAGE, MB, 2>(sp, part, rgroups, slices, stream); break;
+    case 4: launch_splitk_t<STORAGE, MB, 4>(sp, part, rgroups, slices, stream); break;
+    case 8: launch_splitk_t<STORAGE, MB, 8>(sp, part, rgroups, slices, stream); break;
+    default: fail(ANIMA_E_UNSUPPORTED, "small-M split-K GEMM: unsupported slice length");
+  }
+}
+
+template <int STORAGE>
+static void launch_splitk_s(const SmallMParams& sp, float* part, int rgroups, int slices, int chunks,
+                            hipStream_t stream) {
+  switch ((sp.M + 15) / 16) {
+    case 1: launch_splitk_m<STORAGE, 1>(sp, part, rgroups, slices, chunks, stream); break;
+    case 2: launch_splitk_m<STORAGE, 2>(sp, part, rgroups, slices, chunks, stream); break;
+    case 3: launch_splitk_m<STORAGE, 3>(sp, part, rgroups, slices, chunks, stream); break;
+    default: launch_splitk_m<STORAGE, 4>(sp, part, rgroups, slices, chunks, stream); break;
+  }
+}
+
+void launch_smallm_splitk(const GemmParams& g, int storage, hipStream_t stream) {
+  const int slices = smallm_splitk_slices(g, storage);
+  if (slices < 1 || slices != (g.ksplit > 1 ? g.ksplit : 1))
+    fail(ANIMA_E_INVALID_ARGUMENT, "small-M split-K GEMM: slice count does not match the shape");
+  if (slices > 1 && !g.part) fail(ANIMA_E_INVALID_ARGUMENT, "small-M split-K GEMM: missing partial rows");
+  SmallMParams sp{};
+  sp.x = g.x; sp.y = g.y; sp.w = g.w; sp.scale = g.scale; sp.zero = g.zero;
+  sp.row_stride = g.row_stride; sp.M = g.M; sp.N = g.N; sp.K = g.K; sp.groups = g.groups;
+  const int rgroups = (g.N + SK_ROWS - 1) / SK_ROWS;
+  const int chunks = g.K / SM_CHUNK / slices;
+  float* part = slices > 1 ? g.part : nullptr;
+  if (storage == ANIMA_STORAGE_W4)
+    launch_splitk_s<ANIMA_STORAGE_W4>(sp, part, rgroups, slices, chunks, stream);
+  else
+    launch_splitk_s<ANIMA_STORAGE_W8>(sp, part, rgroups, slices, chunks, stream);
+  ANIMA_HIP(hipGetLastError());
+  if (slices > 1) launch_splitk_reduce(g.part, g.y, (int64_t)g.M * g.N, slices, stream);
+}
+
 }  // namespace anima
