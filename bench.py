@@ -64,6 +64,8 @@ def parse():
                          "of the last --trace-last dispatches) and exit")
     ap.add_argument("--trace-last", type=int, default=0, help="with --trace-summary: only the last N dispatches of "
                     "each kernel (the timed ones; 0 = all)")
+    ap.add_argument("--trace-order", type=int, default=0,
+                    help="with --trace-summary: list the last N dispatches of the whole trace in launch order instead")
     return ap.parse_args()
 
 
@@ -87,11 +89,25 @@ def counter_summary(path, last):
             print(f"| `{name[:70]}` | {cname} | {len(v)} | {len(d)} | {d.mean():.1f} | {d.min():.1f} | {d.max():.1f} |")
 
 
-def trace_summary(path, last):
+def trace_summary(path, last, order=0):
     """Per-kernel durations from a rocprofv3 --kernel-trace CSV (Kernel_Name,
-    Start_Timestamp, End_Timestamp in ns)."""
+    Start_Timestamp, End_Timestamp in ns); with ``order`` the last ``order`` dispatches
+    in launch order (start offset from the first of them, duration, grid, kernel)."""
     import csv
     import numpy as np
+    if order:
+        with open(path) as f:
+            rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))[-order:]
+        t0 = int(rows[0]["Start_Timestamp"])
+        print("| start us | duration us | grid (threads) | kernel |")
+        print("|---|---|---|---|")
+        for r in rows:
+            st, en = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+            grid = r.get("Grid_Size_X") or r.get("Grid_Size") or "?"
+            print(f"| {(st - t0) / 1e3:.1f} | {(en - st) / 1e3:.2f} | {grid} | `{r['Kernel_Name'][:80]}` |")
+        last_end = max(int(r["End_Timestamp"]) for r in rows)
+        print(f"\nspan {(last_end - t0) / 1e3:.1f} us, kernel time {sum(int(r['End_Timestamp']) - int(r['Start_Timestamp']) for r in rows) / 1e3:.1f} us")
+        return
     per = {}
     with open(path) as f:
         for r in csv.DictReader(f):
@@ -215,7 +231,7 @@ def time_graph(torch, ctx, fn, calls, reps=5):
 def main():
     args = parse()
     if args.trace_summary:
-        trace_summary(args.trace_summary, args.trace_last)
+        trace_summary(args.trace_summary, args.trace_last, args.trace_order)
         return
     if args.counter_summary:
         counter_summary(args.counter_summary, args.trace_last)
