@@ -160,12 +160,15 @@ void flash_attention_wide_kernel(FlashParams p) {
   floatx16 S;
   half8v P[2];
   auto exps = [&](float msub) __attribute__((always_inline)) -> float {
-    float ls[4] = {0.f, 0.f, 0.f, 0.f};
+    float ls[4];   // started from the first four terms, not from 0.f (same bits)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const float pe = fast_exp2(fmaf(S[e], c2, -msub));
       P[e >> 3][e & 7] = (half_t)pe;
-      ls[e & 3] += pe;
+      if (e < 4)
+        ls[e] = pe;
+      else
+        ls[e & 3] += pe;
     }
     return (ls[0] + ls[1]) + (ls[2] + ls[3]);
   };
