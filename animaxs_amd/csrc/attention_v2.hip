@@ -204,6 +204,13 @@ void flash_attention_v2_kernel(FlashParams p) {
   // ones x P^T product cost more (they lengthen every MFMA phase by 1/8).
   float lrow = 0.f;
   const float c2 = p.scale_log2;
+  // Q carries the factor c2 = scale * log2(e) (folded in before its fp16 rounding), and
+  // the first QK MFMA of each key half starts from C = MB = -mbase: all 16 entries of a
+  // lane's S^T column belong to its query row, so S comes out as the exp2 argument
+  // s * c2 - mbase with no per-score VALU work.  mbase is m_run once a row max exists
+  // (0 before); it changes only on the exact path below.
+  float mbase = 0.f;
+  floatx16 MB = floatx16{};
 
   typedef __attribute__((address_space(3))) half8v lds_half8v;
   typedef __attribute__((address_space(3))) short4v lds_short4v;
@@ -215,12 +222,12 @@ void flash_attention_v2_kernel(FlashParams p) {
   floatx16 S[2];     // scores of the current tile: keys 0..31, 32..63
   half8v P[2][2];    // fp16 probabilities of the previous tile (keys 32h + 16u + ...)
   // G(0) runs the PV step of a tile "-1" in stage 3: P = 0 and V = 0 make it add
-  // exact zeros (stage 3 is first filled in G(1), after two barriers).
+  // exact zeros (stage 3 is zeroed after the prologue's RoPE staging and first filled
+  // in G(1), after two barriers).
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int u = 0; u < 2; ++u) P[h][u] = half8v{};
-  for (int i = tid; i < VTILE / 8; i += F2_NT) reinterpret_cast<half8v*>(V3)[i] = half8v{};
 
   // V^T fragment (c, u) of key half h: lane (d, hh) holds V[key(u, hh, 0..7)][32c + d]
   // with key(u, hh, i) = 32h + 16u + 8(i/4) + 4hh + i%4, the key order of the
@@ -265,7 +272,7 @@ void flash_attention_v2_kernel(FlashParams p) {
       if (i + F2_READ_AHEAD < NOPS) ring[(i + F2_READ_AHEAD) % RING] = read_op(i + F2_READ_AHEAD);
       if (i < NQK) {
         const int h = i / QS;
-        S[h] = mfma32(ring[i % RING], qf[i % QS], i % QS == 0 ? floatx16{} : S[h]);
+        S[h] = mfma32(ring[i % RING], qf[i % QS], i % QS == 0 ? MB : S[h]);
       } else {
         const int k = i - NQK;
         acc[k % OB] = mfma32(ring[i % RING], P[k / (2 * OB)][(k / OB) & 1], acc[k % OB]);
@@ -286,8 +293,9 @@ void flash_attention_v2_kernel(FlashParams p) {
   };
 
   // X(j): the tile copies (tile j+2, staged in registers during X(j-2), goes to
-  // LDS; the loads of tile j+4 start into the buffer it leaves), then P = fp16(exp2(S*c - m)) with the
-  // running max m (updated, with the O rescale, only on the exact path above).  The
+  // LDS; the loads of tile j+4 start into the buffer it leaves), then P = fp16(exp2(S))
+  // (S already holds s * c2 - mbase; the running max m and mbase are updated, with the
+  // O rescale, only on the exact path below).  The
   // copies sit in the VALU phase so that their LDS writes never queue ahead of
   // the fragment reads of this wave's MFMA phase.
   auto x_phase = [&](int j, auto st) __attribute__((always_inline)) {
@@ -311,7 +319,9 @@ void flash_attention_v2_kernel(FlashParams p) {
     // needed anyway.  Only when a lane's sum exceeds that (the first tile, where m_run
     // is -inf, or a row max that grew by about 15) or is not finite does the wave take
     // the exact path: the row max, the O / row-sum rescale, then the exponentials again.
-    auto exps = [&](float msub) __attribute__((always_inline)) -> float {
+    // exps(sub, d): exponentials of S - d (the fast path has d = 0 and no subtraction).
+    auto exps = [&](auto sub, float d) __attribute__((always_inline)) -> float {
+      constexpr bool SUB = decltype(sub)::value;
       // The four partial sums start from the first four terms (not from 0.f, whose
       // addition the compiler must keep): same bits, four adds fewer.
       float ls[4];
@@ -319,7 +329,7 @@ void flash_attention_v2_kernel(FlashParams p) {
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const float pe = fast_exp2(fmaf(S[h][e], c2, -msub));
+          const float pe = fast_exp2(SUB ? S[h][e] - d : S[h][e]);
           P[h][e >> 3][e & 7] = (half_t)pe;
           if (h == 0 && e < 4)
             ls[e] = pe;
@@ -328,8 +338,10 @@ void flash_attention_v2_kernel(FlashParams p) {
         }
       return (ls[0] + ls[1]) + (ls[2] + ls[3]);
     };
-    float tsum = exps(m_run);
-    if (__any(!(tsum <= F2_LAZY_LIMIT))) {
+    float tsum = exps(std::false_type{}, 0.f);
+    // A row with no maximum yet (m_run = -inf: the first tile) always takes the exact
+    // path, so m_run ends up the true running max and mbase = m_run from then on.
+    if (__any(!(tsum <= F2_LAZY_LIMIT) || m_run == -INFINITY)) {
       // NaN-propagating maximum (v_maximum3_f32, no operand canonicalisation) as a
       // shallow tree: 32 scores -> 8 partial maxima -> 1.
       auto mx = [](float a, float b) __attribute__((always_inline)) { return __builtin_elementwise_maximum(a, b); };
@@ -338,7 +350,7 @@ void flash_attention_v2_kernel(FlashParams p) {
       for (int i = 0; i < 8; ++i) part[i] = mx(mx(S[i >> 2][4 * (i & 3)], S[i >> 2][4 * (i & 3) + 1]),
                                               mx(S[i >> 2][4 * (i & 3) + 2], S[i >> 2][4 * (i & 3) + 3]));
       float mloc = mx(mx(mx(part[0], part[1]), mx(part[2], part[3])), mx(mx(part[4], part[5]), mx(part[6], part[7])));
-      mloc = xlane32_max(mloc) * c2;
+      mloc = xlane32_max(mloc) + mbase;
       const float mnew = fmaxf(m_run, mloc);
       if (mnew > m_run) {
         const float alpha = (m_run == -INFINITY) ? 1.f : fast_exp2(m_run - mnew);
@@ -347,7 +359,10 @@ void flash_attention_v2_kernel(FlashParams p) {
         for (int c = 0; c < OB; ++c) acc[c] *= alpha;
         m_run = mnew;
       }
-      tsum = exps((m_run == -INFINITY) ? 0.f : m_run);
+      tsum = exps(std::true_type{}, (m_run == -INFINITY) ? 0.f : m_run - mbase);
+      mbase = (m_run == -INFINITY) ? 0.f : m_run;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) MB[e] = -mbase;
     }
     lrow += tsum;
     asm volatile("" ::"v"(P[0][0]), "v"(P[0][1]), "v"(P[1][0]), "v"(P[1][1]));
@@ -365,16 +380,26 @@ void flash_attention_v2_kernel(FlashParams p) {
   using S3 = std::integral_constant<int, 3>;
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
-  // Prologue: the loads of tiles 0 and 1, of the Q rows and of the Q norm weight are
-  // all in flight together, so the workgroup pays one memory round trip before its
-  // first MFMA instead of three.
-  load_tile(0, B0{});
-  load_tile(1, B1{});
+  // Prologue: the loads of the Q rows, of the Q norm weight, of the RoPE table rows and
+  // of tiles 0 and 1 are all in flight together, so the workgroup pays one memory round
+  // trip before its first MFMA instead of three.
   {
-    half8v wn[QS];
-    issue_q_loads<D>(p, b, head, qi, hh, qf, wn);
-    finish_q_fragment<D>(p, qi, hh, qf, wn);
+    // The Q loads go first (they are on the critical path), then tiles 0 and 1.  The Q
+    // norm weight and RoPE table rows are staged through LDS (finish_q_fragment): waves
+    // 0-3 use K stages 0-3, waves 4-7 V stages 0-3, all free until the tile stores
+    // below, which wait behind one barrier for every wave's staged reads.
+    static_assert(QStage<D>::BYTES <= KTILE * 2 && QStage<D>::BYTES <= VTILE * 2, "Q staging fits a stage");
+    half_t* const rreg = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? K2 : wave == 3 ? K3
+                       : wave == 4 ? V0 : wave == 5 ? V1 : wave == 6 ? V2 : V3;
+    uint32_t wn = 0;
+    uint64_t rp[QStage<D>::LOADS];
+    issue_q_loads<D>(p, b, head, qi, hh, wq0, lane, qf, wn, rp);
+    load_tile(0, B0{});
+    load_tile(1, B1{});
+    finish_q_fragment<D>(p, hh, lane, qf, wn, rp, (__attribute__((address_space(3))) char*)rreg, c2);
+    if (p.q_norm_w || p.rope) barrier();
   }
+  for (int i = tid; i < VTILE / 8; i += F2_NT) reinterpret_cast<half8v*>(V3)[i] = half8v{};
   store_tile(S0{}, B0{});
   store_tile(S1{}, B1{});
   load_tile(2, B0{});

@@ -18,31 +18,77 @@ __device__ __forceinline__ float xlane32_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Q fragment of one 32-row block (B operand of S^T): lane holds
-// Q[row][16s + 8h + 0..7] with the per-head RMSNorm and split-half RoPE fused.
-// issue_q_loads starts the loads of the raw row and of the norm weight (so a caller
-// can put other loads in flight beside them); finish_q_fragment waits for them and
-// applies the norm and the RoPE (whose table rows it loads itself).
+// Q fragment of one 32-row block (B operand of S^T): lane (c32, hh) holds
+// Q[row][16s + 8hh + 0..7] with the per-head RMSNorm and split-half RoPE fused.
+// issue_q_loads starts the loads of the raw rows, of the norm weight and of the RoPE
+// table rows (so a caller can put other loads in flight behind them); finish_q_fragment
+// waits for them, applies the norm and the RoPE, then multiplies by qmul before the
+// one fp16 rounding (a kernel that folds the softmax scale into Q passes it here).
+//
+// All workgroups of a launch run this at once, and the vector memory path (about 32
+// bytes per cycle per CU for 16-byte loads) is what limits it, so the loads move as
+// few bytes as they can and the data that lanes share goes through LDS:
+//  * the norm weight ([D] fp16, the same for every lane) is one 4-byte piece per lane,
+//    written to LDS and read back as the 16-byte pieces each lane needs;
+//  * of each [cos, -sin, sin, cos] table block only (cos, -sin) is loaded (8 bytes);
+//    lane (c32, hh) needs blocks 16s + 8hh + i (s < D/32, i < 8) of the table row of
+//    its query row, which per-lane loads would fetch as 64 different 128-byte lines
+//    per instruction.  Instead the wave loads its 32 rows coalesced (one row piece of
+//    D/2 blocks per D/2 lanes), writes them to LDS rows of PITCH bytes (the 16-byte
+//    pad puts 16 consecutive rows on distinct banks) and each lane reads its blocks
+//    two at a time.
+// The wave's LDS region (QStage<D>::BYTES) is private to it; the caller must not reuse
+// it for other data before every wave of the workgroup is past finish_q_fragment.
 template <int D>
-__device__ __forceinline__ void issue_q_loads(const FlashParams& p, int b, int head, int qi, int hh,
-                                              half8v (&qf)[D / 16], half8v (&wn)[D / 16]) {
+struct QStage {
+  static constexpr int E = D / 2;                 // table blocks per row
+  static constexpr int PITCH = E * 8 + 16;        // LDS row pitch (bytes)
+  static constexpr int LOADS = E / 2;             // 8-byte loads per lane (64 / E rows per load)
+  static constexpr int WN = 32 * PITCH;           // offset of the norm weight copy
+  static constexpr int BYTES = WN + D * 2;        // LDS bytes per wave
+  static_assert(E <= 64 && 64 % E == 0 && E % 16 == 0, "whole rows per load");
+};
+
+template <int D>
+__device__ __forceinline__ void issue_q_loads(const FlashParams& p, int b, int head, int qi, int hh, int wq0,
+                                              int lane, half8v (&qf)[D / 16], uint32_t& wn,
+                                              uint64_t (&rp)[QStage<D>::LOADS]) {
+  using R = QStage<D>;
   constexpr int QS = D / 16;
   const int qrow = qi < p.Sq ? qi : p.Sq - 1;
   const half_t* qp = p.q + (int64_t)b * p.q_batch + (int64_t)head * p.q_head + (int64_t)qrow * p.q_tok;
 #pragma unroll
   for (int s = 0; s < QS; ++s) qf[s] = *reinterpret_cast<const half8v*>(qp + 16 * s + 8 * hh);
-  if (p.q_norm_w) {
+  if (p.q_norm_w && lane < D / 2) wn = *reinterpret_cast<const uint32_t*>(p.q_norm_w + 2 * lane);
+  if (p.rope) {
+    const char* tab = reinterpret_cast<const char*>(p.rope);
 #pragma unroll
-    for (int s = 0; s < QS; ++s) wn[s] = *reinterpret_cast<const half8v*>(p.q_norm_w + 16 * s + 8 * hh);
+    for (int t = 0; t < R::LOADS; ++t) {
+      const int row = t * (64 / R::E) + lane / R::E;
+      const int rrow = wq0 + row < p.Sq ? wq0 + row : p.Sq - 1;
+      rp[t] = *reinterpret_cast<const uint64_t*>(tab + (int64_t)rrow * (8 * D) + (lane % R::E) * 16);
+    }
   }
 }
 
 template <int D>
-__device__ __forceinline__ void finish_q_fragment(const FlashParams& p, int qi, int hh, half8v (&qf)[D / 16],
-                                                  const half8v (&wn)[D / 16]) {
+__device__ __forceinline__ void finish_q_fragment(const FlashParams& p, int hh, int lane, half8v (&qf)[D / 16],
+                                                  uint32_t wn, const uint64_t (&rp)[QStage<D>::LOADS],
+                                                  __attribute__((address_space(3))) char* region,
+                                                  float qmul = 1.f) {
   constexpr int QS = D / 16;
-  if (p.q_norm_w || p.rope) {
-    const int qrow = qi < p.Sq ? qi : p.Sq - 1;
+  using R = QStage<D>;
+  typedef __attribute__((address_space(3))) uint64_t lds_u64;
+  typedef __attribute__((address_space(3))) uint32_t lds_u32;
+  typedef __attribute__((address_space(3))) half8v lds_half8v;
+  typedef __attribute__((address_space(3))) floatx4 lds_floatx4;
+  if (p.q_norm_w && lane < D / 2) *(lds_u32*)(region + R::WN + 4 * lane) = wn;
+  if (p.rope) {
+#pragma unroll
+    for (int t = 0; t < R::LOADS; ++t)
+      *(lds_u64*)(region + (t * (64 / R::E) + lane / R::E) * R::PITCH + (lane % R::E) * 8) = rp[t];
+  }
+  if (p.q_norm_w || p.rope || qmul != 1.f) {
     float x[QS][8];
 #pragma unroll
     for (int s = 0; s < QS; ++s)
@@ -57,35 +103,34 @@ __device__ __forceinline__ void finish_q_fragment(const FlashParams& p, int qi, 
       ss = xlane32_sum(ss);
       const float inv = rsqrtf(ss / (float)D + p.eps);
 #pragma unroll
-      for (int s = 0; s < QS; ++s)
+      for (int s = 0; s < QS; ++s) {
+        const half8v w = *(const lds_half8v*)(region + R::WN + (16 * s + 8 * hh) * 2);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] * inv * (float)wn[s][i];
+        for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] * inv * (float)w[i];
+      }
     }
     if (p.rope) {
-      const float* rr = p.rope + (int64_t)qrow * (D / 2) * 4;
+      const int c32 = lane & 31;
 #pragma unroll
       for (int s = 0; s < QS / 2; ++s)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const floatx4 blk = *reinterpret_cast<const floatx4*>(rr + (16 * s + 8 * hh + i) * 4);
-          const float a = x[s][i], bb = x[s + QS / 2][i];
-          x[s][i] = blk[0] * a + blk[1] * bb;
-          x[s + QS / 2][i] = blk[2] * a + blk[0] * bb;
+        for (int i = 0; i < 8; i += 2) {
+          // blocks 16s + 8hh + i and + i + 1: (cos, -sin) each
+          const floatx4 cs = *(const lds_floatx4*)(region + c32 * R::PITCH + (16 * s + 8 * hh + i) * 8);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const float c = cs[2 * u], ns = cs[2 * u + 1];
+            const float a = x[s][i + u], bb = x[s + QS / 2][i + u];
+            x[s][i + u] = c * a + ns * bb;
+            x[s + QS / 2][i + u] = -ns * a + c * bb;
+          }
         }
     }
 #pragma unroll
     for (int s = 0; s < QS; ++s)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) qf[s][i] = f32_to_f16(x[s][i]);
+      for (int i = 0; i < 8; ++i) qf[s][i] = f32_to_f16(x[s][i] * qmul);
   }
-}
-
-template <int D>
-__device__ __forceinline__ void load_q_fragment(const FlashParams& p, int b, int head, int qi, int hh,
-                                                half8v (&qf)[D / 16]) {
-  half8v wn[D / 16];
-  issue_q_loads<D>(p, b, head, qi, hh, qf, wn);
-  finish_q_fragment<D>(p, qi, hh, qf, wn);
 }
 
 }  // namespace anima
