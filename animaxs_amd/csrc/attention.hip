@@ -57,10 +57,12 @@ __global__ __launch_bounds__(FA_NT, 2) void flash_attention_kernel(FlashParams p
   const int c32 = lane & 31, hh = lane >> 5;
 
   int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  // Heads vary slowest (as in the 256-row kernel): each XCD's range of logical blocks
+  // is whole heads over every batch entry.
   const int qt = lb % p.q_tiles;
   lb /= p.q_tiles;
-  const int head = lb % p.H;
-  const int b = lb / p.H;
+  const int b = lb % p.nbatch;
+  const int head = lb / p.nbatch;
   const int kvh = head / p.group;
   const int q0 = qt * FA_BM;
   const int qi = q0 + wave * 32 + c32;
@@ -532,6 +534,7 @@ int64_t flash_split_bytes(const FlashParams& p, int D, int batch, int splits) {
 // Head dim 384: the wide kernel, 128 query rows per workgroup, keys split when the query
 // tiles alone cannot cover the chip.
 static void launch_flash_wide_plan(FlashParams p, int D, int batch, hipStream_t stream) {
+  p.nbatch = batch;
   if (32 * std::max(p.k_tok, p.v_tok) * (int64_t)sizeof(half_t) >= ((int64_t)1 << 31))
     fail(ANIMA_E_INVALID_SHAPE, "wide flash attention requires 32 key rows to span < 2 GiB");
   p.q_tiles = (p.Sq + FLASH_WIDE_ROWS - 1) / FLASH_WIDE_ROWS;
@@ -552,6 +555,7 @@ static void launch_flash_wide_plan(FlashParams p, int D, int batch, hipStream_t 
 }
 
 void launch_flash(FlashParams p, int D, int batch, int flash_rows, hipStream_t stream) {
+  p.nbatch = batch;   // the kernels map block -> (query tile, batch, head) through it
   if (D == 384) {
     launch_flash_wide_plan(p, D, batch, stream);
     return;
@@ -584,6 +588,8 @@ void launch_flash(FlashParams p, int D, int batch, int flash_rows, hipStream_t s
   if (v2) {
     launch_flash_v2(p, D, grid, stream);
   } else {
+    if (p.nbatch < 1 || p.H < 1 || blocks != (int64_t)p.q_tiles * p.H * p.nbatch)
+      fail(ANIMA_E_INVALID_ARGUMENT, "flash attention grid does not match its tiles, heads and batch");
     if (D == 128)
       hipLaunchKernelGGL(flash_attention_kernel<128>, grid, dim3(FA_NT), 0, stream, p);
     else

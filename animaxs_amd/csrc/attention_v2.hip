@@ -96,10 +96,13 @@ void flash_attention_v2_kernel(FlashParams p) {
     split = lb % p.kv_splits;
     lb /= p.kv_splits;
   }
+  // Heads vary slowest: the XCD that owns a range of logical blocks gets whole heads
+  // (their K/V stay in its L2) over every batch entry, so batches of different key
+  // lengths spread evenly over the XCDs.
   const int qt = lb % p.q_tiles;
   lb /= p.q_tiles;
-  const int head = lb % p.H;
-  const int b = lb / p.H;
+  const int b = lb % p.nbatch;
+  const int head = lb / p.nbatch;
   const int kvh = head / p.group;
   const int q0 = qt * FLASH_V2_ROWS;
   const int wq0 = q0 + wave * 32;
@@ -523,6 +526,11 @@ void launch_flash_combine(const FlashParams& p, int D, int batch, hipStream_t st
 }
 
 void launch_flash_v2(const FlashParams& p, int D, dim3 grid, hipStream_t stream) {
+  // The kernel decodes blockIdx into (split, query tile, batch, head) with these counts:
+  // a grid of any other size would address rows past the tensors.
+  if (p.nbatch < 1 || p.q_tiles < 1 || p.H < 1 ||
+      (int64_t)grid.x != (int64_t)p.q_tiles * p.H * p.nbatch * (p.kv_splits > 1 ? p.kv_splits : 1))
+    fail(ANIMA_E_INVALID_ARGUMENT, "flash attention grid does not match its tiles, heads and batch");
   if (D == 128)
     hipLaunchKernelGGL(flash_attention_v2_kernel<128>, grid, dim3(F2_NT), 0, stream, p);
   else if (D == 64)
