@@ -388,19 +388,20 @@ void flash_attention_v2_kernel(FlashParams p) {
   // trip before its first MFMA instead of three.
   {
     // The Q loads go first (they are on the critical path), then tiles 0 and 1.  The Q
-    // norm weight and RoPE table rows are staged through LDS (finish_q_fragment): waves
-    // 0-3 use K stages 0-3, waves 4-7 V stages 0-3, all free until the tile stores
-    // below, which wait behind one barrier for every wave's staged reads.
+    // rows, the Q norm weight and the RoPE table rows are staged through LDS
+    // (finish_q_fragment): waves 0-3 use K stages 0-3, waves 4-7 V stages 0-3, all free
+    // until the tile stores below, which wait behind one barrier for every wave's
+    // staged reads.
     static_assert(QStage<D>::BYTES <= KTILE * 2 && QStage<D>::BYTES <= VTILE * 2, "Q staging fits a stage");
     half_t* const rreg = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? K2 : wave == 3 ? K3
                        : wave == 4 ? V0 : wave == 5 ? V1 : wave == 6 ? V2 : V3;
     uint32_t wn = 0;
     uint64_t rp[QStage<D>::LOADS];
-    issue_q_loads<D>(p, b, head, qi, hh, wq0, lane, qf, wn, rp);
+    issue_q_loads<D>(p, b, head, hh, wq0, lane, qf, wn, rp);
     load_tile(0, B0{});
     load_tile(1, B1{});
     finish_q_fragment<D>(p, hh, lane, qf, wn, rp, (__attribute__((address_space(3))) char*)rreg, c2);
-    if (p.q_norm_w || p.rope) barrier();
+    barrier();
   }
   for (int i = tid; i < VTILE / 8; i += F2_NT) reinterpret_cast<half8v*>(V3)[i] = half8v{};
   store_tile(S0{}, B0{});

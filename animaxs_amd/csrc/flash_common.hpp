@@ -28,6 +28,10 @@ __device__ __forceinline__ float xlane32_sum(float x) {
 // All workgroups of a launch run this at once, and the vector memory path (about 32
 // bytes per cycle per CU for 16-byte loads) is what limits it, so the loads move as
 // few bytes as they can and the data that lanes share goes through LDS:
+//  * the Q rows: a fragment load would have the 64 lanes of an instruction touch 32
+//    rows with 32 bytes each (about 16 bytes per cycle per CU for that pattern), so
+//    each instruction loads whole row pieces (D/8 lanes per row) into a register,
+//    which goes to LDS rows of QPITCH bytes and back as the lane's fragment;
 //  * the norm weight ([D] fp16, the same for every lane) is one 4-byte piece per lane,
 //    written to LDS and read back as the 16-byte pieces each lane needs;
 //  * of each [cos, -sin, sin, cos] table block only (cos, -sin) is loaded (8 bytes);
@@ -46,19 +50,26 @@ struct QStage {
   static constexpr int LOADS = E / 2;             // 8-byte loads per lane (64 / E rows per load)
   static constexpr int WN = 32 * PITCH;           // offset of the norm weight copy
   static constexpr int BYTES = WN + D * 2;        // LDS bytes per wave
+  static constexpr int QPITCH = D * 2 + 16;       // LDS row pitch of the Q rows (reuses offset 0)
+  static constexpr int QLPR = D / 8;              // lanes per Q row in one load
   static_assert(E <= 64 && 64 % E == 0 && E % 16 == 0, "whole rows per load");
+  static_assert(32 * QPITCH <= WN && 64 % QLPR == 0, "Q rows fit before the norm weight");
 };
 
 template <int D>
-__device__ __forceinline__ void issue_q_loads(const FlashParams& p, int b, int head, int qi, int hh, int wq0,
+__device__ __forceinline__ void issue_q_loads(const FlashParams& p, int b, int head, int hh, int wq0,
                                               int lane, half8v (&qf)[D / 16], uint32_t& wn,
                                               uint64_t (&rp)[QStage<D>::LOADS]) {
   using R = QStage<D>;
   constexpr int QS = D / 16;
-  const int qrow = qi < p.Sq ? qi : p.Sq - 1;
-  const half_t* qp = p.q + (int64_t)b * p.q_batch + (int64_t)head * p.q_head + (int64_t)qrow * p.q_tok;
+  // Q rows: load t moves rows t * 64/QLPR + lane/QLPR, chunk lane % QLPR (rows past the
+  // sequence repeat the last row); finish_q_fragment turns them into the fragment.
+  const half_t* qp = p.q + (int64_t)b * p.q_batch + (int64_t)head * p.q_head + 8 * (lane % R::QLPR);
 #pragma unroll
-  for (int s = 0; s < QS; ++s) qf[s] = *reinterpret_cast<const half8v*>(qp + 16 * s + 8 * hh);
+  for (int t = 0; t < QS; ++t) {
+    const int row = wq0 + t * (64 / R::QLPR) + lane / R::QLPR;
+    qf[t] = *reinterpret_cast<const half8v*>(qp + (int64_t)(row < p.Sq ? row : p.Sq - 1) * p.q_tok);
+  }
   if (p.q_norm_w && lane < D / 2) wn = *reinterpret_cast<const uint32_t*>(p.q_norm_w + 2 * lane);
   if (p.rope) {
     const char* tab = reinterpret_cast<const char*>(p.rope);
@@ -82,6 +93,15 @@ __device__ __forceinline__ void finish_q_fragment(const FlashParams& p, int hh, 
   typedef __attribute__((address_space(3))) uint32_t lds_u32;
   typedef __attribute__((address_space(3))) half8v lds_half8v;
   typedef __attribute__((address_space(3))) floatx4 lds_floatx4;
+  // Q rows to LDS and back as the fragment (lane (c32, hh): row c32, columns 16s + 8hh ..).
+#pragma unroll
+  for (int t = 0; t < QS; ++t)
+    *(lds_half8v*)(region + (t * (64 / R::QLPR) + lane / R::QLPR) * R::QPITCH + (lane % R::QLPR) * 16) = qf[t];
+  {
+    const int c32 = lane & 31;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) qf[s] = *(const lds_half8v*)(region + c32 * R::QPITCH + (16 * s + 8 * hh) * 2);
+  }
   if (p.q_norm_w && lane < D / 2) *(lds_u32*)(region + R::WN + 4 * lane) = wn;
   if (p.rope) {
 #pragma unroll
