@@ -33,7 +33,7 @@ struct FlashParams {
   int kv_splits;                   // 0 or 1: no split
   int nbatch;                      // batch count (partial row index)
   int kv_chunk;                    // keys per split, a multiple of 64
-  float* part_o;
+  void* part_o;                    // key splits: rows [split][batch][head][Sq][D]: fp16 O_s / l_s (fp32 O_s for D = 384)
   float* part_ml;
 };
 
@@ -53,6 +53,7 @@ void launch_flash(FlashParams p, int D, int batch, int flash_rows, hipStream_t s
 // p.part_o / p.part_ml of flash_split_bytes() when it returns more than 1.
 int flash_kv_splits(const FlashParams& p, int D, int batch, int flash_rows);
 int64_t flash_split_bytes(const FlashParams& p, int D, int batch, int splits);
+int64_t flash_split_o_bytes(const FlashParams& p, int D, int batch, int splits);
 
 // 256-row flash variant (attention_v2.hip); p.q_tiles counts 256-row tiles.
 constexpr int FLASH_V2_ROWS = 256;

@@ -304,8 +304,8 @@ void AttentionExecutor::encode_impl(const anima_attention_args& a, bool no_alloc
   if (use_flash) {
     if (splits > 1) {
       p.kv_splits = splits;
-      p.part_o = reinterpret_cast<float*>(pw);
-      p.part_ml = reinterpret_cast<float*>(pw + checked_product({(int64_t)splits, B, H, Sq, D, 4}, "attention"));
+      p.part_o = pw;
+      p.part_ml = reinterpret_cast<float*>(pw + flash_split_o_bytes(p, (int)D, (int)B, splits));
     }
     launch_flash(p, (int)D, (int)B, cfg_.flash_rows, stream);
   } else {

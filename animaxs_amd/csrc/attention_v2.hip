@@ -433,19 +433,12 @@ void flash_attention_v2_kernel(FlashParams p) {
   wait_vmcnt_imm<0>();            // loads of tiles past the end (no memory traffic)
 
   const float l_tot = xlane32_sum(lrow);
-  if (p.kv_splits > 1) {
-    if (qi < p.Sq) {
-      const int64_t row = (((int64_t)split * p.nbatch + b) * p.H + head) * p.Sq + qi;
-      float* po = p.part_o + row * D;
-#pragma unroll
-      for (int c = 0; c < OB; ++c)
-#pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4)
-          *reinterpret_cast<floatx4*>(po + 32 * c + 8 * e4 + 4 * hh) =
-              floatx4{acc[c][4 * e4], acc[c][4 * e4 + 1], acc[c][4 * e4 + 2], acc[c][4 * e4 + 3]};
-      if (hh == 0) *reinterpret_cast<float2*>(p.part_ml + row * 2) = make_float2(m_run, l_tot);
-    }
-    return;
+  // A key split stores its normalised rows O_s / l_s in fp16 (below, through the same
+  // whole-row path as O) beside the fp32 (max, sum) pair of each row; the merge weighs
+  // them by l_s.
+  if (p.kv_splits > 1 && qi < p.Sq && hh == 0) {
+    const int64_t row = (((int64_t)split * p.nbatch + b) * p.H + head) * p.Sq + qi;
+    *reinterpret_cast<float2*>(p.part_ml + row * 2) = make_float2(m_run, l_tot);
   }
   // The fp16 O rows go through LDS so that every global store is a 16-byte piece of a
   // whole row (D/8 lanes per row).  In registers a lane holds 4-column pieces of one
@@ -466,17 +459,22 @@ void flash_attention_v2_kernel(FlashParams p) {
       *reinterpret_cast<half4v*>(ost + c32 * KROW + 32 * c + 8 * e4 + 4 * hh) = val;
     }
   constexpr int CPR = D / 8, RPI = 64 / CPR;   // 16-byte chunks per row, rows per store
-  half_t* const obase = p.o + (int64_t)b * p.o_batch + (int64_t)head * p.o_head;
+  half_t* const obase = p.kv_splits > 1
+                            ? static_cast<half_t*>(p.part_o) + (((int64_t)split * p.nbatch + b) * p.H + head) * p.Sq * D
+                            : p.o + (int64_t)b * p.o_batch + (int64_t)head * p.o_head;
+  const int64_t otok = p.kv_splits > 1 ? D : p.o_tok;
 #pragma unroll
   for (int i = 0; i < 32 / RPI; ++i) {
     const int r = i * RPI + lane / CPR, ch = lane % CPR;
     const u32x4 v = *reinterpret_cast<const u32x4*>(ost + r * KROW + ch * 8);
-    if (wq0 + r < p.Sq) *reinterpret_cast<u32x4*>(obase + (int64_t)(wq0 + r) * p.o_tok + ch * 8) = v;
+    if (wq0 + r < p.Sq) *reinterpret_cast<u32x4*>(obase + (int64_t)(wq0 + r) * otok + ch * 8) = v;
   }
 }
 
 // Merge of the key splits: O = sum_s w_s O_s / sum_s w_s l_s with w_s = 2^(m_s - max m).
-// Thread t of a row handles columns 8t .. 8t+7.
+// The 256-row kernel stores O_s as l_s * Ohat_s with Ohat_s its fp16 normalised row; the
+// head-dim-384 kernel stores O_s itself in fp32.  Thread t of a row handles columns
+// 8t .. 8t+7.
 template <int D>
 __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p, int64_t rows) {
   constexpr int TPR = D / 8;
@@ -495,13 +493,20 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p, int64
   for (int s = 0; s < p.kv_splits; ++s) {
     const float ms = p.part_ml[(s * rows + row) * 2];
     const float w = ms == -INFINITY ? 0.f : fast_exp2(ms - mmax);
-    l = fmaf(w, p.part_ml[(s * rows + row) * 2 + 1], l);
-    const float* po = p.part_o + (s * rows + row) * D + 8 * t;
-    const floatx4 a = *reinterpret_cast<const floatx4*>(po), c = *reinterpret_cast<const floatx4*>(po + 4);
+    const float wl = w * p.part_ml[(s * rows + row) * 2 + 1];
+    l += wl;
+    if constexpr (D == 384) {
+      const float* po = static_cast<const float*>(p.part_o) + (s * rows + row) * D + 8 * t;
+      const floatx4 a = *reinterpret_cast<const floatx4*>(po), c = *reinterpret_cast<const floatx4*>(po + 4);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      acc[e] = fmaf(w, a[e], acc[e]);
-      acc[4 + e] = fmaf(w, c[e], acc[4 + e]);
+      for (int e = 0; e < 4; ++e) {
+        acc[e] = fmaf(w, a[e], acc[e]);
+        acc[4 + e] = fmaf(w, c[e], acc[4 + e]);
+      }
+    } else {
+      const half8v a = *reinterpret_cast<const half8v*>(static_cast<const half_t*>(p.part_o) + (s * rows + row) * D + 8 * t);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(wl, (float)a[e], acc[e]);
     }
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;

@@ -247,7 +247,7 @@ void flash_attention_wide_kernel(FlashParams p) {
   if (p.kv_splits > 1) {
     if (qi < p.Sq) {
       const int64_t row = (((int64_t)split * p.nbatch + b) * p.H + head) * p.Sq + qi;
-      float* po = p.part_o + row * D + DH * dh;
+      float* po = static_cast<float*>(p.part_o) + row * D + DH * dh;
 #pragma unroll
       for (int c = 0; c < OB; ++c)
 #pragma unroll
