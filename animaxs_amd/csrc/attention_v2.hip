@@ -30,11 +30,13 @@
 //     distinct banks (64 banks x 4 B); padding instead of an XOR swizzle keeps
 //     every fragment address "per-lane base + immediate".  V^T fragments come
 //     straight from the row-major V tile with ds_read_b64_tr_b16.
-//   * Exps use the running max without computing the tile's row max: a lane's
-//     share of the tile's row sum above 2^15 (or not finite) sends the wave to the
-//     exact path (row max, O / row-sum rescale, exps again), which the first tile
-//     always takes.  Four LDS stages: tile j is read by QK while tile j-1 is read
-//     by PV and tile j+2 is written.
+//   * Q carries scale * log2(e) and the QK MFMAs start from C = -m, so the scores
+//     come out as exp2 arguments.  Exps use the running max without computing the
+//     tile's row max: a lane's share of the tile's row sum above 2^15 (or not
+//     finite), or a row with no max yet, sends the wave to the exact path (row max,
+//     O / row-sum rescale, exps again), which the first tile always takes.  Four LDS
+//     stages: tile j is read by QK while tile j-1 is read by PV and tile j+2 is
+//     written.
 //   * Everything (Q, O accumulators, scores, row sums) lives in the 256 VGPRs a
 //     wave gets at 2 waves/SIMD.
 #include <type_traits>
@@ -245,9 +247,8 @@ void flash_attention_v2_kernel(FlashParams p) {
     return half8v{lo_h[0], lo_h[1], lo_h[2], lo_h[3], hi_h[0], hi_h[1], hi_h[2], hi_h[3]};
   };
 
-  // G(j): S = K_j Q^T, O += V_{j-1}^T P_{j-1}; the probabilities of keys 32..63 of
-  // tile j-1 are computed under the first (key half 0) QK MFMAs, before QK
-  // overwrites those scores.
+  // G(j): S = K_j Q^T - m (each key half's first MFMA starts from C = MB),
+  // O += V_{j-1}^T P_{j-1}.
   auto g_phase = [&](int j, auto st) __attribute__((always_inline)) {
     constexpr int ST = decltype(st)::value;
     using SPREV = std::integral_constant<int, (ST + 3) % F2_STAGES>;
@@ -408,8 +409,6 @@ void flash_attention_v2_kernel(FlashParams p) {
   store_tile(S1{}, B1{});
   load_tile(2, B0{});
   load_tile(3, B1{});
-#pragma unroll
-  for (int e = 0; e < 16; ++e) S[1][e] = -INFINITY;   // G(0) derives P[1] of tile "-1": zeros
   barrier();                      // tiles 0 and 1 resident
   if (group == 1) barrier();      // group 1 runs one phase behind
   // Tile j uses stage j % 4; the loop is unrolled by four so every stage is static.
