@@ -251,6 +251,9 @@ void flash_attention_v2_kernel(FlashParams p) {
   // O += V_{j-1}^T P_{j-1}.
   auto g_phase = [&](int j, auto st) __attribute__((always_inline)) {
     constexpr int ST = decltype(st)::value;
+    // The MFMA phase's wave issues ahead of its SIMD partner's VALU phase (the
+    // partner fills the gaps): -1 % at S=4096 against equal priorities.
+    __builtin_amdgcn_s_setprio(1);
     using SPREV = std::integral_constant<int, (ST + 3) % F2_STAGES>;
     const lds_half8v* ks = (const lds_half8v*)(kstage(st) + kfrag);
     // Anchor the keys-32..63 exponentials in this phase (the compiler would hoist
@@ -284,6 +287,7 @@ void flash_attention_v2_kernel(FlashParams p) {
       __builtin_amdgcn_sched_barrier(0);
     }
     asm volatile("" ::"v"(S[0]), "v"(S[1]));
+    __builtin_amdgcn_s_setprio(0);
   };
 
   // Final PV of the last tile (stage st).

@@ -268,6 +268,8 @@ void pingpong_gemm_kernel(GemmGroup gp) {
   // the wave redoes the block with the fp32 FMA after the MFMAs (next_exact).
   auto m_phase = [&](auto buf_c) __attribute__((always_inline)) {
     constexpr int NOPS = 16, RING = PG_READ_AHEAD + 1;
+    // The MFMA phase's wave issues ahead of its SIMD partner's memory phase.
+    __builtin_amdgcn_s_setprio(1);
     half8v ring[RING];
     auto read_op = [&](int i) __attribute__((always_inline)) -> half8v {
       return xfrag[((i & 3) * 32 * PG_XROW + (i >> 2) * 8) / 8];
@@ -292,6 +294,7 @@ void pingpong_gemm_kernel(GemmGroup gp) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int m = 0; m < 4; ++m) asm volatile("" ::"v"(acc[t][m]));
+    __builtin_amdgcn_s_setprio(0);
   };
 
   // The barrier is written out (s_barrier after lgkmcnt(0)) so that the compiler
