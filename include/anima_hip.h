@@ -116,8 +116,8 @@ typedef struct anima_attention_config {
   int32_t backend;        /* anima_attention_backend */
   int32_t layout;         /* anima_layout default of encode() */
   int64_t token_stride;   /* half elements per token row for TOKEN_MAJOR */
-  int32_t flash_rows;     /* query rows per flash workgroup: 0 = auto (256 when that grid
-                             still covers every CU, else 128), 128 or 256 */
+  int32_t flash_rows;     /* query rows per flash workgroup: 0 = auto (256 whenever 64 key
+                             rows span < 2 GiB, else 128), 128 or 256 */
 } anima_attention_config;
 
 typedef struct anima_attention anima_attention;
