@@ -526,12 +526,11 @@ int flash_kv_splits(const FlashParams& p, int D, int batch, int flash_rows) {
   return splits >= 2 ? splits : 1;
 }
 
-// Key-split workspace: the partial rows (rows x D: fp16 normalised rows from the 256-row
-// kernel; fp32 unnormalised rows from the head-dim-384 kernel, where fp16 rows measured
-// no faster), padded to 256 bytes, then the fp32 (max, sum) pair of each row.
+// Key-split workspace: the partial rows (rows x D fp16 normalised rows), padded to 256
+// bytes, then the fp32 (max, sum) pair of each row.
 int64_t flash_split_o_bytes(const FlashParams& p, int D, int batch, int splits) {
   const int64_t rows = checked_product({(int64_t)splits, (int64_t)batch, (int64_t)p.H, (int64_t)p.Sq}, "attention");
-  return (checked_product({rows, (int64_t)D, D == 384 ? 4 : 2}, "attention") + 255) / 256 * 256;
+  return (checked_product({rows, (int64_t)D, 2}, "attention") + 255) / 256 * 256;
 }
 
 int64_t flash_split_bytes(const FlashParams& p, int D, int batch, int splits) {

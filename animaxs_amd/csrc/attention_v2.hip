@@ -475,9 +475,8 @@ void flash_attention_v2_kernel(FlashParams p) {
 }
 
 // Merge of the key splits: O = sum_s w_s O_s / sum_s w_s l_s with w_s = 2^(m_s - max m).
-// The 256-row kernel stores O_s as l_s * Ohat_s with Ohat_s its fp16 normalised row; the
-// head-dim-384 kernel stores O_s itself in fp32.  Thread t of a row handles columns
-// 8t .. 8t+7.
+// The kernels store O_s as l_s * Ohat_s with Ohat_s its fp16 normalised row.  Thread t
+// of a row handles columns 8t .. 8t+7.
 template <int D>
 __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p, int64_t rows) {
   constexpr int TPR = D / 8;
@@ -498,19 +497,9 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p, int64
     const float w = ms == -INFINITY ? 0.f : fast_exp2(ms - mmax);
     const float wl = w * p.part_ml[(s * rows + row) * 2 + 1];
     l += wl;
-    if constexpr (D == 384) {
-      const float* po = static_cast<const float*>(p.part_o) + (s * rows + row) * D + 8 * t;
-      const floatx4 a = *reinterpret_cast<const floatx4*>(po), c = *reinterpret_cast<const floatx4*>(po + 4);
+    const half8v a = *reinterpret_cast<const half8v*>(static_cast<const half_t*>(p.part_o) + (s * rows + row) * D + 8 * t);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[e] = fmaf(w, a[e], acc[e]);
-        acc[4 + e] = fmaf(w, c[e], acc[4 + e]);
-      }
-    } else {
-      const half8v a = *reinterpret_cast<const half8v*>(static_cast<const half_t*>(p.part_o) + (s * rows + row) * D + 8 * t);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] = fmaf(wl, (float)a[e], acc[e]);
-    }
+    for (int e = 0; e < 8; ++e) acc[e] = fmaf(wl, (float)a[e], acc[e]);
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   half8v o;

@@ -244,31 +244,40 @@ void flash_attention_wide_kernel(FlashParams p) {
   }
 
   const float l_tot = xlane32_sum(lrow);
-  if (p.kv_splits > 1) {
-    if (qi < p.Sq) {
-      const int64_t row = (((int64_t)split * p.nbatch + b) * p.H + head) * p.Sq + qi;
-      float* po = static_cast<float*>(p.part_o) + row * D + DH * dh;
-#pragma unroll
-      for (int c = 0; c < OB; ++c)
-#pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4)
-          *reinterpret_cast<floatx4*>(po + 32 * c + 8 * e4 + 4 * hh) =
-              floatx4{acc[c][4 * e4], acc[c][4 * e4 + 1], acc[c][4 * e4 + 2], acc[c][4 * e4 + 3]};
-      if (hh == 0 && dh == 0) *reinterpret_cast<float2*>(p.part_ml + row * 2) = make_float2(m_run, l_tot);
-    }
-    return;
+  // A key split stores its normalised rows O_s / l_s in fp16 (the same whole-row path as
+  // O, below) beside the fp32 (max, sum) pair of each row; the merge weighs them by l_s.
+  if (p.kv_splits > 1 && qi < p.Sq && hh == 0 && dh == 0) {
+    const int64_t row = (((int64_t)split * p.nbatch + b) * p.H + head) * p.Sq + qi;
+    *reinterpret_cast<float2*>(p.part_ml + row * 2) = make_float2(m_run, l_tot);
   }
+  // The fp16 rows go through LDS so that every global store is a 16-byte piece of a
+  // 384-byte half row (24 lanes per row); the register layout would scatter each store
+  // instruction over 32 rows.  Wave w stages its 32 rows x 192 columns in its own slice
+  // of the K/V stages, which every wave has finished reading after this barrier.
+  constexpr int OPITCH = DH + 8;           // halfs per staged row
+  constexpr int OCH = DH / 8;              // 16-byte chunks per staged row
+  static_assert(FW_WAVES * 32 * OPITCH <= 2 * STAGE, "staged rows fit the K/V stages");
+  static_assert((32 * OCH) % 64 == 0, "whole store instructions");
+  barrier();
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (qi < p.Sq) {
-    half_t* op = p.o + (int64_t)b * p.o_batch + (int64_t)head * p.o_head + (int64_t)qi * p.o_tok + DH * dh;
+  half_t* const ost = smem + wave * 32 * OPITCH;
 #pragma unroll
-    for (int c = 0; c < OB; ++c)
+  for (int c = 0; c < OB; ++c)
 #pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        const half4v val = {(half_t)(acc[c][4 * e4 + 0] * inv), (half_t)(acc[c][4 * e4 + 1] * inv),
-                            (half_t)(acc[c][4 * e4 + 2] * inv), (half_t)(acc[c][4 * e4 + 3] * inv)};
-        *reinterpret_cast<half4v*>(op + 32 * c + 8 * e4 + 4 * hh) = val;
-      }
+    for (int e4 = 0; e4 < 4; ++e4) {
+      const half4v val = {(half_t)(acc[c][4 * e4 + 0] * inv), (half_t)(acc[c][4 * e4 + 1] * inv),
+                          (half_t)(acc[c][4 * e4 + 2] * inv), (half_t)(acc[c][4 * e4 + 3] * inv)};
+      *reinterpret_cast<half4v*>(ost + c32 * OPITCH + 32 * c + 8 * e4 + 4 * hh) = val;
+    }
+  half_t* const obase = p.kv_splits > 1
+                            ? static_cast<half_t*>(p.part_o) + (((int64_t)split * p.nbatch + b) * p.H + head) * p.Sq * D
+                            : p.o + (int64_t)b * p.o_batch + (int64_t)head * p.o_head;
+  const int64_t otok = p.kv_splits > 1 ? D : p.o_tok;
+#pragma unroll
+  for (int i = 0; i < 32 * OCH / 64; ++i) {
+    const int n = i * 64 + lane, r = n / OCH, ch = n % OCH;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(ost + r * OPITCH + ch * 8);
+    if (wq0 + r < p.Sq) *reinterpret_cast<u32x4*>(obase + (int64_t)(wq0 + r) * otok + DH * dh + ch * 8) = v;
   }
 }
 
