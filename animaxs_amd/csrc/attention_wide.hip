@@ -5,19 +5,26 @@
 // v_mfma_f32_32x32x16_f16, fp32 online softmax in base 2 with the lazy running max,
 // fp16 P, O^T += V^T P^T; a Q RMSNorm / RoPE runs in the prologue kernel), organised so
 // that a 384-wide O fits the registers:
-//   * 8 waves, 2 per SIMD, 128 query rows per workgroup.  Waves w and w+4 (one SIMD) are
-//     a pair over the same 32 query rows; wave w owns O columns 0-191 and wave w+4 columns
+//   * 8 waves, 2 per SIMD, 128 query rows per workgroup.  Waves 2p and 2p+1 are a pair
+//     over query rows 32p .. 32p+31; wave 2p owns O columns 0-191 and wave 2p+1 columns
 //     192-383 (6 accumulator tiles each), and each holds the Q fragments of its half.
 //   * Per 32-key tile each wave of a pair computes the partial S^T over its 192 columns
-//     (12 MFMAs), the pair swaps partial sums through LDS and both add them (a + b equals
-//     b + a, so both waves hold the same scores and take the same softmax steps), then
-//     each wave accumulates its half of O^T += V^T P^T (12 MFMAs).
-//   * K and V tiles are register-staged copies into two LDS stages (16 threads move one
-//     key row's 768 bytes, 256 contiguous bytes per instruction); each tile is read through
-//     one buffer descriptor sized to the last key row in use, so rows past it read as
-//     zeros without touching memory.  K rows are padded to D+8 halfs and V rows to D+32
-//     (the bank-conflict-free pitches of the 128-wide kernel), and V^T fragments come
-//     straight from the row-major V tile with ds_read_b64_tr_b16.
+//     (12 MFMAs) and writes it to LDS; after the next barrier both waves add the
+//     partner's half (a + b equals b + a, so both hold the same scores and take the same
+//     softmax steps), then each accumulates its half of O^T += V^T P^T (12 MFMAs).
+//   * Waves 0-3 (group 0) and 4-7 (group 1) put one wave of each group on every SIMD and
+//     run a phase apart: while one group issues its MFMAs (M phase: PV of tile j-1, then
+//     the partial QK^T of tile j) the other runs the softmax of its previous tile and the
+//     tile copies (X phase), and the two swap at every barrier.  A pair lives in one
+//     group, so its score exchange needs no extra synchronisation.
+//   * K and V tiles have two LDS stages each.  Group 1 copies K tiles and group 0 V
+//     tiles, each in its X phase: registers take tile loads two phases before they are
+//     written to LDS (8 threads move one key row's 768 bytes, 128 contiguous bytes per
+//     instruction), and each tile is read through one buffer descriptor sized to the
+//     last key row in use, so rows past it read as zeros without touching memory.  K
+//     rows are padded to D+8 halfs and V rows to D+32 (the bank-conflict-free pitches of
+//     the 128-wide kernel); V^T fragments come straight from the row-major V tile with
+//     ds_read_b64_tr_b16.
 //   * One query head has only ceil(Sq/128) workgroups, so the keys are split across
 //     workgroups (flash_kv_splits) and flash_combine_kernel merges the partial rows.
 //     Query tiles are the fastest grid index, so the workgroups of one XCD share one key
@@ -40,17 +47,19 @@ void flash_attention_wide_kernel(FlashParams p) {
   constexpr int OB = DH / 32;            // 32-wide O blocks per wave
   constexpr int KROW = D + 8, VROW = D + 32;
   constexpr int KTILE = FW_BN * KROW, VTILE = FW_BN * VROW;   // halfs
-  constexpr int STAGE = KTILE + VTILE;
-  constexpr int TPR = FW_NT / FW_BN;     // copy threads per key row (16)
-  constexpr int CPR = D / 8 / TPR;       // 16-byte chunks per copy thread and row (3)
+  constexpr int VBASE = 2 * KTILE;       // K stages 0-1, then V stages 0-1
+  constexpr int GT = FW_NT / 2;          // threads per wave group
+  constexpr int TPR = GT / FW_BN;        // copy threads per key row (8)
+  constexpr int CPR = D / 8 / TPR;       // 16-byte chunks per copy thread (6)
   constexpr int XBUF = 64 * 16;          // floats of one wave's partial scores
   static_assert(D % (8 * TPR) == 0 && DH % 32 == 0, "tile splits evenly");
-  __shared__ __attribute__((aligned(1024))) half_t smem[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) half_t smem[2 * KTILE + 2 * VTILE];
   __shared__ __attribute__((aligned(16))) float xbuf[FW_WAVES * XBUF];
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = tid >> 6;
-  const int pr = wave & 3, dh = wave >> 2;       // query block, column half
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int group = wave >> 2;
+  const int pr = wave >> 1, dh = wave & 1;       // query block, column half
   const int c32 = lane & 31, hh = lane >> 5;
   const int jj = lane & 15, gg = lane >> 4;
 
@@ -82,38 +91,34 @@ void flash_attention_wide_kernel(FlashParams p) {
   if (p.causal) kend = min(kend, q0 + FLASH_WIDE_ROWS);
   const int ntiles = (kend + FW_BN - 1) / FW_BN;
 
-  const half_t* kbase = p.k + (int64_t)b * p.k_batch + (int64_t)kvh * p.k_head + (int64_t)kofs * p.k_tok;
-  const half_t* vbase = p.v + (int64_t)b * p.v_batch + (int64_t)kvh * p.v_head + (int64_t)kofs * p.v_tok;
-
-  // Tile copies: thread t moves row t/16 of the tile, 16-byte chunks (t%16) + 16r for
-  // r < CPR, of K and of V.
-  const int crow = tid / TPR, cc = tid % TPR;
-  const uint32_t ktok2 = (uint32_t)p.k_tok * 2u, vtok2 = (uint32_t)p.v_tok * 2u;
-  const uint32_t goff_k = (uint32_t)crow * ktok2 + (uint32_t)cc * 16u;
-  const uint32_t goff_v = (uint32_t)crow * vtok2 + (uint32_t)cc * 16u;
-  const int loff_k = crow * KROW + cc * 8, loff_v = KTILE + crow * VROW + cc * 8;   // halfs within a stage
-  const int64_t kstep = (int64_t)FW_BN * ktok2, vstep = (int64_t)FW_BN * vtok2;
-  const int64_t kbytes = kend > 0 ? (int64_t)(kend - 1) * ktok2 + D * 2 : 0;
-  const int64_t vbytes = kend > 0 ? (int64_t)(kend - 1) * vtok2 + D * 2 : 0;
-  auto clamp_bytes = [](int64_t rem) __attribute__((always_inline)) -> int {
-    return rem <= 0 ? 0 : (rem >= 0x7fffffff ? 0x7fffffff : (int)rem);
+  // Tile copies: group 1 moves K tiles, group 0 V tiles.  Thread t of the group moves
+  // row t/8 of the tile, 16-byte chunks (t%8) + 8r for r < CPR.
+  const int gt = tid & (GT - 1);
+  const int crow = gt / TPR, cc = gt % TPR;
+  const half_t* const cbase =
+      group ? p.k + (int64_t)b * p.k_batch + (int64_t)kvh * p.k_head + (int64_t)kofs * p.k_tok
+            : p.v + (int64_t)b * p.v_batch + (int64_t)kvh * p.v_head + (int64_t)kofs * p.v_tok;
+  const uint32_t ctok2 = (uint32_t)(group ? p.k_tok : p.v_tok) * 2u;
+  const uint32_t goff = (uint32_t)crow * ctok2 + (uint32_t)cc * 16u;
+  const int64_t cstep = (int64_t)FW_BN * ctok2;
+  const int64_t cbytes = kend > 0 ? (int64_t)(kend - 1) * ctok2 + D * 2 : 0;
+  const int crowp = group ? KROW : VROW;
+  const int loff = (group ? 0 : VBASE) + crow * crowp + cc * 8;   // halfs within stage 0
+  const int cstage = group ? KTILE : VTILE;                      // halfs between stages
+  u32x4 stg[CPR];
+  auto load_copy = [&](int j) __attribute__((always_inline)) {
+    // Chunk r goes through its own descriptor, based 16 * TPR * r bytes further on, so
+    // that every load shares the one lane offset goff.
+    const char* t = reinterpret_cast<const char*>(cbase) + j * cstep;
+    const int64_t rem = cbytes - j * cstep;
+    const int n = rem <= 0 ? 0 : (rem >= 0x7fffffff ? 0x7fffffff : (int)rem);
+#pragma unroll
+    for (int r = 0; r < CPR; ++r) stg[r] = load16_bounded(t + 16 * TPR * r, max(n - 16 * TPR * r, 0), goff);
   };
-  u32x4 stg[2 * CPR];
-  auto load_tile = [&](int j) __attribute__((always_inline)) {
-    const char* kt = reinterpret_cast<const char*>(kbase) + j * kstep;
-    const char* vt = reinterpret_cast<const char*>(vbase) + j * vstep;
-    const int nk = clamp_bytes(kbytes - j * kstep), nv = clamp_bytes(vbytes - j * vstep);
+  auto store_copy = [&](int s) __attribute__((always_inline)) {
+    half_t* st = smem + loff + s * cstage;
 #pragma unroll
-    for (int r = 0; r < CPR; ++r) stg[r] = load16_bounded(kt, nk, goff_k + 16u * TPR * r);
-#pragma unroll
-    for (int r = 0; r < CPR; ++r) stg[CPR + r] = load16_bounded(vt, nv, goff_v + 16u * TPR * r);
-  };
-  auto store_tile = [&](int s) __attribute__((always_inline)) {
-    half_t* st = smem + s * STAGE;
-#pragma unroll
-    for (int r = 0; r < CPR; ++r) *reinterpret_cast<u32x4*>(st + loff_k + 8 * TPR * r) = stg[r];
-#pragma unroll
-    for (int r = 0; r < CPR; ++r) *reinterpret_cast<u32x4*>(st + loff_v + 8 * TPR * r) = stg[CPR + r];
+    for (int r = 0; r < CPR; ++r) *reinterpret_cast<u32x4*>(st + 8 * TPR * r) = stg[r];
   };
 
   // Q fragments of this wave's column half (B operand of S^T): lane holds
@@ -137,16 +142,17 @@ void flash_attention_wide_kernel(FlashParams p) {
   typedef __attribute__((address_space(3))) half8v lds_half8v;
   typedef __attribute__((address_space(3))) short4v lds_short4v;
   const int kfrag = c32 * KROW + DH * dh + hh * 8;
-  const int vfrag = KTILE + (4 * hh + (jj >> 2)) * VROW + DH * dh + 16 * (gg & 1) + 4 * (jj & 3);
+  const int vfrag = VBASE + (4 * hh + (jj >> 2)) * VROW + DH * dh + 16 * (gg & 1) + 4 * (jj & 3);
   float* const xmine = xbuf + wave * XBUF + lane * 16;
-  const float* const xpeer = xbuf + (wave ^ 4) * XBUF + lane * 16;
+  const float* const xpeer = xbuf + (wave ^ 1) * XBUF + lane * 16;
 
-  // V^T fragment (c, u): lane (d, hh) holds V[16u + 8(i/4) + 4hh + i%4][DH*dh + 32c + d].
-  auto vfrag_read = [&](int sbase, int u, int c) __attribute__((always_inline)) -> half8v {
-    lds_short4v* vs = (lds_short4v*)(smem + sbase + vfrag);
+  // V^T fragment (c, u) of V stage vs: lane (d, hh) holds
+  // V[16u + 8(i/4) + 4hh + i%4][DH*dh + 32c + d].
+  auto vfrag_read = [&](int vs, int u, int c) __attribute__((always_inline)) -> half8v {
+    lds_short4v* vp = (lds_short4v*)(smem + vs * VTILE + vfrag);
     const int off = 16 * u * VROW + 32 * c;
-    const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vs + off / 4);
-    const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vs + (off + 8 * VROW) / 4);
+    const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vp + off / 4);
+    const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vp + (off + 8 * VROW) / 4);
     const half4v lo_h = __builtin_bit_cast(half4v, lo), hi_h = __builtin_bit_cast(half4v, hi);
     return half8v{lo_h[0], lo_h[1], lo_h[2], lo_h[3], hi_h[0], hi_h[1], hi_h[2], hi_h[3]};
   };
@@ -173,19 +179,24 @@ void flash_attention_wide_kernel(FlashParams p) {
     return (ls[0] + ls[1]) + (ls[2] + ls[3]);
   };
 
-  if (ntiles > 0) {
-    load_tile(0);
-    store_tile(0);
-    load_tile(1);
-    for (int j = 0; j < ntiles; ++j) {
-      const int st = (j & 1) * STAGE;
-      // Tile j is resident and every wave has finished tile j-1: its stage takes tile
-      // j+1, the staging registers the loads of tile j+2, and xbuf is free again.
-      barrier();
-      store_tile((j + 1) & 1);
-      load_tile(j + 2);
-      // Partial S^T over this wave's columns.
-      const lds_half8v* ks = (const lds_half8v*)(smem + st + kfrag);
+  // M phase of tile j: O^T += V^T P^T of tile j-1 (P is free after it), then this wave's
+  // partial S^T of tile j into its exchange buffer.  (Interleaving the two products'
+  // MFMAs with a deeper fragment read-ahead shortened this phase but lengthened the other
+  // group's X phase by more: the two phases share the LDS, and it is the limit here.)
+  auto m_phase = [&](int j) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_setprio(1);
+    if (j > 0) {
+      const int vs = (j - 1) & 1;
+      half8v vr[2];
+      vr[0] = vfrag_read(vs, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 2 * OB; ++i) {
+        if (i + 1 < 2 * OB) vr[(i + 1) & 1] = vfrag_read(vs, (i + 1) / OB, (i + 1) % OB);
+        acc[i % OB] = mfma32(vr[i & 1], P[i / OB], acc[i % OB]);
+      }
+    }
+    if (j < ntiles) {
+      const lds_half8v* ks = (const lds_half8v*)(smem + (j & 1) * KTILE + kfrag);
       half8v kr[2];
       kr[0] = ks[0];
 #pragma unroll
@@ -196,15 +207,27 @@ void flash_attention_wide_kernel(FlashParams p) {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         *reinterpret_cast<floatx4*>(xmine + 4 * q) = floatx4{S[4 * q], S[4 * q + 1], S[4 * q + 2], S[4 * q + 3]};
-      barrier();
+    }
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  // X phase of tile j: the full scores (own partial + the partner's), masking, the
+  // exponentials against the running max (the exact path, with the row max and the
+  // O / row-sum rescale, when a lane's share exceeds the lazy bound), then this group's
+  // tile copy: the tile loaded two phases ago goes to LDS and the next one is loaded.
+  auto x_phase = [&](int j) __attribute__((always_inline)) {
+    const int cj = group ? j + 2 : j;
+    if (cj < ntiles) {
+      store_copy(cj & 1);
+      load_copy(cj + 1);
+    }
+    if (j >= 0 && j < ntiles) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const floatx4 o = *reinterpret_cast<const floatx4*>(xpeer + 4 * q);
 #pragma unroll
         for (int e = 0; e < 4; ++e) S[4 * q + e] += o[e];
       }
-      // Masking, then the exponentials against the running max; the exact path (row
-      // max, O / row-sum rescale) when a lane's share exceeds the lazy bound.
       const int k0 = j * FW_BN;
       if ((k0 + FW_BN > kv_len) || (p.causal && k0 + FW_BN - 1 > wq0)) {
 #pragma unroll
@@ -231,17 +254,37 @@ void flash_attention_wide_kernel(FlashParams p) {
         tsum = exps((m_run == -INFINITY) ? 0.f : m_run);
       }
       lrow += tsum;
-      // O^T += V^T P^T over this wave's columns.
-      half8v vr[2];
-      vr[0] = vfrag_read(st, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 2 * OB; ++i) {
-        if (i + 1 < 2 * OB) vr[(i + 1) & 1] = vfrag_read(st, (i + 1) / OB, (i + 1) % OB);
-        acc[i % OB] = mfma32(vr[i & 1], P[i / OB], acc[i % OB]);
-      }
     }
-    wait_vmcnt_imm<0>();   // staged loads past the end (no memory traffic)
+    // Group 0 (X phase of tile j) stores V tile j and loads V tile j+1; group 1 (X phase
+    // of tile j, one phase later in the schedule) stores K tile j+2 and loads K tile j+3.
+  };
+
+  // Prologue: group 1 brings K tile 0 to LDS and loads K tile 1, group 0 loads V tile 0.
+  if (group) {
+    load_copy(0);
+    store_copy(0);
+    load_copy(1);
+  } else {
+    load_copy(0);
   }
+  barrier();
+  // Group 1 runs one phase behind group 0: it starts with the copy step of X(-1), so in
+  // every later phase one group issues MFMAs while the other runs its X phase.  Both
+  // groups then run the same loop, and every wave passes 2 (ntiles + 1) barriers.
+  if (group) {
+    x_phase(-1);
+    barrier();
+  }
+  for (int t = 0; t < ntiles; ++t) {
+    m_phase(t);
+    barrier();
+    x_phase(t);
+    barrier();
+  }
+  m_phase(ntiles);   // PV of the last tile
+  barrier();
+  if (!group) barrier();
+  wait_vmcnt_imm<0>();   // tile loads past the end (no memory traffic)
 
   const float l_tot = xlane32_sum(lrow);
   // A key split stores its normalised rows O_s / l_s in fp16 (the same whole-row path as
@@ -253,12 +296,11 @@ void flash_attention_wide_kernel(FlashParams p) {
   // The fp16 rows go through LDS so that every global store is a 16-byte piece of a
   // 384-byte half row (24 lanes per row); the register layout would scatter each store
   // instruction over 32 rows.  Wave w stages its 32 rows x 192 columns in its own slice
-  // of the K/V stages, which every wave has finished reading after this barrier.
+  // of the K/V stages, which every wave finished reading before the loop's last barrier.
   constexpr int OPITCH = DH + 8;           // halfs per staged row
   constexpr int OCH = DH / 8;              // 16-byte chunks per staged row
-  static_assert(FW_WAVES * 32 * OPITCH <= 2 * STAGE, "staged rows fit the K/V stages");
+  static_assert(FW_WAVES * 32 * OPITCH <= 2 * KTILE + 2 * VTILE, "staged rows fit the K/V stages");
   static_assert((32 * OCH) % 64 == 0, "whole store instructions");
-  barrier();
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   half_t* const ost = smem + wave * 32 * OPITCH;
 #pragma unroll
@@ -283,6 +325,8 @@ void flash_attention_wide_kernel(FlashParams p) {
 
 void launch_flash_wide(const FlashParams& p, int D, dim3 grid, hipStream_t stream) {
   if (D != 384) fail(ANIMA_E_UNSUPPORTED, "wide flash attention requires head_dim 384");
+  const int64_t want = (int64_t)p.q_tiles * p.H * p.nbatch * (p.kv_splits > 1 ? p.kv_splits : 1);
+  if (want != (int64_t)grid.x) fail(ANIMA_E_INVALID_SHAPE, "wide flash attention grid does not match its tiles");
   hipLaunchKernelGGL(flash_attention_wide_kernel<384>, grid, dim3(FW_NT), 0, stream, p);
   ANIMA_HIP(hipGetLastError());
 }
