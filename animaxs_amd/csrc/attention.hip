@@ -508,7 +508,6 @@ constexpr int64_t F2_MIN_BLOCKS = 256;
 // (non-causal, no per-sequence key lengths, automatic row choice): enough splits to
 // reach F2_MIN_BLOCKS workgroups, each of at least F2_MIN_SPLIT_KEYS keys.
 constexpr int F2_MIN_SPLIT_KEYS = 256;
-constexpr int F2_MAX_SPLITS = 8;
 
 int flash_kv_splits(const FlashParams& p, int D, int batch, int flash_rows) {
   if (p.causal || p.key_lengths_dev || p.use_host_lengths) return 1;
@@ -521,7 +520,7 @@ int flash_kv_splits(const FlashParams& p, int D, int batch, int flash_rows) {
   if (t256 >= F2_MIN_BLOCKS || t256 <= 0) return 1;
   if (64 * std::max(p.k_tok, p.v_tok) * (int64_t)sizeof(half_t) >= ((int64_t)1 << 31)) return 1;
   int splits = (int)((F2_MIN_BLOCKS + t256 - 1) / t256);
-  splits = std::min<int>(splits, F2_MAX_SPLITS);
+  splits = std::min<int>(splits, FLASH_MAX_SPLITS);
   splits = std::min<int>(splits, p.Sk / F2_MIN_SPLIT_KEYS);
   return splits >= 2 ? splits : 1;
 }

@@ -60,6 +60,8 @@ constexpr int FLASH_V2_ROWS = 256;
 // Wide-head (head_dim 384) flash kernel (attention_wide.hip): 128 query rows per
 // workgroup, p.q_tiles counts 128-row tiles.
 constexpr int FLASH_WIDE_ROWS = 128;
+// Most key splits of one attention call (flash_kv_splits); the merge holds them all.
+constexpr int FLASH_MAX_SPLITS = 8;
 void launch_flash_wide(const FlashParams& p, int D, dim3 grid, hipStream_t stream);
 void launch_flash_v2(const FlashParams& p, int D, dim3 grid, hipStream_t stream);
 void launch_flash_combine(const FlashParams& p, int D, int batch, hipStream_t stream);

@@ -476,7 +476,8 @@ void flash_attention_v2_kernel(FlashParams p) {
 
 // Merge of the key splits: O = sum_s w_s O_s / sum_s w_s l_s with w_s = 2^(m_s - max m).
 // The kernels store O_s as l_s * Ohat_s with Ohat_s its fp16 normalised row.  Thread t
-// of a row handles columns 8t .. 8t+7.
+// of a row handles columns 8t .. 8t+7; it issues every split's loads before the first
+// use, so all of them are in flight at once.
 template <int D>
 __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p, int64_t rows) {
   constexpr int TPR = D / 8;
@@ -488,19 +489,30 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p, int64
   const int qi = (int)(row % p.Sq);
   const int head = (int)((row / p.Sq) % p.H);
   const int b = (int)(row / ((int64_t)p.Sq * p.H));
+  const int ns = p.kv_splits;
+  float2 ml[FLASH_MAX_SPLITS];
+  half8v a[FLASH_MAX_SPLITS];
+#pragma unroll
+  for (int s = 0; s < FLASH_MAX_SPLITS; ++s)
+    if (s < ns) {
+      ml[s] = *reinterpret_cast<const float2*>(p.part_ml + (s * rows + row) * 2);
+      a[s] = *reinterpret_cast<const half8v*>(static_cast<const half_t*>(p.part_o) + (s * rows + row) * D + 8 * t);
+    }
   float mmax = -INFINITY;
-  for (int s = 0; s < p.kv_splits; ++s) mmax = fmaxf(mmax, p.part_ml[(s * rows + row) * 2]);
+#pragma unroll
+  for (int s = 0; s < FLASH_MAX_SPLITS; ++s)
+    if (s < ns) mmax = fmaxf(mmax, ml[s].x);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float l = 0.f;
-  for (int s = 0; s < p.kv_splits; ++s) {
-    const float ms = p.part_ml[(s * rows + row) * 2];
-    const float w = ms == -INFINITY ? 0.f : fast_exp2(ms - mmax);
-    const float wl = w * p.part_ml[(s * rows + row) * 2 + 1];
-    l += wl;
-    const half8v a = *reinterpret_cast<const half8v*>(static_cast<const half_t*>(p.part_o) + (s * rows + row) * D + 8 * t);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = fmaf(wl, (float)a[e], acc[e]);
-  }
+  for (int s = 0; s < FLASH_MAX_SPLITS; ++s)
+    if (s < ns) {
+      const float w = ml[s].x == -INFINITY ? 0.f : fast_exp2(ml[s].x - mmax);
+      const float wl = w * ml[s].y;
+      l += wl;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(wl, (float)a[s][e], acc[e]);
+    }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   half8v o;
 #pragma unroll
@@ -510,6 +522,7 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p, int64
 }
 
 void launch_flash_combine(const FlashParams& p, int D, int batch, hipStream_t stream) {
+  if (p.kv_splits < 2 || p.kv_splits > FLASH_MAX_SPLITS) fail(ANIMA_E_INVALID_ARGUMENT, "flash key splits out of range");
   const int64_t rows = (int64_t)batch * p.H * p.Sq;
   const int rpb = 256 / (D / 8);
   const int64_t blocks = (rows + rpb - 1) / rpb;
