@@ -207,7 +207,7 @@ def test_flash_matches_oracle_ragged(ctx, D, Sq, Sk, causal):
 def test_flash_key_splits(ctx, D, B, Sq, Sk):
     """Short query sequences over long key sequences: the 256-row kernel splits the keys across
     workgroups (last split possibly empty for Sk=2056 with 8 splits) and a second kernel merges the
-    fp32 partial rows; token-major layout, batch > 1."""
+    fp16 normalised partial rows by their fp32 (max, sum) pairs; token-major layout, batch > 1."""
     g = torch.Generator().manual_seed(B * Sq + Sk + D)
     H = 4
     q = torch.randn(B, Sq, H, D, generator=g).half()
@@ -320,10 +320,12 @@ def test_vae_attention_head_dim_384_matches_oracle(ctx):
 
 @pytest.mark.parametrize("B,H,Sq,Sk,causal,lengths", [(1, 1, 300, 777, False, None), (2, 2, 129, 64, False, None),
                                                       (1, 3, 260, 260, True, None), (2, 1, 200, 450, False, [37, 450]),
-                                                      (1, 1, 1, 33, False, None), (1, 2, 5000, 40, False, None)])
+                                                      (1, 1, 1, 33, False, None), (1, 2, 5000, 40, False, None),
+                                                      (1, 1, 128, 2049, False, None)])
 def test_wide_flash_head_dim_384_ragged(ctx, B, H, Sq, Sk, causal, lengths):
     """Ragged tiles, batch and heads, causal rows, per-sequence key lengths (no key splits) and the
-    split path (300 x 777: 3 splits); large logits so the lazy running max must rescale."""
+    split path (300 x 777: 3 splits; 128 x 2049: 8 splits of 320 keys, the last one empty); large
+    logits so the lazy running max must rescale."""
     D = 384
     g = torch.Generator().manual_seed(B * 100000 + H * 10000 + Sq + Sk)
     q = (torch.randn(B, Sq, H, D, generator=g) * 4.0).half()    # logits ~N(0, 16^2): the running max
