@@ -66,6 +66,15 @@ def test_noalloc_equals_encode_on_consecutive_calls(ctx):
                        layout=("tokenMajor", 2048))
     assert torch.equal(got4.view(torch.int16), ref4.view(torch.int16))
 
+    # 4) the head-dim-384 kernel (VAE mid-block shape): 8 key splits, whose fp16 partial rows
+    #    (24 MiB) and (max, sum) pairs take the static array.
+    g = torch.Generator().manual_seed(384)
+    q8, k8, v8 = (dev(torch.randn(4096, 384, generator=g).half()) for _ in range(3))
+    ref8, got8 = _pair(ctx, "D384 key splits", query=q8, key=k8, value=v8, heads=1, query_count=4096,
+                       key_count=4096, head_dim=384, out_shape=(4096, 384), layout="headMajor")
+    assert torch.isfinite(got8.float()).all()
+    assert torch.equal(got8.view(torch.int16), ref8.view(torch.int16))
+
 
 def test_noalloc_refuses_a_workspace_beyond_its_array(ctx):
     """K prologue rows of 16448 tokens x 16 heads x 128 = 64.25 MiB > 64 MiB."""
