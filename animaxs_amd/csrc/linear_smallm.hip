@@ -122,7 +122,9 @@ __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kerne
   half_t* z_lds = s_lds + 16 * R * p.groups;
   const int nrows = min(16 * R, p.N - n0);
   const int nparam = nrows * p.groups;
-  constexpr int PARAM_REGS = SM_PARAM_REGS;
+  // Scale/zero halfs per thread: 16R rows x K/64 groups over 64 x S threads, with
+  // S x NCH x NST chunks of 128 covering K, is at most ceil(R x NCH x NST / 2) per thread.
+  constexpr int PARAM_REGS = std::min(SM_PARAM_REGS, (R * NCH * NST + 1) / 2);
   half_t sreg[PARAM_REGS], zreg[PARAM_REGS];
   if constexpr (STORAGE != ANIMA_STORAGE_FP16) {
     const half_t* sbase = p.scale + (int64_t)n0 * p.groups;
