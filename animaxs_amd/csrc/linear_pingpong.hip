@@ -281,8 +281,6 @@ void pingpong_gemm_kernel(GemmGroup gp) {
       if (i + PG_READ_AHEAD < NOPS) ring[(i + PG_READ_AHEAD) % RING] = read_op(i + PG_READ_AHEAD);
 #pragma unroll
       for (int t = 0; t < 2; ++t) acc[t][i & 3] = mfma32(wf[t][i >> 2], ring[i % RING], acc[t][i & 3]);
-      // Steps 0-2 of the next block, one (row tile, step) every second op from op 4
-      // on: step s is last read by op 4s+3.
       // Steps 0-2 of the next block, half a (row tile, step) per op from op 4 on:
       // step s is last read by op 4s+3.
       if (i >= 4) dq_half(buf_c, ((i - 4) >> 1) & 1, (i - 4) >> 2, (i - 4) & 1);
