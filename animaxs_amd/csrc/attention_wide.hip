@@ -18,8 +18,8 @@
 //     tile copies (X phase), and the two swap at every barrier.  A pair lives in one
 //     group, so its score exchange needs no extra synchronisation.
 //   * K and V tiles have two LDS stages each.  Group 1 copies K tiles and group 0 V
-//     tiles, each in its X phase: registers take tile loads two phases before they are
-//     written to LDS (8 threads move one key row's 768 bytes, 128 contiguous bytes per
+//     tiles, each at the start of its X phase: registers take a tile's loads in the
+//     group's previous X phase, two phases before they are written to LDS (8 threads move one key row's 768 bytes, 128 contiguous bytes per
 //     instruction), and each tile is read through one buffer descriptor sized to the
 //     last key row in use, so rows past it read as zeros without touching memory.  K
 //     rows are padded to D+8 halfs and V rows to D+32 (the bank-conflict-free pitches of
@@ -211,10 +211,12 @@ void flash_attention_wide_kernel(FlashParams p) {
     __builtin_amdgcn_s_setprio(0);
   };
 
-  // X phase of tile j: the full scores (own partial + the partner's), masking, the
-  // exponentials against the running max (the exact path, with the row max and the
-  // O / row-sum rescale, when a lane's share exceeds the lazy bound), then this group's
-  // tile copy: the tile loaded two phases ago goes to LDS and the next one is loaded.
+  // X phase of tile j: first this group's tile copy (the tile loaded in its previous X
+  // phase goes to LDS and the next one is loaded), then the full scores (own partial +
+  // the partner's), masking and the exponentials against the running max (the exact
+  // path, with the row max and the O / row-sum rescale, when a lane's share exceeds the
+  // lazy bound).  Group 0 stores V tile j and loads V tile j+1; group 1 (one phase later
+  // in the schedule) stores K tile j+2 and loads K tile j+3.
   auto x_phase = [&](int j) __attribute__((always_inline)) {
     const int cj = group ? j + 2 : j;
     if (cj < ntiles) {
@@ -255,8 +257,6 @@ void flash_attention_wide_kernel(FlashParams p) {
       }
       lrow += tsum;
     }
-    // Group 0 (X phase of tile j) stores V tile j and loads V tile j+1; group 1 (X phase
-    // of tile j, one phase later in the schedule) stores K tile j+2 and loads K tile j+3.
   };
 
   // Prologue: group 1 brings K tile 0 to LDS and loads K tile 1, group 0 loads V tile 0.
