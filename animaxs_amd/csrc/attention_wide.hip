@@ -19,9 +19,10 @@
 //     group, so its score exchange needs no extra synchronisation.
 //   * K and V tiles have two LDS stages each.  Group 1 copies K tiles and group 0 V
 //     tiles, each at the start of its X phase: registers take a tile's loads in the
-//     group's previous X phase, two phases before they are written to LDS (8 threads move one key row's 768 bytes, 128 contiguous bytes per
-//     instruction), and each tile is read through one buffer descriptor sized to the
-//     last key row in use, so rows past it read as zeros without touching memory.  K
+//     group's previous X phase, two phases before they are written to LDS (8 threads
+//     move one key row's 768 bytes, 128 contiguous bytes per instruction), and each
+//     tile is read through one buffer descriptor sized to the last key row in use, so
+//     rows past it read as zeros without touching memory.  K
 //     rows are padded to D+8 halfs and V rows to D+32 (the bank-conflict-free pitches of
 //     the 128-wide kernel); V^T fragments come straight from the row-major V tile with
 //     ds_read_b64_tr_b16.
