@@ -203,11 +203,12 @@ def test_flash_matches_oracle_ragged(ctx, D, Sq, Sk, causal):
 
 
 @pytest.mark.parametrize("D", [64, 128])
-@pytest.mark.parametrize("B,Sq,Sk", [(2, 300, 2056), (1, 1024, 1024), (3, 64, 520), (1, 1, 4096)])
+@pytest.mark.parametrize("B,Sq,Sk", [(2, 300, 2056), (1, 1024, 1024), (3, 64, 1040), (1, 1, 4096)])
 def test_flash_key_splits(ctx, D, B, Sq, Sk):
     """Short query sequences over long key sequences: the 256-row kernel splits the keys across
-    workgroups (last split possibly empty for Sk=2056 with 8 splits) and a second kernel merges the
-    fp16 normalised partial rows by their fp32 (max, sum) pairs; token-major layout, batch > 1."""
+    workgroups (2 to 8 splits of at least 512 keys, the last one ragged: 2056 keys in 4 splits of
+    576, 1040 in 2 of 576) and a second kernel merges the fp16 normalised partial rows by their fp32
+    (max, sum) pairs; token-major layout, batch > 1."""
     g = torch.Generator().manual_seed(B * Sq + Sk + D)
     H = 4
     q = torch.randn(B, Sq, H, D, generator=g).half()
@@ -324,8 +325,8 @@ def test_vae_attention_head_dim_384_matches_oracle(ctx):
                                                       (1, 1, 128, 2049, False, None)])
 def test_wide_flash_head_dim_384_ragged(ctx, B, H, Sq, Sk, causal, lengths):
     """Ragged tiles, batch and heads, causal rows, per-sequence key lengths (no key splits) and the
-    split path (300 x 777: 3 splits; 128 x 2049: 8 splits of 320 keys, the last one empty); large
-    logits so the lazy running max must rescale."""
+    split path (128 x 2049: 4 splits of 576 keys, the last one ragged; 300 x 777 is too short to
+    split); large logits so the lazy running max must rescale."""
     D = 384
     g = torch.Generator().manual_seed(B * 100000 + H * 10000 + Sq + Sk)
     q = (torch.randn(B, Sq, H, D, generator=g) * 4.0).half()    # logits ~N(0, 16^2): the running max

@@ -47,7 +47,7 @@ def test_noalloc_equals_encode_on_consecutive_calls(ctx):
     assert torch.isfinite(got.float()).all()
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
 
-    # 2) smaller: S=1024 without a prologue takes four key splits; their partial rows now
+    # 2) smaller: S=1024 without a prologue takes two key splits; their partial rows now
     #    occupy the same static array from offset 0.
     d1 = inputs.self_attention(1)
     q1, k1, v1 = (dev(d1[n]) for n in "qkv")
