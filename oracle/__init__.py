@@ -65,7 +65,17 @@ PINNING = {
         "shift/scale outputs (detects a shift/scale swap and layout errors)"),
     "blocks.dit_block": (
         "composition of pinned parts following scripts/dit_block0_oracle.py:327-391; "
-        "zero-gate identity and zero-weight invariants; closed-form blocks (Q = K = 0 with identity "
-        "V/O/MLP projections; a 2x2 grid where only RoPE shapes the softmax) that reject swapped "
-        "shift/scale, another branch's gate, cross K/V from x and a missing Q or K RoPE"),
+        "zero-gate identity and zero-weight invariants; closed-form blocks against fp64 brute "
+        "force (Q = K = 0 with identity V/O/MLP projections; a 2x2 grid where only RoPE and the "
+        "distinct self Q/K norm weights shape the softmax; a cross branch with non-zero Q/K and "
+        "distinct cross norm weights) that reject swapped shift/scale, another branch's gate, "
+        "cross K/V from x, a missing Q or K RoPE, a Q or K normalised with the other's weight, "
+        "a dropped cross Q or K norm, the self weights in the cross branch and RoPE on cross Q/K"),
+    "blocks.qwen_layer": (
+        "composition following QwenEncoderMetal.swift:244-303 and "
+        "scripts/qwen_comfy_oracle.py:268-300; zero-projection, causality, padding and "
+        "sequence-independence invariants; a closed-form layer with W8 identity/doubling codes "
+        "(129 -> 1, 130 -> 2) against fp64 brute force that rejects a dropped Q or K norm, one "
+        "side using the other's norm weight, RoPE missing on Q or K, a missing causal mask, the "
+        "input-norm weight in the post-attention norm and gate/up swapped in the SwiGLU"),
 }

@@ -252,10 +252,12 @@ def test_block_closed_form_rope_changes_the_softmax():
     """2x2 grid.  Token rows share their first 1024 columns and permute their last 1024, so
     LayerNorm statistics (hence the first half of n1) are the same for every token.  Q and K
     both read the first half (heads 0-7 and 8-15 alike) through identity blocks, so Q = K is
-    one vector for every token; V = n1 differs per token in heads 8-15.  Without RoPE every
-    score is equal (uniform attention); with RoPE on Q only, a query row's scores are still
-    equal; with RoPE on K only they differ from RoPE on both.  The expected self branch is an
-    fp64 brute force with those roundings; cross and MLP gates are zeroed."""
+    one vector for every token before the norms; V = n1 differs per token in heads 8-15.  The
+    Q and K norm weights differ, so a self-attention Q normalised with the K weight (or the
+    other way round) changes every score.  Without RoPE every score of a query row is equal
+    (uniform attention); with RoPE on one side only they differ from RoPE on both.  The
+    expected self branch is an fp64 brute force with those roundings; cross and MLP gates
+    are zeroed."""
     S, T = 4, 2
     first_half = lambda r: np.where(r < 1024, r, r - 1024)  # noqa: E731
     d = _identity_block(S, T, self_q=_identity(DIM, DIM, first_half), self_k=_identity(DIM, DIM, first_half))
@@ -264,8 +266,8 @@ def test_block_closed_form_rope_changes_the_softmax():
     B = torch.randn(1024, generator=g) * 2
     x = torch.stack([torch.cat([A, B[torch.randperm(1024, generator=g)]]) for _ in range(S)])
     d["x"] = x
-    d["self_q_norm"] = torch.ones(HD).half()
-    d["self_k_norm"] = torch.ones(HD).half()
+    d["self_q_norm"] = (0.5 + torch.rand(HD, generator=g)).half()
+    d["self_k_norm"] = (0.5 + torch.rand(HD, generator=g)).half()
     for br in ("cross", "mlp"):
         w2 = d[f"mod_{br}_w2"].clone()
         w2[2 * DIM:] = 0
@@ -279,13 +281,17 @@ def test_block_closed_form_rope_changes_the_softmax():
     rope = d["rope"].double().numpy()                          # [4, 64, 2, 2]
     eps = d["eps"]
 
-    def branch(rope_q: bool, rope_k: bool):
+    wq = d["self_q_norm"].double().numpy()
+    wk = d["self_k_norm"].double().numpy()
+
+    def branch(rope_q: bool, rope_k: bool, q_w=wq, k_w=wk):
         out = np.zeros((S, DIM))
         for h in range(NH):
             src = n1[:, (h % 8) * HD:(h % 8 + 1) * HD]            # Q/K projection: first half
-            qn = np.stack([_h(src[t] / np.sqrt((src[t] ** 2).mean() + eps)).double().numpy() for t in range(S)])
-            q = np.stack([_h(_rope_rotate(qn[t], rope[t])).double().numpy() if rope_q else qn[t] for t in range(S)])
-            k = np.stack([_h(_rope_rotate(qn[t], rope[t])).double().numpy() if rope_k else qn[t] for t in range(S)])
+            qn = np.stack([src[t] / np.sqrt((src[t] ** 2).mean() + eps) * q_w for t in range(S)])
+            kn = np.stack([src[t] / np.sqrt((src[t] ** 2).mean() + eps) * k_w for t in range(S)])
+            q = np.stack([_hv(_rope_rotate(qn[t], rope[t]) if rope_q else qn[t]) for t in range(S)])
+            k = np.stack([_hv(_rope_rotate(kn[t], rope[t]) if rope_k else kn[t]) for t in range(S)])
             v = n1[:, h * HD:(h + 1) * HD]
             for t in range(S):
                 sc = np.array([q[t] @ k[j] for j in range(S)]) / math.sqrt(HD)
@@ -299,6 +305,189 @@ def test_block_closed_form_rope_changes_the_softmax():
     tol = 2e-3 * float(want.abs().max())
     err = float((got - want).abs().max())
     assert err <= tol, (err, tol)
-    for mistake in (branch(False, False), branch(True, False), branch(False, True)):
+    for mistake in (branch(False, False), branch(True, False), branch(False, True),
+                    branch(True, True, q_w=wk), branch(True, True, k_w=wq)):
         gap = float((mistake - x - want).abs().max())
         assert gap > 10 * tol, (gap, tol)
+
+
+# --------------------------------------------------------------------------------------
+# Closed forms that pin the Q/K norm wiring of both blocks and the Qwen layer's SwiGLU and
+# norm weights.  W8 codes with zero = -128*scale decode to (code - 128)*scale
+# (AnimaKernels.metal:43-66), so with scale 1 code 128 is an exact 0, 129 an exact 1 and
+# 130 an exact 2: diagonal code matrices are exact identity / doubling projections.  The
+# expected values are fp64 brute force over plain loops with the fp16 roundings at the
+# places the reference stores fp16 (QwenEncoderMetal.swift:244-303,
+# DiTBlockExecutor.swift:1035-1242).
+# --------------------------------------------------------------------------------------
+
+def _w8_diag(rows: int, cols: int, code: int = 129, col_of_row=None) -> dict:
+    q = np.full((rows, cols), 128, np.uint8)
+    r = np.arange(rows)
+    c = r if col_of_row is None else col_of_row(r)
+    keep = c < cols
+    q[r[keep], c[keep]] = code
+    groups = (cols + 63) // 64
+    s = np.ones((rows, groups), np.float16)
+    z = np.full((rows, groups), -128.0, np.float16)
+    return {"storage": 1, "rows": rows, "cols": cols, "row_stride": cols,
+            "packed": q.reshape(-1), "scale_bits": s.view(np.uint16), "zero_bits": z.view(np.uint16)}
+
+
+def _hv(a):
+    """fp16 rounding of an fp64 numpy array, back to fp64."""
+    return np.asarray(a, np.float64).astype(np.float16).astype(np.float64)
+
+
+def _rms64(v, w, eps):
+    v = np.asarray(v, np.float64)
+    return v / math.sqrt(float((v * v).mean()) + eps) * np.asarray(w, np.float64)
+
+
+def _softmax_rows(scores):
+    p = np.exp(scores - scores.max())
+    return p / p.sum()
+
+
+def test_qwen_closed_form_norm_weights_rope_and_swiglu():
+    """B1 S5 (key length 4), hidden 256, 2 query heads on 1 KV head, W8 identity projections:
+        n1 = h(rms(x) * 3);  q_h = n1[128h:128h+128], k = n1[0:128], v = n1[128:256]
+        q_h' = h(rope_t(rms(q_h) * wq)), k' = h(rope_t(rms(k) * wk))    (distinct wq, wk)
+        a_h(t) = h(sum_{j<=t, j<4} softmax_j(q_h'(t).k'(j)/sqrt(128)) v(j))
+        x1 = x + h(a);  n2 = h(rms(x1) * 0.5);  x2 = x1 + h(h(silu(n2) * h(2 n2)))
+    (gate = identity, up = 2 x identity, down = identity).  A dropped Q or K norm, a Q/K
+    norm weight swap, RoPE missing on Q or K, the input-norm weight in the post-attention
+    norm, gate and up swapped in the SwiGLU and a missing causal mask each move the result
+    by far more than the tolerance."""
+    B, S, hidden, H, Hkv, I, L = 1, 5, 256, 2, 1, 256, 4
+    d = inputs.qwen_layer(B=B, S=S, hidden=hidden, heads=H, kv_heads=Hkv, intermediate=I)
+    g = torch.Generator().manual_seed(31)
+    d["key_lengths"] = torch.tensor([L], dtype=torch.int32)
+    d["input_norm"] = torch.full((hidden,), 3.0).half()
+    d["post_attention_norm"] = torch.full((hidden,), 0.5).half()
+    d["q_norm"] = (0.5 + torch.rand(HD, generator=g)).half()
+    d["k_norm"] = (0.5 + torch.rand(HD, generator=g)).half()
+    d["w"] = {"q": _w8_diag(H * HD, hidden), "k": _w8_diag(Hkv * HD, hidden),
+              "v": _w8_diag(Hkv * HD, hidden, col_of_row=lambda r: r + 128),
+              "o": _w8_diag(hidden, H * HD), "gate": _w8_diag(I, hidden),
+              "up": _w8_diag(I, hidden, code=130), "down": _w8_diag(hidden, I)}
+    eps = d["eps"]
+    x = d["x"][0].double().numpy()
+    rope = d["rope"].double().numpy()
+    wq = d["q_norm"].double().numpy()
+    wk = d["k_norm"].double().numpy()
+    w_in = d["input_norm"].double().numpy()
+    w_post = d["post_attention_norm"].double().numpy()
+
+    def layer(q_norm=True, k_norm=True, q_w=wq, k_w=wk, rope_q=True, rope_k=True,
+              post_w=w_post, swap_gate_up=False, causal=True):
+        n1 = np.stack([_hv(_rms64(x[t], w_in, eps)) for t in range(S)])
+
+        def qk(vec, t, norm, w, rot):
+            y = _rms64(vec, w, eps) if norm else vec
+            return _hv(_rope_rotate(y, rope[t]) if rot else y)
+        k = np.stack([qk(n1[t, 0:HD], t, k_norm, k_w, rope_k) for t in range(S)])
+        v = n1[:, HD:2 * HD]
+        a = np.zeros((S, H * HD))
+        for h in range(H):
+            for t in range(S):
+                qv = qk(n1[t, h * HD:(h + 1) * HD], t, q_norm, q_w, rope_q)
+                keys = [j for j in range(S) if (j <= t or not causal) and j < L]
+                p = _softmax_rows(np.array([qv @ k[j] for j in keys]) / math.sqrt(HD))
+                a[t, h * HD:(h + 1) * HD] = _hv(sum(p[i] * v[j] for i, j in enumerate(keys)))
+        x1 = x + a
+        n2 = np.stack([_hv(_rms64(x1[t], post_w, eps)) for t in range(S)])
+        gate, up = n2, _hv(2 * n2)
+        if swap_gate_up:
+            gate, up = up, gate
+        m = _hv(gate / (1 + np.exp(-gate)) * up)
+        return x1, x1 + m
+
+    x1_ref, x2_ref = layer()
+    out, inter = blocks.qwen_layer(d, return_intermediates=True)
+    got1, got2 = inter["x1"][0].double().numpy(), out[0].double().numpy()
+    tol1 = 2e-3 * np.abs(x1_ref - x).max()
+    tol2 = 2e-3 * np.abs(x2_ref - x1_ref).max()
+    assert np.abs(got1 - x1_ref).max() <= tol1, (np.abs(got1 - x1_ref).max(), tol1)
+    assert np.abs(got2 - x2_ref).max() <= tol1 + tol2, (np.abs(got2 - x2_ref).max(), tol2)
+
+    attention_mistakes = {
+        "no Q norm": dict(q_norm=False), "no K norm": dict(k_norm=False),
+        "Q uses the K weight": dict(q_w=wk), "K uses the Q weight": dict(k_w=wq),
+        "no RoPE on Q": dict(rope_q=False), "no RoPE on K": dict(rope_k=False),
+        "no causal mask": dict(causal=False),
+    }
+    for name, kw in attention_mistakes.items():
+        gap = np.abs(layer(**kw)[0] - x1_ref).max()
+        assert gap > 10 * tol1, (name, gap, tol1)
+    mlp_mistakes = {"post norm with the input weight": dict(post_w=w_in),
+                    "gate and up swapped": dict(swap_gate_up=True)}
+    for name, kw in mlp_mistakes.items():
+        gap = np.abs(layer(**kw)[1] - x2_ref).max()
+        assert gap > 10 * (tol1 + tol2), (name, gap, tol2)
+
+
+def test_block_closed_form_cross_attention_norms():
+    """Cross branch with non-zero Q and K.  adaLN (shared by the branches) is shift 0,
+    scale 2 (so LN(x) * 3), gate 0; W2 is zero except the cross gate rows, so only the cross
+    branch has a gate g2.  Q = n2 through an
+    identity projection; K = ctx[:, r % 1024] and V = ctx[:, r % 1024] for output column r;
+    identity O.  Per head: q' = h(rms(q_h) * wq), k' = h(rms(k_h) * wk) (distinct weights, no
+    RoPE), x2 = x + g2 * h(h(softmax(q'k'^T / sqrt(128)) v)).  A dropped cross Q or K norm, one
+    side normalised with the other's weight, the self-attention weights used, or RoPE applied
+    to the cross Q/K each move the result by far more than the tolerance.  (Exchanging the two
+    weights is not among them: q'.k' depends only on their per-column product.)"""
+    S, T = 4, 3
+    wrap = lambda r: r % 1024  # noqa: E731
+    d = _identity_block(S, T, cross_q=_identity(DIM, DIM), cross_k=_identity(DIM, 1024, wrap),
+                        cross_v=_identity(DIM, 1024, wrap))
+    g = torch.Generator().manual_seed(12)
+    d["cross_q_norm"] = (0.5 + torch.rand(HD, generator=g)).half()
+    d["cross_k_norm"] = (0.5 + torch.rand(HD, generator=g)).half()
+    d["self_q_norm"] = (0.5 + torch.rand(HD, generator=g)).half()
+    d["self_k_norm"] = (0.5 + torch.rand(HD, generator=g)).half()
+    d["ctx"] = (torch.randn(T, 1024, generator=g) * 2).half()
+    for br in ("self", "cross", "mlp"):
+        d[f"mod_{br}_w2"] = torch.zeros_like(d[f"mod_{br}_w2"])
+    d["mod_cross_w2"][2 * DIM:] = (torch.randn(DIM, 256, generator=g) * 0.05).half()
+    d["adaln"] = torch.cat([torch.zeros(DIM), torch.full((DIM,), 2.0), torch.zeros(DIM)])
+    m = _mods(d)
+    assert float(m["self"][2].abs().max()) == 0 and float(m["mlp"][2].abs().max()) == 0
+    assert float(m["cross"][0].abs().max()) == 0 and float(m["cross"][1].min()) == 2.0
+    g2 = m["cross"][2].double().numpy()
+    assert np.abs(g2).min() > 0
+
+    eps = d["eps"]
+    x = d["x"].double().numpy()
+    ctx = d["ctx"].double().numpy()
+    rope = d["rope"].double().numpy()
+    cq, ck = d["cross_q_norm"].double().numpy(), d["cross_k_norm"].double().numpy()
+    sq, sk = d["self_q_norm"].double().numpy(), d["self_k_norm"].double().numpy()
+    n2 = _h(_ln_mod(d["x"].float(), m["cross"][1], m["cross"][0])).double().numpy()
+    kv = np.stack([ctx[j, np.arange(DIM) % 1024] for j in range(T)])
+
+    def branch(q_norm=True, k_norm=True, q_w=cq, k_w=ck, rope_qk=False):
+        out = np.zeros((S, DIM))
+        for h in range(NH):
+            cols = slice(h * HD, (h + 1) * HD)
+
+            def pro(vec, t, norm, w):
+                y = _rms64(vec, w, eps) if norm else vec
+                return _hv(_rope_rotate(y, rope[t]) if rope_qk else y)
+            keys = np.stack([pro(kv[j, cols], j, k_norm, k_w) for j in range(T)])
+            for t in range(S):
+                qv = pro(n2[t, cols], t, q_norm, q_w)
+                p = _softmax_rows(keys @ qv / math.sqrt(HD))
+                out[t, cols] = _hv(p @ kv[:, cols])
+        return x + g2 * out
+
+    want = branch()
+    got = blocks.dit_block(d).double().numpy()
+    tol = 2e-3 * np.abs(want - x).max()
+    assert np.abs(got - want).max() <= tol, (np.abs(got - want).max(), tol)
+    mistakes = {"no cross Q norm": dict(q_norm=False), "no cross K norm": dict(k_norm=False),
+                "cross Q with the K weight": dict(q_w=ck), "cross K with the Q weight": dict(k_w=cq),
+                "self-attention weights": dict(q_w=sq, k_w=sk), "RoPE on cross Q/K": dict(rope_qk=True)}
+    for name, kw in mistakes.items():
+        gap = np.abs(branch(**kw) - want).max()
+        assert gap > 10 * tol, (name, gap, tol)
