@@ -24,7 +24,7 @@ STATUS_NAMES = {
 # enums
 LAYOUT_HEAD_MAJOR, LAYOUT_TOKEN_MAJOR = 0, 1
 NUMERICS_LEGACY, NUMERICS_FP32_SCORES, NUMERICS_BF16_COMPUTE = 0, 1, 2
-ATTN_AUTO, ATTN_FLASH, ATTN_GENERIC = 0, 1, 2
+ATTN_AUTO, ATTN_FLASH, ATTN_GENERIC, ATTN_LEGACY_MPS = 0, 1, 2, 3
 STORAGE_W4, STORAGE_W8, STORAGE_FP16, STORAGE_FP32 = 0, 1, 2, 3
 LINEAR_AUTO, LINEAR_FUSED, LINEAR_DEQUANT_THEN_GEMM = 0, 1, 2
 FAMILY_OTHER, FAMILY_ATTENTION_PROJECTION, FAMILY_MLP_UP, FAMILY_MLP_DOWN = 0, 1, 2, 3

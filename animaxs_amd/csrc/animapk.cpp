@@ -404,6 +404,9 @@ PackTensor decode_tensor(const JValue& t, size_t index) {
   r.name = need_str(t, "name", where);
   const JValue& shape = need(t, "shape", where);
   if (shape.kind != JValue::ARR) json_err("shape of " + r.name + " is not an array");
+  // anima_pack_tensor carries at most 8 dimensions; a longer shape is refused here rather
+  // than cut off where it is handed out.
+  if (shape.a.size() > 8) json_err("shape of " + r.name + " has more than 8 dimensions");
   for (const JValue& d : shape.a) r.shape.push_back(json_i64(d, "shape of " + r.name));
   r.logical_dtype = need_str(t, "logical_dtype", where);
   r.storage_dtype = need_str(t, "storage_dtype", where);
@@ -555,7 +558,7 @@ void to_c(const PackTensor& t, anima_pack_tensor& o) {
   std::memset(&o, 0, sizeof o);
   o.name = t.name.c_str();
   o.storage = t.storage;
-  o.rank = (int32_t)std::min<size_t>(t.shape.size(), 8);
+  o.rank = (int32_t)t.shape.size();  // <= 8, checked when the JSON is decoded
   for (int i = 0; i < o.rank; ++i) o.shape[i] = t.shape[i];
   o.blob_offset = (int64_t)t.blob_offset;
   o.blob_size = (int64_t)t.blob_size;

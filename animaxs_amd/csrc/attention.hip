@@ -345,6 +345,90 @@ __global__ __launch_bounds__(64) void generic_attention_kernel(FlashParams p, in
 }
 
 // ===========================================================================
+// MPS-rounding kernel: the reference's score-tile backends (legacyHeadMajorMPS,
+// stridedTokenMajorMPS; AttentionExecutor.swift:221-301, 412-496) under legacy
+// numerics store the scaled scores as fp16 (MPSMatrixMultiplication with
+// alpha = scale into an fp16 matrix), take the row max, exp and sum in fp32, store
+// the normalised probabilities as fp16 (attention_softmax_rows,
+// AnimaKernels.metal:1051-1100), then multiply them with V in fp32 into an fp16
+// output.  This kernel keeps exactly those rounding points: one 64-lane workgroup
+// per (batch, head, query row), lane j of a pass owning key k0 + j; the three
+// passes (max, sum, probabilities and PV) recompute the same fp16 scores instead
+// of storing a score tile.
+// ===========================================================================
+__device__ __forceinline__ float legacy_score(const float* qs, const half_t* kr, int D, float scale) {
+  float dot = 0.f;
+  for (int d = 0; d < D; ++d) dot = fmaf(qs[d], (float)kr[d], dot);
+  return (float)f32_to_f16(dot * scale);
+}
+
+__global__ __launch_bounds__(64) void legacy_mps_attention_kernel(FlashParams p, int D) {
+  __shared__ float qs[GEN_MAX_D];
+  __shared__ float ps[64];
+  const int lane = threadIdx.x;
+  const int qi = blockIdx.x;
+  const int head = blockIdx.y % p.H;
+  const int b = blockIdx.y / p.H;
+  const int kvh = head / p.group;
+
+  int kv_len = p.Sk;
+  if (p.key_lengths_dev) {
+    int L = p.key_lengths_dev[b];
+    kv_len = L < 1 ? 1 : (L > p.Sk ? p.Sk : L);
+  } else if (p.use_host_lengths) {
+    kv_len = p.host_lengths[b];
+  }
+  int kend = kv_len;
+  if (p.causal) kend = min(kend, qi + 1);
+
+  const half_t* qp = p.q + (int64_t)b * p.q_batch + (int64_t)head * p.q_head + (int64_t)qi * p.q_tok;
+  for (int d = lane; d < D; d += 64) qs[d] = (float)qp[d];
+  __syncthreads();
+  const half_t* kb = p.k + (int64_t)b * p.k_batch + (int64_t)kvh * p.k_head;
+  const half_t* vb = p.v + (int64_t)b * p.v_batch + (int64_t)kvh * p.v_head;
+
+  // pass 1: row max of the fp16 scores
+  float m = -INFINITY;
+  for (int j = lane; j < kend; j += 64) m = fmaxf(m, legacy_score(qs, kb + (int64_t)j * p.k_tok, D, p.scale));
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  // pass 2: fp32 sum of exp(s - max)
+  float l = 0.f;
+  for (int j = lane; j < kend; j += 64) l += expf(legacy_score(qs, kb + (int64_t)j * p.k_tok, D, p.scale) - m);
+  for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+  const float inv = 1.f / l;
+  // pass 3: fp16 probabilities, fp32 PV
+  constexpr int EMAX = GEN_MAX_D / 64;
+  float acc[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) acc[e] = 0.f;
+  for (int k0 = 0; k0 < kend; k0 += 64) {
+    const int j = k0 + lane;
+    float pj = 0.f;
+    if (j < kend)
+      pj = (float)f32_to_f16(expf(legacy_score(qs, kb + (int64_t)j * p.k_tok, D, p.scale) - m) * inv);
+    ps[lane] = pj;
+    __syncthreads();
+    const int cnt = min(64, kend - k0);
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) {
+      const int d = lane + 64 * e;
+      if (d < D) {
+        float a = acc[e];
+        for (int jj = 0; jj < cnt; ++jj) a = fmaf(ps[jj], (float)vb[(int64_t)(k0 + jj) * p.v_tok + d], a);
+        acc[e] = a;
+      }
+    }
+    __syncthreads();
+  }
+  half_t* op = p.o + (int64_t)b * p.o_batch + (int64_t)head * p.o_head + (int64_t)qi * p.o_tok;
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) {
+    const int d = lane + 64 * e;
+    if (d < D) op[d] = f32_to_f16(acc[e]);
+  }
+}
+
+// ===========================================================================
 // Q/K prologue: per-(batch, token, head) RMSNorm with a shared [D] weight and
 // optional split-half RoPE, fp32 maths, fp16 dense head-major output
 // [batch][heads][rows][D].  One wave per row; lane p owns the pairs
@@ -615,6 +699,14 @@ void launch_generic(const FlashParams& p, int D, int batch, hipStream_t stream) 
   if ((int64_t)p.H * batch > 65535) fail(ANIMA_E_INVALID_SHAPE, "attention heads * batch too large");
   dim3 grid((unsigned)p.Sq, (unsigned)(p.H * batch)), block(64);
   hipLaunchKernelGGL(generic_attention_kernel, grid, block, 0, stream, p, D);
+  ANIMA_HIP(hipGetLastError());
+}
+
+void launch_legacy_mps(const FlashParams& p, int D, int batch, hipStream_t stream) {
+  if (D > GEN_MAX_D) fail(ANIMA_E_UNSUPPORTED, "MPS-rounding attention supports head_dim <= 512");
+  if ((int64_t)p.H * batch > 65535) fail(ANIMA_E_INVALID_SHAPE, "attention heads * batch too large");
+  dim3 grid((unsigned)p.Sq, (unsigned)(p.H * batch)), block(64);
+  hipLaunchKernelGGL(legacy_mps_attention_kernel, grid, block, 0, stream, p, D);
   ANIMA_HIP(hipGetLastError());
 }
 

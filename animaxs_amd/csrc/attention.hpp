@@ -19,6 +19,7 @@ struct FlashParams {
   int Sq, Sk, H, group;
   int q_tiles;
   float scale_log2;                // scale * log2(e)
+  float scale;                     // the softmax scale itself (MPS-rounding kernel)
   int causal;
   const int* key_lengths_dev;      // device lengths (clamped in-kernel) or null
   int use_host_lengths;
@@ -26,14 +27,15 @@ struct FlashParams {
   const half_t* q_norm_w;          // fused Q RMSNorm weight or null
   float eps;
   const float* rope;               // fused Q RoPE table or null
-  // Key splits (256-row kernel, non-causal, no key lengths): workgroup split s takes keys
-  // [s*kv_chunk, (s+1)*kv_chunk) and writes its unnormalised fp32 O rows to part_o
-  // ([split][batch][head][Sq][D]) and (running max in log2 units, row sum) to part_ml
-  // ([split][batch][head][Sq][2]); flash_combine_kernel merges them into o.
+  // Key splits (256-row and head-dim-384 kernels, non-causal, no key lengths): workgroup
+  // split s takes keys [s*kv_chunk, (s+1)*kv_chunk) and writes its normalised O rows in fp16
+  // to part_o ([split][batch][head][Sq][D]) and (running max in log2 units, row sum) in fp32
+  // to part_ml ([split][batch][head][Sq][2]); flash_combine_kernel merges them into o.
   int kv_splits;                   // 0 or 1: no split
   int nbatch;                      // batch count (partial row index)
   int kv_chunk;                    // keys per split, a multiple of 64
-  void* part_o;                    // key splits: rows [split][batch][head][Sq][D]: fp16 O_s / l_s (fp32 O_s for D = 384)
+  void* part_o;                    // key splits: fp16 O_s / l_s rows [split][batch][head][Sq][D] for every
+                                   // head_dim, then (256-byte aligned) part_ml
   float* part_ml;
 };
 
@@ -66,6 +68,7 @@ void launch_flash_wide(const FlashParams& p, int D, dim3 grid, hipStream_t strea
 void launch_flash_v2(const FlashParams& p, int D, dim3 grid, hipStream_t stream);
 void launch_flash_combine(const FlashParams& p, int D, int batch, hipStream_t stream);
 void launch_generic(const FlashParams& p, int D, int batch, hipStream_t stream);
+void launch_legacy_mps(const FlashParams& p, int D, int batch, hipStream_t stream);
 void launch_prologue(const PrologueParams& p, hipStream_t stream);
 
 class AttentionExecutor {

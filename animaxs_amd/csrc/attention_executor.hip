@@ -14,7 +14,7 @@ AttentionExecutor::AttentionExecutor(anima_ctx* ctx, const anima_attention_confi
   if (cfg.tile_rows <= 0) fail(ANIMA_E_INVALID_ARGUMENT, "attention tile rows must be positive");
   if (cfg.numerics < ANIMA_NUMERICS_LEGACY || cfg.numerics > ANIMA_NUMERICS_BF16_COMPUTE)
     fail(ANIMA_E_INVALID_ARGUMENT, "unknown attention numerics");
-  if (cfg.backend < ANIMA_ATTENTION_BACKEND_AUTO || cfg.backend > ANIMA_ATTENTION_BACKEND_GENERIC)
+  if (cfg.backend < ANIMA_ATTENTION_BACKEND_AUTO || cfg.backend > ANIMA_ATTENTION_BACKEND_LEGACY_MPS)
     fail(ANIMA_E_INVALID_ARGUMENT, "unknown attention backend");
   if (cfg.layout != ANIMA_LAYOUT_HEAD_MAJOR && cfg.layout != ANIMA_LAYOUT_TOKEN_MAJOR)
     fail(ANIMA_E_INVALID_ARGUMENT, "unknown attention layout");
@@ -216,6 +216,7 @@ void AttentionExecutor::encode_impl(const anima_attention_args& a, bool no_alloc
       use_flash = true;
       break;
     case ANIMA_ATTENTION_BACKEND_GENERIC:
+    case ANIMA_ATTENTION_BACKEND_LEGACY_MPS:
       use_flash = false;
       break;
     default:
@@ -254,6 +255,7 @@ void AttentionExecutor::encode_impl(const anima_attention_args& a, bool no_alloc
   }
   p.Sq = (int)Sq; p.Sk = (int)Sk; p.H = (int)H; p.group = (int)(H / kvh);
   p.scale_log2 = scale * 1.4426950408889634f;
+  p.scale = scale;
   p.causal = a.causal ? 1 : 0;
   p.eps = eps;
   if (use_flash && !need_q_pro) {
@@ -308,6 +310,8 @@ void AttentionExecutor::encode_impl(const anima_attention_args& a, bool no_alloc
       p.part_ml = reinterpret_cast<float*>(pw + flash_split_o_bytes(p, (int)D, (int)B, splits));
     }
     launch_flash(p, (int)D, (int)B, cfg_.flash_rows, stream);
+  } else if (cfg_.backend == ANIMA_ATTENTION_BACKEND_LEGACY_MPS && cfg_.numerics == ANIMA_NUMERICS_LEGACY) {
+    launch_legacy_mps(p, (int)D, (int)B, stream);
   } else {
     launch_generic(p, (int)D, (int)B, stream);
   }

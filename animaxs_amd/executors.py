@@ -107,7 +107,9 @@ class Context:
 
 _NUMERICS = {"legacy": _abi.NUMERICS_LEGACY, "fp32ScoresAndSoftmax": _abi.NUMERICS_FP32_SCORES,
              "fp32": _abi.NUMERICS_FP32_SCORES, "bf16_compute": _abi.NUMERICS_BF16_COMPUTE}
-_BACKENDS = {"auto": _abi.ATTN_AUTO, "flash": _abi.ATTN_FLASH, "generic": _abi.ATTN_GENERIC}
+_BACKENDS = {"auto": _abi.ATTN_AUTO, "flash": _abi.ATTN_FLASH, "generic": _abi.ATTN_GENERIC,
+             "legacyMPS": _abi.ATTN_LEGACY_MPS, "legacyHeadMajorMPS": _abi.ATTN_LEGACY_MPS,
+             "stridedTokenMajorMPS": _abi.ATTN_LEGACY_MPS, "metalFlash": _abi.ATTN_FLASH}
 
 
 @dataclass

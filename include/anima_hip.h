@@ -88,10 +88,16 @@ typedef enum anima_layout {
   ANIMA_LAYOUT_TOKEN_MAJOR = 1  /* [batch][rows][token_stride]; head h at columns h*head_dim */
 } anima_layout;
 
-/* AttentionNumerics (AttentionExecutor.swift:5-12).  Every kernel here keeps
- * scores, softmax and accumulation in fp32 (P is rounded to fp16 for the PV
- * product on the matrix cores); LEGACY and FP32_SCORES therefore both select it,
- * BF16_COMPUTE is refused with ANIMA_E_UNSUPPORTED. */
+/* AttentionNumerics (AttentionExecutor.swift:5-12).  As in the reference, what
+ * LEGACY means depends on the backend.  The reference's metalFlash and
+ * streamingMPS backends keep fp32 scores and softmax state under legacy numerics
+ * (:179-203), and so do AUTO, FLASH and GENERIC here (the flash kernels round P
+ * to fp16 for the PV product on the matrix cores).  Its MPS score-tile backends
+ * round the scaled scores and the normalised probabilities to fp16 between
+ * passes (:221-301, 412-496); ANIMA_ATTENTION_BACKEND_LEGACY_MPS keeps those
+ * rounding points.  FP32_SCORES selects fp32 scores on every backend (the
+ * reference's encodeFP32 ignores the backend).  BF16_COMPUTE is refused with
+ * ANIMA_E_UNSUPPORTED. */
 typedef enum anima_attention_numerics {
   ANIMA_NUMERICS_LEGACY = 0,
   ANIMA_NUMERICS_FP32_SCORES = 1,
@@ -99,14 +105,20 @@ typedef enum anima_attention_numerics {
 } anima_attention_numerics;
 
 /* DiTAttentionBackend (AttentionExecutor.swift:29-44) re-cut for MI355X:
- * AUTO picks the MFMA flash kernel when its contract holds (head_dim 64/128,
+ * AUTO picks the MFMA flash kernel when its contract holds (head_dim 64/128/384,
  * 16-byte aligned rows) and the generic fp32 kernel otherwise; FLASH demands the
  * MFMA kernel and fails loudly when the shape is outside it (the metalFlash gate,
- * :685-705); GENERIC forces the generic kernel (the fp32 diagnostic path). */
+ * :685-705); GENERIC forces the generic kernel (the fp32 diagnostic path);
+ * LEGACY_MPS is the legacyHeadMajorMPS / stridedTokenMajorMPS pair: under LEGACY
+ * numerics it stores fp16 scaled scores and fp16 normalised probabilities, as
+ * the MPS passes and attention_softmax_rows (AnimaKernels.metal:1051-1100) do
+ * (one workgroup per query row, a compatibility path, not a fast one); under
+ * FP32_SCORES it runs the generic kernel. */
 typedef enum anima_attention_backend {
   ANIMA_ATTENTION_BACKEND_AUTO = 0,
   ANIMA_ATTENTION_BACKEND_FLASH = 1,
-  ANIMA_ATTENTION_BACKEND_GENERIC = 2
+  ANIMA_ATTENTION_BACKEND_GENERIC = 2,
+  ANIMA_ATTENTION_BACKEND_LEGACY_MPS = 3
 } anima_attention_backend;
 
 /* AttentionExecutor.init (AttentionExecutor.swift:97-110). */
@@ -443,8 +455,12 @@ anima_status anima_dit_forward_encode(anima_dit_block* blk, const anima_dit_bloc
  * while earlier blocks compute; an event per slot makes the compute stream wait
  * for the copy, and the copy for the last block that read the slot, so a slot is
  * never overwritten in flight (the reference's markInFlight/complete, enforced on
- * the device instead of by host waits).  Host ranges should be pinned
- * (hipHostMalloc) for the copies to overlap with compute. */
+ * the device instead of by host waits).  The copies are queued with
+ * hipMemcpyAsync, so every host range must stay valid (mapped, not freed) until
+ * the forward's stream work has completed (anima_ctx_synchronize).  Only pinned
+ * ranges (hipHostMalloc) copy while earlier blocks compute; pageable memory, such
+ * as the pages of a memory-mapped .animapk, is staged by the HIP runtime and the
+ * copy then blocks the host and does not overlap with compute. */
 typedef struct anima_weight_streamer anima_weight_streamer;
 anima_status anima_weight_streamer_create(anima_ctx* ctx, int64_t capacity, int32_t slots,
                                           anima_weight_streamer** out);

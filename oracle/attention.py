@@ -2,7 +2,10 @@
 
 Restates:
   * the attention of ``scripts/dit_block0_oracle.py:124-143`` (softmax(scale*QK^T) V,
-    fp32 scores / probabilities; the ``LEGACY_ATTENTION`` fp16 rounding is off),
+    fp32 scores / probabilities; with ``legacy=True`` the ``LEGACY_ATTENTION`` rounding of
+    :135-141: the scaled scores and the normalised probabilities pass through fp16, the
+    rounding points of the reference's MPS backends and ``attention_softmax_rows``,
+    AnimaKernels.metal:1051-1100),
   * ``DiTBlockCPU.attentionHead`` (AnimaXS/Runtime/Text/DiTBlockCPU.swift:151-186) and
     ``QwenNumerics.scaledDotAttention`` (AnimaXS/Runtime/Text/QwenNumerics.swift:89-115),
   * GQA head map ``kvHead = h / (H / Hkv)`` (AnimaXS/Runtime/Metal/AttentionExecutor.swift:222;
@@ -43,11 +46,13 @@ def qk_prologue(x: torch.Tensor, norm_w: torch.Tensor | None, eps: float,
 
 
 def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float | None = None,
-         causal: bool = False, key_lengths=None) -> torch.Tensor:
+         causal: bool = False, key_lengths=None, legacy: bool = False) -> torch.Tensor:
     """Attention over ``q[B,Sq,H,D]``, ``k,v[B,Sk,Hkv,D]`` -> ``[B,Sq,H,D]`` fp32.
 
     ``key_lengths[b]`` keys ``j >= L_b`` receive the additive ``finfo(fp32).min/4``
-    mask; ``causal`` adds the same value above the diagonal (requires Sq == Sk)."""
+    mask; ``causal`` adds the same value above the diagonal (requires Sq == Sk).
+    ``legacy`` rounds the scaled scores (before the mask) and the normalised
+    probabilities to fp16."""
     B, Sq, H, D = q.shape
     Sk, Hkv = k.shape[1], k.shape[2]
     assert H % Hkv == 0
@@ -71,9 +76,13 @@ def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float | No
         for h in range(H):
             kh = h // rep
             s = (qf[b, :, h, :] @ kf[b, :, kh, :].T) * scale
+            if legacy:
+                s = s.half().float()
             if mask is not None:
                 s = s + mask
             p = torch.softmax(s, dim=-1)
+            if legacy:
+                p = p.half().float()
             out[b, :, h, :] = p @ vf[b, :, kh, :]
     return out
 

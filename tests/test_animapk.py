@@ -140,6 +140,9 @@ def test_tensor_and_table_rejections(tmp_path):
            "failed to decode architecture JSON")
     expect(lambda: AnimapkFile(_meta_pack(tmp_path, field(0, "shape", "4"))), _abi.E_FORMAT,
            "shape of a is not an array")
+    # the C record holds 8 dimensions: a 9-dimensional shape is refused, never cut off
+    expect(lambda: AnimapkFile(_meta_pack(tmp_path, field(0, "shape", [1] * 8 + [4]))), _abi.E_FORMAT,
+           "shape of a has more than 8 dimensions")
 
 
 def test_malformed_json_text(tmp_path):

@@ -340,3 +340,76 @@ def test_wide_flash_head_dim_384_ragged(ctx, B, H, Sq, Sk, causal, lengths):
              out_shape=(B, Sq, H, D), batch=B, causal=causal, backend="flash", **kw)
     ref = oatt.sdpa(q, k, v, causal=causal, key_lengths=lengths)
     assert_attention_close(o, ref, label=f"wide D384 B{B} H{H} Sq{Sq} Sk{Sk} causal={causal}")
+
+
+@pytest.mark.parametrize("B,H,Hkv,Sq,Sk,causal,lengths", [(1, 4, 2, 256, 1100, False, None),
+                                                          (2, 4, 1, 130, 300, False, [300, 77]),
+                                                          (1, 2, 1, 200, 200, True, None)])
+def test_wide_flash_head_dim_384_grouped_kv_heads(ctx, B, H, Hkv, Sq, Sk, causal, lengths):
+    """Head dim 384 with fewer K/V heads than query heads (head h reads K/V head h / (H / Hkv)):
+    K/V in their own token-major rows of Hkv * 384 halfs.  1 x 4/2 x 256 x 1100 splits the keys
+    (2 splits, the last one ragged); the others run unsplit with key lengths or causal rows."""
+    D = 384
+    g = torch.Generator().manual_seed(B * 1000 + H * 100 + Hkv * 10 + Sq + Sk)
+    q = (torch.randn(B, Sq, H, D, generator=g) * 2.0).half()
+    k = (torch.randn(B, Sk, Hkv, D, generator=g) * 2.0).half()
+    v = torch.randn(B, Sk, Hkv, D, generator=g).half()
+    kw = {}
+    if lengths is not None:
+        kw["key_lengths"] = np.array(lengths, np.int32)
+    print(f"WIDE GQA D384 B{B} H{H}/{Hkv} Sq{Sq} Sk{Sk} causal={causal} lengths={lengths}", flush=True)
+    o = _run(ctx, dev(q), dev(k), dev(v), layout=("tokenMajor", H * D), heads=H, Sq=Sq, Sk=Sk, D=D,
+             out_shape=(B, Sq, H, D), batch=B, causal=causal, backend="flash", key_value_heads=Hkv,
+             kv_token_stride=Hkv * D, **kw)
+    ref = oatt.sdpa(q, k, v, causal=causal, key_lengths=lengths)
+    assert_attention_close(o, ref, label=f"wide GQA D384 B{B} H{H}/{Hkv} Sq{Sq} Sk{Sk} causal={causal}")
+
+
+# ---------------------------------------------------------------------------
+# The MPS-rounding backend (legacyHeadMajorMPS / stridedTokenMajorMPS under legacy numerics,
+# AttentionExecutor.swift:221-301, 412-496): fp16 scaled scores and fp16 normalised
+# probabilities, against the oracle's legacy mode (scripts/dit_block0_oracle.py:135-141).
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("case", ["head_major_gqa_causal_lengths", "token_major_norm_rope", "hd64"])
+def test_legacy_mps_backend_matches_legacy_oracle(ctx, case):
+    g = torch.Generator().manual_seed({"head_major_gqa_causal_lengths": 41, "token_major_norm_rope": 42, "hd64": 43}[case])
+    kw = {}
+    if case == "head_major_gqa_causal_lengths":
+        B, H, Hkv, S, D = 2, 4, 2, 200, 128
+        q = (torch.randn(B, H, S, D, generator=g) * 2).half()
+        k = (torch.randn(B, Hkv, S, D, generator=g) * 2).half()
+        v = torch.randn(B, Hkv, S, D, generator=g).half()
+        L = [200, 71]
+        o = _run(ctx, dev(q), dev(k), dev(v), layout="headMajor", heads=H, Sq=S, Sk=S, D=D,
+                 out_shape=(B, H, S, D), backend="legacyMPS", batch=B, key_value_heads=Hkv, causal=True,
+                 key_lengths=L).permute(0, 2, 1, 3)
+        qq, kk, vv = (t.permute(0, 2, 1, 3) for t in (q, k, v))
+        kw = dict(causal=True, key_lengths=L)
+    elif case == "token_major_norm_rope":
+        d = inputs.self_attention(2, S=256)
+        pro = QKPrologue(dev(d["q_norm_w"]), dev(d["k_norm_w"]), d["eps"], dev(d["rope"]), 256, True, True)
+        o = _run(ctx, dev(d["q"]), dev(d["k"]), dev(d["v"]), layout=("tokenMajor", 2048), heads=16, Sq=256,
+                 Sk=256, D=128, out_shape=(1, 256, 16, 128), backend="stridedTokenMajorMPS", prologue=pro)
+        qq = oatt.qk_prologue(d["q"], d["q_norm_w"], d["eps"], d["rope"]).half()
+        kk = oatt.qk_prologue(d["k"], d["k_norm_w"], d["eps"], d["rope"]).half()
+        vv = d["v"]
+    else:
+        B, H, Sq, Sk, D = 1, 3, 77, 300, 64
+        q = (torch.randn(B, Sq, H, D, generator=g) * 2).half()
+        k = (torch.randn(B, Sk, H, D, generator=g) * 2).half()
+        v = torch.randn(B, Sk, H, D, generator=g).half()
+        o = _run(ctx, dev(q), dev(k), dev(v), layout=("tokenMajor", H * D), heads=H, Sq=Sq, Sk=Sk, D=D,
+                 out_shape=(B, Sq, H, D), backend="legacyHeadMajorMPS", batch=B)
+        qq, kk, vv = q, k, v
+    print(f"LEGACY MPS {case}", flush=True)
+    ref_legacy = oatt.sdpa(qq, kk, vv, legacy=True, **kw)
+    ref_fp32 = oatt.sdpa(qq, kk, vv, **kw)
+    # Legacy numerics are by design less accurate than fp32 scores: against the fp32 oracle the
+    # kernel may be as far as the legacy oracle is, plus its fp16 output rounding.
+    gap = float((ref_legacy - ref_fp32).abs().sum() / ref_fp32.abs().sum())
+    assert_attention_close(o, ref_fp32, mean_rel_tol=gap + 3e-4, label=f"legacy MPS {case} vs fp32 oracle")
+    # The same rounding points as the legacy oracle (whose output, like the kernel's, is
+    # stored as fp16): far closer to it than the two oracles are to each other (they differ
+    # only by those roundings).
+    assert_attention_close(o, ref_legacy.half(), max_abs_tol=2e-3, mean_rel_tol=min(1e-4, 0.25 * gap),
+                           label=f"legacy MPS {case} vs fp16 legacy oracle (oracle gap {gap:.2e})")

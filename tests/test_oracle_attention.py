@@ -158,3 +158,65 @@ def test_generators_are_seeded_and_shaped():
         if isinstance(a[key], torch.Tensor):
             assert torch.equal(a[key], b[key]), key
     assert a["q"].shape == (1, 64, 16, 128) and a["q"].dtype == torch.float16
+
+
+# --------------------------------------------------------------------------------------
+# Legacy rounding (scripts/dit_block0_oracle.py:135-141; the MPS backends' fp16 score and
+# probability matrices, AnimaKernels.metal:1051-1100).
+# --------------------------------------------------------------------------------------
+
+def test_legacy_uniform_weights_round_to_fp16():
+    """Q = K = 0 over 3 keys: every score is 0 and every probability 1/3, stored as the fp16
+    0.333251953125 (= 1365 / 4096), so the output is 1365/4096 * (v0 + v1 + v2) rather than
+    the mean.  Over 64 keys 1/64 is exact and legacy equals the mean of V."""
+    g = torch.Generator().manual_seed(21)
+    q = torch.zeros(1, 2, 1, 8, dtype=torch.half)
+    k = torch.zeros(1, 3, 1, 8, dtype=torch.half)
+    v = rnd(g, 1, 3, 1, 8, std=4.0)
+    got = A.sdpa(q, k, v, legacy=True)[0, :, 0].double()
+    want = (1365.0 / 4096.0) * v[0, :, 0].double().sum(0)
+    assert torch.allclose(got, want.expand_as(got), rtol=0, atol=1e-5)
+    assert not torch.allclose(got, v[0, :, 0].double().mean(0).expand_as(got), rtol=0, atol=1e-4)
+    k64 = torch.zeros(1, 64, 1, 8, dtype=torch.half)
+    v64 = rnd(g, 1, 64, 1, 8)
+    mean = v64.float().mean(dim=1, keepdim=True)
+    assert torch.allclose(A.sdpa(q, k64, v64, legacy=True), mean.expand(1, 2, 1, 8), atol=1e-6)
+
+
+def test_legacy_two_key_closed_form():
+    """One query, two keys, scale 1.  Scores 1 + 2^-12 and 0: fp16 stores the first as 1
+    (spacing 2^-10 at 1), so the weights are fp16(sigmoid(1)) = 0.73095703125 and
+    fp16(sigmoid(-1)) = 0.26904296875, against the fp32 oracle's sigmoid(1 + 2^-12)."""
+    D = 8
+    q = torch.zeros(1, 1, 1, D)
+    q[0, 0, 0, 0] = 1.0
+    k = torch.zeros(1, 2, 1, D)
+    k[0, 0, 0, 0] = 1.0 + 2.0 ** -12
+    v = torch.zeros(1, 2, 1, D)
+    v[0, 0, 0, :] = 1.0
+    v[0, 1, 0, :] = -3.0
+    p0 = float(np.float16(1.0 / (1.0 + math.exp(-1.0))))
+    p1 = float(np.float16(1.0 / (1.0 + math.exp(1.0))))
+    assert (p0, p1) == (0.73095703125, 0.26904296875)
+    got = A.sdpa(q, k, v, scale=1.0, legacy=True)[0, 0, 0].double()
+    assert torch.allclose(got, torch.full((D,), p0 * 1.0 + p1 * -3.0, dtype=torch.float64), rtol=0, atol=1e-6)
+    s = 1.0 + 2.0 ** -12
+    w = 1.0 / (1.0 + math.exp(-s))
+    fp32 = A.sdpa(q, k, v, scale=1.0)[0, 0, 0].double()
+    assert torch.allclose(fp32, torch.full((D,), w - 3.0 * (1 - w), dtype=torch.float64), rtol=0, atol=1e-6)
+    assert float((got - fp32).abs().max()) > 1e-4
+
+
+def test_legacy_stays_near_fp32_and_keeps_masks():
+    """On random inputs legacy differs from fp32 only by the fp16 roundings (a few 1e-4
+    relative), and causal / key-length masking behaves as in fp32 (masked keys get weight 0)."""
+    g = torch.Generator().manual_seed(22)
+    B, S, H, Hkv, D = 2, 9, 4, 2, 16
+    q, k, v = rnd(g, B, S, H, D, std=2.0), rnd(g, B, S, Hkv, D, std=2.0), rnd(g, B, S, Hkv, D)
+    for causal, L in ((False, None), (True, [9, 4])):
+        lg = A.sdpa(q, k, v, causal=causal, key_lengths=L, legacy=True)
+        fp = A.sdpa(q, k, v, causal=causal, key_lengths=L)
+        rel = float((lg - fp).abs().sum() / fp.abs().sum())
+        assert 1e-6 < rel < 3e-3, rel
+    lg = A.sdpa(q, k, v, key_lengths=[4, 4], legacy=True)
+    assert torch.equal(lg, A.sdpa(q, k[:, :4], v[:, :4], legacy=True))
