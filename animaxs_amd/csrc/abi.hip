@@ -221,6 +221,25 @@ anima_status anima_dequant_to_half_encode(anima_ctx* ctx, const anima_qweight* w
   });
 }
 
+anima_status anima_read_probe_encode(anima_ctx* ctx, anima_buffer src, int64_t src_offset, int64_t bytes,
+                                     anima_buffer sink) {
+  return guarded([&] {
+    require(ctx, "context");
+    if (bytes < 0 || bytes % 16 != 0) fail(ANIMA_E_INVALID_SHAPE, "read probe: bytes must be a non-negative multiple of 16");
+    if (src_offset < 0 || (src_offset & 15) != 0 || !src.ptr || ((uintptr_t)src.ptr & 15u) != 0)
+      fail(ANIMA_E_MISALIGNED, "read probe: the source must be 16-byte aligned");
+    if (checked_end(src_offset, bytes, "read probe") > src.length)
+      fail(ANIMA_E_OUT_OF_BOUNDS, "read probe: source range is out of bounds");
+    if (bytes == 0) return;
+    if (!sink.ptr || ((uintptr_t)sink.ptr & 15u) != 0 || sink.length < read_probe_sink_bytes(bytes))
+      fail(ANIMA_E_OUT_OF_BOUNDS, "read probe: sink must be 16-byte aligned and hold anima_read_probe_sink_bytes bytes");
+    DeviceGuard g(ctx);
+    launch_read_probe(static_cast<const char*>(src.ptr) + src_offset, bytes, sink.ptr, ctx->stream);
+  });
+}
+
+int64_t anima_read_probe_sink_bytes(int64_t bytes) { return bytes > 0 ? read_probe_sink_bytes(bytes) : 0; }
+
 // ---------------------------------------------------------------- DiT block support kernels
 
 anima_status anima_layernorm_modulate_to_half_encode(anima_ctx* ctx, anima_buffer residual, anima_buffer modulation,

@@ -49,6 +49,7 @@ inline int64_t checked_end(int64_t off, int64_t bytes, const char* what) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+inline bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
 inline const char* byte_ptr(const anima_buffer& b, int64_t off) {
   return static_cast<const char*>(b.ptr) + off;

@@ -554,4 +554,52 @@ void launch_matvec(const MatvecParams& p, hipStream_t stream) {
   launch_matvec_batch(&p, 1, stream);
 }
 
+// ---------------------------------------------------------------------------
+// Read probe: the achievable rate of a plain streaming read of `bytes` bytes, the
+// floor a weight-streaming kernel of the same byte count is measured against.  Every
+// thread XOR-folds 16-byte nontemporal loads (UNROLL in flight per iteration) and
+// each workgroup writes one 16-byte word to `sink`, so the probe reads exactly the
+// bytes asked and writes a few KB.
+// ---------------------------------------------------------------------------
+constexpr int PROBE_THREADS = 256, PROBE_UNROLL = 4, PROBE_MAX_BLOCKS = 2048;
+
+__global__ __launch_bounds__(PROBE_THREADS) void read_probe_kernel(const u32x4* src, int64_t chunks, u32x4* sink) {
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  const int64_t stride = (int64_t)gridDim.x * PROBE_THREADS;
+  int64_t i = (int64_t)blockIdx.x * PROBE_THREADS + threadIdx.x;
+  for (; i + (PROBE_UNROLL - 1) * stride < chunks; i += PROBE_UNROLL * stride) {
+    u32x4 v[PROBE_UNROLL];
+#pragma unroll
+    for (int u = 0; u < PROBE_UNROLL; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
+#pragma unroll
+    for (int u = 0; u < PROBE_UNROLL; ++u) acc ^= v[u];
+  }
+  for (; i < chunks; i += stride) acc ^= __builtin_nontemporal_load(src + i);
+  __shared__ u32x4 part[PROBE_THREADS];
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = PROBE_THREADS / 2; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) part[threadIdx.x] ^= part[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) sink[blockIdx.x] = part[0];
+}
+
+// One 16-byte chunk per thread up to PROBE_MAX_BLOCKS workgroups (small reads spread over
+// the whole chip), then grid-stride loops with PROBE_UNROLL loads in flight.
+int64_t read_probe_sink_bytes(int64_t bytes) {
+  const int64_t chunks = bytes / 16;
+  const int64_t blocks = std::min<int64_t>(PROBE_MAX_BLOCKS, std::max<int64_t>(1, (chunks + PROBE_THREADS - 1) / PROBE_THREADS));
+  return blocks * 16;
+}
+
+void launch_read_probe(const void* src, int64_t bytes, void* sink, hipStream_t stream) {
+  const int64_t chunks = bytes / 16;
+  if (chunks <= 0) return;
+  const int64_t blocks = read_probe_sink_bytes(bytes) / 16;
+  hipLaunchKernelGGL(read_probe_kernel, dim3((unsigned)blocks), dim3(PROBE_THREADS), 0, stream,
+                     static_cast<const u32x4*>(src), chunks, static_cast<u32x4*>(sink));
+  ANIMA_HIP(hipGetLastError());
+}
+
 }  // namespace anima

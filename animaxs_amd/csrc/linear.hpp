@@ -149,6 +149,10 @@ void launch_matvec(const MatvecParams& p, hipStream_t stream);
 // count (1..MV_BATCH) matvecs; one launch when they share storage and lane split.
 void launch_matvec_batch(const MatvecParams* ps, int count, hipStream_t stream);
 void launch_dequant(const DequantParams& p, hipStream_t stream);
+// Plain streaming read of `bytes` (a multiple of 16, 16-byte aligned); one 16-byte word per
+// workgroup goes to sink (read_probe_sink_bytes(bytes) bytes).
+int64_t read_probe_sink_bytes(int64_t bytes);
+void launch_read_probe(const void* src, int64_t bytes, void* sink, hipStream_t stream);
 
 class LinearExecutor {
  public:

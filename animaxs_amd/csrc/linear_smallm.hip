@@ -93,7 +93,7 @@ constexpr int smallm_max_chunks() {
   return STORAGE == ANIMA_STORAGE_W8 ? 1 : (MB <= 2 ? 2 : 1);
 }
 
-template <int STORAGE, int MB, int R, int NCH, int NST>
+template <int STORAGE, int MB, int R, int NCH, int NST, bool DIRECT>
 __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kernel(SmallMParams p) {
   constexpr int WORDS = SmallMChunk<STORAGE>::WORDS;
   // Dynamic LDS: the S x R*MB partial-sum tiles of the final reduction, then the
@@ -114,10 +114,15 @@ __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kerne
     const int n = min(n0 + rb * 16 + r, p.N - 1);
     wrow[rb] = p.w + (int64_t)n * p.row_stride * (STORAGE == ANIMA_STORAGE_FP16 ? 2 : 1);
   }
-  // Scale / zero of the workgroup's 16R rows are one contiguous run of the
-  // [N][groups] arrays: copy them into LDS with coalesced loads (lanes read
+  // Scale / zero.  With a short slice (DIRECT: at most 4 chunks per wave, K a multiple
+  // of 256) each lane loads its own rows' pairs straight into registers: chunk c of the
+  // slice uses group kslice/64 + 2c + g/2, so one 8-byte load of four consecutive groups
+  // serves two chunks, and the loads go out with the weight loads (one memory round trip
+  // before the MFMAs, no barrier).  Otherwise the workgroup's 16R rows are one contiguous
+  // run of the [N][groups] arrays, copied into LDS with coalesced loads (lanes read
   // consecutive halfs) rather than one scattered 2-byte load per lane and chunk.
   constexpr int PAIRS = R * MB;
+  constexpr int SLICE_CHUNKS = NCH * NST;
   half_t* s_lds = reinterpret_cast<half_t*>(red + S * PAIRS * 4 * 64);
   half_t* z_lds = s_lds + 16 * R * p.groups;
   const int nrows = min(16 * R, p.N - n0);
@@ -126,7 +131,27 @@ __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kerne
   // S x NCH x NST chunks of 128 covering K, is at most ceil(R x NCH x NST / 2) per thread.
   constexpr int PARAM_REGS = std::min(SM_PARAM_REGS, (R * NCH * NST + 1) / 2);
   half_t sreg[PARAM_REGS], zreg[PARAM_REGS];
-  if constexpr (STORAGE != ANIMA_STORAGE_FP16) {
+  // DIRECT: per row block, (SLICE_CHUNKS + 1) / 2 loads of 4 groups (one of 2 groups for a
+  // one-chunk slice) of scale and of zero.
+  constexpr int DLOADS = (SLICE_CHUNKS + 1) / 2;
+  uint64_t sdir[DIRECT ? R : 1][DIRECT ? DLOADS : 1], zdir[DIRECT ? R : 1][DIRECT ? DLOADS : 1];
+  if constexpr (DIRECT) {
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb) {
+      const int n = min(n0 + rb * 16 + r, p.N - 1);
+      const int64_t base = (int64_t)n * p.groups + kslice / 64;
+#pragma unroll
+      for (int q = 0; q < DLOADS; ++q) {
+        if constexpr (SLICE_CHUNKS == 1) {
+          sdir[rb][q] = *reinterpret_cast<const uint32_t*>(p.scale + base);
+          zdir[rb][q] = *reinterpret_cast<const uint32_t*>(p.zero + base);
+        } else {
+          sdir[rb][q] = *reinterpret_cast<const uint64_t*>(p.scale + base + 4 * q);
+          zdir[rb][q] = *reinterpret_cast<const uint64_t*>(p.zero + base + 4 * q);
+        }
+      }
+    }
+  } else if constexpr (STORAGE != ANIMA_STORAGE_FP16) {
     const half_t* sbase = p.scale + (int64_t)n0 * p.groups;
     const half_t* zbase = p.zero + (int64_t)n0 * p.groups;
 #pragma unroll
@@ -137,13 +162,16 @@ __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kerne
       zreg[i] = zbase[ec];
     }
   }
-  const half_t* xrow[MB];
-  bool xvalid[MB];
+  // X is read through one bounded buffer descriptor over its M x K halfs: lanes of rows
+  // past M (and chunks past the slice) get the offset xbytes, so their loads return
+  // zeros without touching memory (the load is still issued, which keeps the in-order
+  // load counter exact).  Rows past M are 15 of 16 lanes at M = 1.
+  const int xbytes = p.M * p.K * 2;
+  uint32_t xoff[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int m = mb * 16 + r;
-    xvalid[mb] = m < p.M;
-    xrow[mb] = p.x + (int64_t)(xvalid[mb] ? m : 0) * p.K;
+    xoff[mb] = m < p.M ? (uint32_t)m * (uint32_t)p.K * 2u : 0xffffffffu;
   }
 
   floatx4 acc[R][MB];
@@ -189,17 +217,14 @@ __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kerne
   // loaded from valid addresses and zeroed with a mask (no branch around the load).
   auto load_x = [&](int step, int c, half8v (&xf)[MB][4]) {
     const int kc = kslice + step * STEP_K + c * SM_CHUNK;
-    const uint32_t live = kc < kstop ? 0xffffffffu : 0u;
-    const int kl = min(kc, klast) + 32 * g;
+    const bool live = kc < kstop;
+    const uint32_t kb = (uint32_t)(kc + 32 * g) * 2u;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      const uint32_t mask = xvalid[mb] ? live : 0u;
+      const uint32_t base = live && xoff[mb] != 0xffffffffu ? xoff[mb] + kb : (uint32_t)xbytes;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        u32x4 v = *reinterpret_cast<const u32x4*>(xrow[mb] + kl + 8 * t);
-        v &= mask;
-        xf[mb][t] = __builtin_bit_cast(half8v, v);
-      }
+      for (int t = 0; t < 4; ++t)
+        xf[mb][t] = __builtin_bit_cast(half8v, load16_bounded(p.x, xbytes, base + 16u * t));
     }
   };
 
@@ -213,7 +238,14 @@ __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kerne
       half_t sc[R], zc[R];
 #pragma unroll
       for (int rb = 0; rb < R; ++rb) {
-        if constexpr (STORAGE != ANIMA_STORAGE_FP16) {
+        if constexpr (DIRECT) {
+          // Slice chunk i = step * NCH + c (chunks past the slice re-read its last one);
+          // its group is half (i % 2) * 2 + g / 2 of load i / 2.
+          const int i = min(step * NCH + c, (kstop - kslice) / SM_CHUNK - 1);
+          const int sh = 16 * ((i & 1) * 2 + (g >> 1));
+          sc[rb] = __builtin_bit_cast(half_t, (unsigned short)(sdir[rb][i >> 1] >> sh));
+          zc[rb] = __builtin_bit_cast(half_t, (unsigned short)(zdir[rb][i >> 1] >> sh));
+        } else if constexpr (STORAGE != ANIMA_STORAGE_FP16) {
           const int li = (rb * 16 + r) * p.groups + (kl >> 6);
           sc[rb] = s_lds[li];
           zc[rb] = z_lds[li];
@@ -251,25 +283,33 @@ __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kerne
   Step sa, sb;
   half8v xs[NCH][MB][4];
   load_step(0, sa);
-  // Park the scale/zero copy in LDS (waits only for those loads, issued before the
-  // weight loads) and make it visible to every wave.
-  if constexpr (STORAGE != ANIMA_STORAGE_FP16) {
+  if constexpr (DIRECT) {
+    // Everything step 0 needs is in flight at once: weights, scale/zero, X.
 #pragma unroll
-    for (int i = 0; i < PARAM_REGS; ++i) {
-      const int e = threadIdx.x + i * (int)blockDim.x;
-      if (e < nparam) {
-        s_lds[(e / p.groups) * p.groups + e % p.groups] = sreg[i];
-        z_lds[(e / p.groups) * p.groups + e % p.groups] = zreg[i];
+    for (int c = 0; c < NCH; ++c) load_x(0, c, xs[c]);
+  } else {
+    // Park the scale/zero copy in LDS (waits only for those loads, issued before the
+    // weight loads) and make it visible to every wave.
+    if constexpr (STORAGE != ANIMA_STORAGE_FP16) {
+#pragma unroll
+      for (int i = 0; i < PARAM_REGS; ++i) {
+        const int e = threadIdx.x + i * (int)blockDim.x;
+        if (e < nparam) {
+          s_lds[(e / p.groups) * p.groups + e % p.groups] = sreg[i];
+          z_lds[(e / p.groups) * p.groups + e % p.groups] = zreg[i];
+        }
       }
     }
+    __syncthreads();
   }
-  __syncthreads();
 #pragma unroll
   for (int step = 0; step < NST; ++step) {
     Step& cur = (step & 1) ? sb : sa;
     Step& nxt = (step & 1) ? sa : sb;
+    if (!DIRECT || step > 0) {
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) load_x(step, c, xs[c]);
+      for (int c = 0; c < NCH; ++c) load_x(step, c, xs[c]);
+    }
     if (step + 1 < NST) load_step(step + 1, nxt);
     compute_step(step, cur, xs);
   }
@@ -309,8 +349,19 @@ template <int STORAGE, int MB, int R, int NCH, int NST>
 static void launch_smallm_t(SmallMParams p, int S, hipStream_t stream) {
   p.kw = NCH * NST * SM_CHUNK;
   const int wgs = (p.N + 16 * R - 1) / (16 * R);
-  const size_t lds = (size_t)S * R * MB * 4 * 64 * sizeof(float) + (size_t)2 * 16 * R * p.groups * sizeof(half_t);
-  hipLaunchKernelGGL((smallm_gemm_kernel<STORAGE, MB, R, NCH, NST>), dim3(wgs), dim3(64 * S), lds, stream, p);
+  // Per-lane scale/zero loads: a slice of at most 4 chunks, every wave's slice whole (so
+  // its groups stay inside the row), and 8-byte aligned runs of 4 groups (rows of a
+  // multiple of 4 groups; a one-chunk slice needs 4-byte runs of 2).
+  constexpr bool SHORT = NCH * NST <= 4 && STORAGE != ANIMA_STORAGE_FP16;
+  const bool aligned = NCH * NST == 1 ? (p.groups % 2 == 0 && aligned4(p.scale) && aligned4(p.zero))
+                                      : (p.groups % 4 == 0 && aligned8(p.scale) && aligned8(p.zero));
+  if (SHORT && aligned && p.K % p.kw == 0) {
+    const size_t lds = (size_t)S * R * MB * 4 * 64 * sizeof(float);
+    hipLaunchKernelGGL((smallm_gemm_kernel<STORAGE, MB, R, NCH, NST, SHORT>), dim3(wgs), dim3(64 * S), lds, stream, p);
+  } else {
+    const size_t lds = (size_t)S * R * MB * 4 * 64 * sizeof(float) + (size_t)2 * 16 * R * p.groups * sizeof(half_t);
+    hipLaunchKernelGGL((smallm_gemm_kernel<STORAGE, MB, R, NCH, NST, false>), dim3(wgs), dim3(64 * S), lds, stream, p);
+  }
 }
 
 template <int STORAGE, int MB>
@@ -390,6 +441,7 @@ static bool smallm_fits(int M, int K) {
 
 bool smallm_supported(const GemmParams& p, int storage) {
   if (p.M < 1 || p.M > SMALLM_MAX_ROWS || p.K % SM_CHUNK != 0 || !aligned16(p.x) || !aligned16(p.w)) return false;
+  if ((int64_t)p.M * p.K * 2 > 0x7fffffff) return false;   // X is addressed with 32-bit buffer offsets
   if (storage == ANIMA_STORAGE_FP16) return p.row_stride % 8 == 0 && smallm_fits<ANIMA_STORAGE_FP16>(p.M, p.K);
   if (p.row_stride % 16 != 0) return false;
   return storage == ANIMA_STORAGE_W4 ? smallm_fits<ANIMA_STORAGE_W4>(p.M, p.K) : smallm_fits<ANIMA_STORAGE_W8>(p.M, p.K);

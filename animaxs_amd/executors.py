@@ -399,6 +399,17 @@ class DitRoPE:
         return out
 
 
+def read_probe_sink_bytes(nbytes: int) -> int:
+    """Bytes the read probe writes for a read of ``nbytes``."""
+    return int(_abi.load().anima_read_probe_sink_bytes(int(nbytes)))
+
+
+def read_probe(context: Context, src, nbytes: int, sink, src_offset: int = 0) -> None:
+    """A plain streaming read of ``nbytes`` of ``src`` (the measurement probe
+    anima_read_probe_encode): the floor for a weight-streaming kernel of that byte count."""
+    call("anima_read_probe_encode", context.handle, as_buffer(src), int(src_offset), int(nbytes), as_buffer(sink))
+
+
 def qwen_rope(tokens: int, head_dim: int = 128, theta: float = 1.0e6) -> np.ndarray:
     """QwenEncoderMetal.makeRope (QwenEncoderMetal.swift:126-143): fp32 [tokens, hd/2, 2, 2]."""
     out = np.zeros((tokens, head_dim // 2, 2, 2), np.float32)

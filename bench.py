@@ -398,6 +398,20 @@ def calibration_copies(torch):
     torch.cuda.synchronize()
 
 
+def read_floor_ms(torch, A, ctx, nbytes, nsets):
+    """ms per call of a plain streaming read of ``nbytes`` (the library's read probe),
+    rotating over ``nsets`` disjoint buffers and replayed from a HIP graph exactly like the
+    small-M GEMM it is the floor of."""
+    per = -(-nbytes // 256) * 256
+    buf = torch.empty(per * nsets, dtype=torch.uint8, device="cuda")
+    buf.random_(0, 256)
+    sink = torch.empty(A.read_probe_sink_bytes(per), dtype=torch.uint8, device="cuda")
+    nb = -(-nbytes // 16) * 16
+    ms = time_graph(torch, ctx, lambda i: A.read_probe(ctx, buf, nb, sink, src_offset=(i % nsets) * per), nsets)
+    del buf
+    return ms
+
+
 def gemm_weight_sets(torch, A, N, K, min_bytes=600 << 20):
     """Rotating W4 weight sets (random codes, group-64 scales, zero = -8 * scale) whose
     total exceeds the 256 MB Infinity Cache."""
@@ -542,11 +556,17 @@ def other_workloads(torch, A, ctx, stream, args):
             ms = time_region(torch, stream, call, max(args.steps, nsets), args.warmup)
         byts = N * K / 2 + 2 * 2 * N * (K // 64) + 2 * M * K + 2 * M * N
         f = 2.0 * M * N * K
-        res[f"w4_gemm_m{M}_n{N}_k{K}"] = {"ms": round(ms, 5), "gbs": round(byts / ms / 1e6, 1),
-                                          "hbm_frac": round(byts / ms / 1e6 / HBM_PEAK_GBS, 4),
-                                          "tflops": round(f / ms / 1e9, 2),
-                                          "mfma_frac": round(f / ms / 1e9 / FP16_PEAK_TFLOPS, 4)}
+        entry = {"ms": round(ms, 5), "gbs": round(byts / ms / 1e6, 1),
+                 "hbm_frac": round(byts / ms / 1e6 / HBM_PEAK_GBS, 4),
+                 "tflops": round(f / ms / 1e9, 2),
+                 "mfma_frac": round(f / ms / 1e9 / FP16_PEAK_TFLOPS, 4)}
         del ws
+        if M <= 64:
+            floor_ms = read_floor_ms(torch, A, ctx, int(byts), nsets)
+            entry["copy_floor_us"] = round(floor_ms * 1e3, 3)
+            entry["copy_floor_gbs"] = round(byts / floor_ms / 1e6, 1)
+            entry["vs_copy_floor"] = round(ms / floor_ms, 3)
+        res[f"w4_gemm_m{M}_n{N}_k{K}"] = entry
     for k_, v_ in res.items():
         print(f"# {k_}: {v_}", file=sys.stderr, flush=True)
     return res

@@ -340,6 +340,15 @@ anima_status anima_dequant_to_half_encode(anima_ctx* ctx, const anima_qweight* w
                                           anima_buffer output, int64_t output_offset,
                                           int64_t out_row_stride);
 
+/* No counterpart in the reference (a measurement probe, like its diagnostics):
+ * a plain streaming read of `bytes` bytes of src (16-byte aligned, a multiple of
+ * 16) that writes anima_read_probe_sink_bytes(bytes) bytes to sink.  It times the
+ * achievable rate of reading a given number of bytes, the floor a weight-streaming
+ * GEMM of the same byte count is compared with. */
+anima_status anima_read_probe_encode(anima_ctx* ctx, anima_buffer src, int64_t src_offset, int64_t bytes,
+                                     anima_buffer sink);
+int64_t anima_read_probe_sink_bytes(int64_t bytes);
+
 /* ------------------------------------------------------------------------- */
 /* CPU decoders: QuantDecoders (QuantDecoders.swift:17-164).                   */
 /* scale/zero are raw binary16 payloads; outputs are fp32.                     */

@@ -302,7 +302,8 @@ def _affine_weight(storage: int, N: int, K: int, seed: int, pad: int = 0) -> dic
 @pytest.mark.parametrize("storage", [0, 1, 2])
 @pytest.mark.parametrize("M,N,K,pad", [(1, 2048, 2048, 0), (5, 1000, 384, 16), (16, 8192, 2048, 0),
                                        (17, 130, 1280, 32), (33, 2048, 1024, 0), (64, 2048, 8192, 0),
-                                       (64, 4000, 2048, 16), (64, 8192, 2048, 0), (40, 8200, 1024, 16)])
+                                       (64, 4000, 2048, 16), (64, 8192, 2048, 0), (40, 8200, 1024, 16),
+                                       (3, 1004, 1024, 0), (1, 2052, 8192, 0), (16, 2048, 8192, 16)])
 def test_small_m_weight_stream_gemm(ctx, storage, M, N, K, pad):
     """M <= 64 with K a multiple of 128 takes the weight-streaming kernel: every storage, ragged N,
     padded row strides; the output's neighbours stay untouched."""
@@ -365,12 +366,14 @@ def _one_hot_params(rng, N: int, groups: int) -> tuple:
 
 
 @pytest.mark.parametrize("storage", [0, 1])
-@pytest.mark.parametrize("M", [64, 128])
+@pytest.mark.parametrize("M", [5, 16, 64, 128])
 def test_gemm_dequant_bit_exact_via_one_hot(ctx, storage, M):
     """Row m of X is one-hot at column k_m, so y[m, n] = deq(W)[n, k_m] exactly (a single
     1*w product in fp32): the GEMM's in-register dequantization must reproduce the oracle's
     RNE16(fl32(q*s + z)) bit for bit, including the fallback taken when q*s + z is not exact in
-    fp32.  M=64 runs the weight-streaming kernel, M=128 the tiled GEMM."""
+    fp32.  M=5 and 16 run the weight-streaming kernel with per-lane scale/zero loads (and X rows
+    past M read as zeros through the bounded loads), M=64 that kernel with scale/zero staged in
+    LDS, M=128 the tiled GEMM."""
     rng = np.random.default_rng(40 + storage + M)
     N, K = 384, 1024
     groups = K // 64
