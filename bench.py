@@ -56,6 +56,12 @@ def parse():
     ap.add_argument("--profile-vae", action="store_true",
                     help="only the VAE mid-block attention (1 head, head_dim 384, 4096 positions), settle + "
                          "--warmup + --steps calls; for a rocprofv3 kernel trace")
+    ap.add_argument("--profile-c1", action="store_true",
+                    help="only workload 1 (S=1024 self-attention, key splits + merge), settle + --warmup + --steps "
+                         "calls, then the calibration copies; for rocprofv3")
+    ap.add_argument("--profile-c3", action="store_true",
+                    help="only workload 3 (B4 masked cross attention), settle + --warmup + --steps calls, then the "
+                         "calibration copies; for rocprofv3")
     ap.add_argument("--counter-summary", metavar="CSV",
                     help="no GPU: per-dispatch means of a rocprofv3 --pmc counter_collection.csv, per kernel "
                          "(last --trace-last dispatches of each) and exit")
@@ -254,8 +260,8 @@ def main():
     print(f"# device {dev_name}", file=sys.stderr, flush=True)
 
     if args.profile_block:
-        ms = time_block(torch, A, ctx, stream, args)
-        print(f"# profile-block: DiT block S4096 {ms:.3f} ms", file=sys.stderr)
+        blk = time_block(torch, A, ctx, stream, args)
+        print(f"# profile-block: DiT block S4096 {blk['ms']:.3f} ms ({blk['timing']})", file=sys.stderr)
         return
     if args.profile_gemm:
         profile_gemm(torch, A, ctx, stream, args, *(int(x) for x in args.profile_gemm.split(",")))
@@ -263,6 +269,13 @@ def main():
     if args.profile_vae:
         ms = time_region(torch, stream, vae_attention_call(torch, A, ctx), args.steps, args.warmup)
         print(f"# profile-vae: {ms * 1e3:.2f} us per call (HIP events, {args.steps} timed calls)", file=sys.stderr)
+        return
+    if args.profile_c1 or args.profile_c3:
+        fn = c1_call(torch, A, ctx) if args.profile_c1 else c3_call(torch, A, ctx)[0]
+        ms = time_region(torch, stream, fn, args.steps, args.warmup)
+        calibration_copies(torch)
+        print(f"# profile-{'c1' if args.profile_c1 else 'c3'}: {ms * 1e3:.2f} us per call (HIP events, {args.steps} "
+              "timed calls), then 3 x 256 MiB copies", file=sys.stderr)
         return
     if args.profile_step:
         st_ms, first_ms, fwd_ms, finite = time_sampler_step(torch, A, ctx, stream, args)
@@ -335,8 +348,10 @@ def main():
 
     block_ms = None
     if not args.no_block:
-        block_ms = time_block(torch, A, ctx, stream, args)
-        print(f"# DiT block S4096: {block_ms:.3f} ms", file=sys.stderr, flush=True)
+        blk = time_block(torch, A, ctx, stream, args)
+        block_ms = blk["ms"]
+        extra["dit_block_s4096"] = blk
+        print(f"# DiT block S4096: {blk}", file=sys.stderr, flush=True)
         qwen = time_qwen_layer(torch, A, ctx, stream, args)
         extra["qwen_layer_b4_s512"] = qwen
         print(f"# Qwen layer B4 S512: {qwen}", file=sys.stderr, flush=True)
@@ -449,23 +464,21 @@ def load_traffic():
     return None
 
 
-def other_workloads(torch, A, ctx, stream, args):
-    """ms/call and throughput of the other attention workloads (parity configs) and the
-    small-M W4 GEMMs, each against its binding roofline."""
-    res = {}
+def c1_call(torch, A, ctx):
+    """Workload 1: DiT self-attention at 512 px, B1 H16 D128 S1024, no norm / RoPE."""
     g = torch.Generator(device="cuda")
     g.manual_seed(1001)
-    # workload 1: S=1024 plain self-attention
     q, k, v = (torch.randn(1, 1024, H, D, device="cuda", generator=g).half() for _ in range(3))
     o = torch.empty_like(q)
     ex = A.AttentionExecutor(ctx, layout=("tokenMajor", H * D), backend="flash")
-    t = time_calls(torch, stream, lambda i: ex.encode(query=q, key=k, value=v, output=o, heads=H, query_count=1024,
-                                                      key_count=1024, head_dim=D), args.steps, args.warmup)
-    ms = t["mean_ms"]
-    f = attn_flops(1024, 1024)
-    res["self_attention_s1024"] = {"ms": round(ms, 5), "tflops": round(f / ms / 1e9, 2),
-                                   "mfma_frac": round(f / ms / 1e9 / FP16_PEAK_TFLOPS, 4), "timing": t}
-    # workload 3: cross attention B4, 4096 queries, 512 keys, masked, q/k RMSNorm
+    return lambda i: ex.encode(query=q, key=k, value=v, output=o, heads=H, query_count=1024, key_count=1024,
+                               head_dim=D)
+
+
+def c3_call(torch, A, ctx):
+    """Workload 3: DiT cross attention, B4, 4096 queries over 512 context keys with per-image
+    key lengths, per-head Q/K RMSNorm; 4 rotating input sets.  Returns (call, lengths, norm weight)."""
+    g = torch.Generator(device="cuda")
     g.manual_seed(1003)
     sets = []
     for _ in range(4):
@@ -482,7 +495,22 @@ def other_workloads(torch, A, ctx, stream, args):
         q, k, v, o = sets[i % 4]
         ex3.encode(query=q, key=k, value=v, output=o, heads=H, query_count=4096, key_count=512, head_dim=D, batch=4,
                    key_lengths=lengths, prologue=pro)
+    return s3, lengths, nw
 
+
+def other_workloads(torch, A, ctx, stream, args):
+    """ms/call and throughput of the other attention workloads (parity configs) and the
+    small-M W4 GEMMs, each against its binding roofline."""
+    res = {}
+    g = torch.Generator(device="cuda")
+    # workload 1: S=1024 plain self-attention
+    t = time_calls(torch, stream, c1_call(torch, A, ctx), args.steps, args.warmup)
+    ms = t["mean_ms"]
+    f = attn_flops(1024, 1024)
+    res["self_attention_s1024"] = {"ms": round(ms, 5), "tflops": round(f / ms / 1e9, 2),
+                                   "mfma_frac": round(f / ms / 1e9 / FP16_PEAK_TFLOPS, 4), "timing": t}
+    # workload 3: cross attention B4, 4096 queries, 512 keys, masked, q/k RMSNorm
+    s3, lengths, nw = c3_call(torch, A, ctx)
     t = time_calls(torch, stream, s3, args.steps, args.warmup)
     ms = t["mean_ms"]
     L = [int(x) for x in lengths]
@@ -511,8 +539,10 @@ def other_workloads(torch, A, ctx, stream, args):
     f = 4.0 * D * 16 * pairs
     byts = (4 * 16 * 512 * D * 2) * 2 + (4 * 8 * 512 * D * 2) * 2
     res["qwen_causal_gqa_b4_s512_per_layer"] = {"ms": round(ms, 5), "tflops": round(f / ms / 1e9, 2),
-                                                "gbs": round(byts / ms / 1e6, 1), "key_lengths": [int(x) for x in lens],
-                                                "timing": t}
+                                                "gbs": round(byts / ms / 1e6, 1),
+                                                "hbm_frac": round(byts / ms / 1e6 / HBM_PEAK_GBS, 4),
+                                                "mfma_frac": round(f / ms / 1e9 / FP16_PEAK_TFLOPS, 4),
+                                                "key_lengths": [int(x) for x in lens], "timing": t}
     # VAE decoder mid-block attention: one head, head_dim 384, 4096 positions (64x64 latent),
     # Q/K/V contiguous [4096, 384] (VAEDecoder.swift:396-404); 4 rotating input sets
     t = time_calls(torch, stream, vae_attention_call(torch, A, ctx), args.steps, args.warmup)
@@ -594,10 +624,17 @@ def time_block(torch, A, ctx, stream, args):
     shapes = {"self_q": (dim, dim), "self_k": (dim, dim), "self_v": (dim, dim), "self_o": (dim, dim),
               "cross_q": (dim, dim), "cross_k": (dim, C), "cross_v": (dim, C), "cross_o": (dim, dim),
               "mlp1": (hidden, dim), "mlp2": (dim, hidden)}
-    weights = {n: w4(*s) for n, s in shapes.items()}
-    for br in ("self", "cross", "mlp"):
-        weights[f"mod_{br}_w1"] = f16(256, dim)
-        weights[f"mod_{br}_w2"] = f16(3 * dim, 256)
+
+    def block_weights():
+        weights = {n: w4(*s) for n, s in shapes.items()}
+        for br in ("self", "cross", "mlp"):
+            weights[f"mod_{br}_w1"] = f16(256, dim)
+            weights[f"mod_{br}_w2"] = f16(3 * dim, 256)
+        return weights
+
+    # Eight weight sets (about 8 x 38 MB, more than the 256 MB Infinity Cache) taken in turn,
+    # as consecutive blocks of the forward read different weights from HBM.
+    wsets = [block_weights() for _ in range(8)]
     norms = {n: (0.8 + 0.4 * torch.rand(128, device="cuda", generator=g)).half()
              for n in ("self_q_norm", "self_k_norm", "cross_q_norm", "cross_k_norm")}
     residual = torch.randn(S, dim, device="cuda", generator=g)
@@ -608,9 +645,20 @@ def time_block(torch, A, ctx, stream, args):
     blk = A.DiTBlockExecutor(ctx)
 
     def step(i):
-        blk.encode(weights, norms, residual, emb, adaln, ctxt, rope, tokens=S)
+        blk.encode(wsets[i % len(wsets)], norms, residual, emb, adaln, ctxt, rope, tokens=S)
 
-    return time_region(torch, stream, step, args.block_steps, 2)
+    t = time_calls(torch, stream, step, max(args.block_steps, 16), 2)
+    f = block_flops()
+    return {"ms": t["mean_ms"], "tflops": round(f / t["mean_ms"] / 1e9, 2),
+            "mfma_frac": round(f / t["mean_ms"] / 1e9 / FP16_PEAK_TFLOPS, 4), "gflop": round(f / 1e9, 2),
+            "weight_sets": len(wsets), "timing": t}
+
+
+def block_flops(S_=4096, T=512, dim=2048, C=1024, hidden=8192, heads=16, hd=128):
+    """Algorithmic FLOPs of one DiT block: the ten linears plus self and cross attention."""
+    lin = 2 * S_ * dim * dim * 6 + 2 * T * dim * C * 2 + 2 * S_ * dim * hidden * 2
+    att = 4 * heads * hd * S_ * S_ + 4 * heads * hd * S_ * T
+    return float(lin + att)
 
 
 def time_sampler_step(torch, A, ctx, stream, args, blocks=28):
@@ -726,7 +774,7 @@ def time_qwen_layer(torch, A, ctx, stream, args):
     lin = 2 * rows * sum(n * k for n, k in shapes.values())
     att = sum(2 * D * L * (L + 1) for L in lengths) * H
     return {"ms": round(ms, 5), "tflops": round((lin + att) / ms / 1e9, 2), "gflop": round((lin + att) / 1e9, 2),
-            "key_lengths": lengths}
+            "mfma_frac": round((lin + att) / ms / 1e9 / FP16_PEAK_TFLOPS, 4), "key_lengths": lengths}
 
 
 def _host_info():
