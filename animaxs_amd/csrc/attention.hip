@@ -682,7 +682,18 @@ void launch_flash(FlashParams p, int D, int batch, int flash_rows, hipStream_t s
   if (blocks > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "attention grid too large");
   const dim3 grid((unsigned)blocks);
   if (v2) {
-    launch_flash_v2(p, D, grid, stream);
+    // Batched non-causal calls without Q RoPE whose query tiles x heads fill whole
+    // rounds of the chip run persistent: one workgroup per (query tile, head) walks the
+    // batch entries, so an entry's Q rows and first tiles load behind the previous
+    // entry's key loop and epilogue (the same number of rounds as one workgroup per
+    // entry, balanced because every workgroup takes the same entries in order).
+    const int64_t qh = (int64_t)p.q_tiles * p.H;
+    const bool persist = batch >= 2 && !p.causal && !p.rope && qh % F2_MIN_BLOCKS == 0 &&
+                         flash_v2_persist_fits(p, D);
+    if (persist)
+      launch_flash_v2(p, D, dim3((unsigned)qh), stream, true);
+    else
+      launch_flash_v2(p, D, grid, stream);
   } else {
     if (p.nbatch < 1 || p.H < 1 || blocks != (int64_t)p.q_tiles * p.H * p.nbatch)
       fail(ANIMA_E_INVALID_ARGUMENT, "flash attention grid does not match its tiles, heads and batch");

@@ -65,7 +65,10 @@ constexpr int FLASH_WIDE_ROWS = 128;
 // Most key splits of one attention call (flash_kv_splits); the merge holds them all.
 constexpr int FLASH_MAX_SPLITS = 8;
 void launch_flash_wide(const FlashParams& p, int D, dim3 grid, hipStream_t stream);
-void launch_flash_v2(const FlashParams& p, int D, dim3 grid, hipStream_t stream);
+// persist: grid of q_tiles x H workgroups, each walking the batch entries of its query
+// tile and head (no Q RoPE, no key splits, flash_v2_persist_fits).
+void launch_flash_v2(const FlashParams& p, int D, dim3 grid, hipStream_t stream, bool persist = false);
+bool flash_v2_persist_fits(const FlashParams& p, int D);
 void launch_flash_combine(const FlashParams& p, int D, int batch, hipStream_t stream);
 void launch_generic(const FlashParams& p, int D, int batch, hipStream_t stream);
 void launch_legacy_mps(const FlashParams& p, int D, int batch, hipStream_t stream);

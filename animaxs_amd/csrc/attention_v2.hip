@@ -51,9 +51,23 @@ constexpr int F2_BN = 64;
 constexpr int F2_STAGES = 4;
 constexpr float F2_LAZY_LIMIT = 32768.f;   // largest tile row-sum share the fast path accepts
 constexpr int F2_READ_AHEAD = 4;    // MFMA operand fragments read from LDS ahead of their MFMA
+// PERSIST: the next batch entry's Q rows load in the key loop's last two tile periods
+// (true) or after the key loop, behind the epilogue (false).
+constexpr bool F2_Q_PREFETCH = true;
 static_assert(FLASH_V2_ROWS == 32 * F2_WAVES, "one 32-row block per wave");
 
-template <int D>
+// PERSIST: the grid covers query tiles x heads and every workgroup walks all batch entries
+// of its (tile, head), so the work per workgroup is the same.  The workgroups of head h
+// start at entry h % nbatch: at any moment the heads are spread over entries of different
+// key lengths, so their Q-row loads and O-row stores do not all fall at the same time.
+// Across entries the next entry's Q rows load into the tile-staging registers in this
+// entry's last two tile periods, and its first two K/V tiles load before this entry's
+// epilogue, so neither the Q rows' HBM round trip nor the first tiles' wait is paid again
+// per entry (measured on a B4 cross attention, 4096 queries over 418/506/86/149 keys: the
+// Q wait went from 4.9 us to the 2.7 us of the fragment's own norm and barriers).
+// Requires no fused Q RoPE, no key splits and the per-(batch, head) Q rows within 2 GiB
+// (launch_flash_v2 checks).
+template <int D, bool PERSIST = false>
 __global__ __launch_bounds__(F2_NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void flash_attention_v2_kernel(FlashParams p) {
   constexpr int DCH = D / 8;             // 16-byte data chunks per row
@@ -84,11 +98,7 @@ void flash_attention_v2_kernel(FlashParams p) {
     else return V3;
   };
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c32 = lane & 31, hh = lane >> 5;
-  const int jj = lane & 15, gg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   // Waves w and w+4 share a SIMD; one of them is in each group.
   const int group = wave >> 2;
 
@@ -103,30 +113,64 @@ void flash_attention_v2_kernel(FlashParams p) {
   // lengths spread evenly over the XCDs.
   const int qt = lb % p.q_tiles;
   lb /= p.q_tiles;
-  const int b = lb % p.nbatch;
-  const int head = lb / p.nbatch;
+  const int head = PERSIST ? lb : lb / p.nbatch;
+  // PERSIST: the workgroups of head h start at entry h % nbatch and wrap around, so at any
+  // time the heads are spread over the entries (of different key lengths) and their Q-row
+  // loads and O-row stores do not all fall at the same moment.
+  int b = PERSIST ? head % p.nbatch : lb % p.nbatch;
   const int kvh = head / p.group;
   const int q0 = qt * FLASH_V2_ROWS;
   const int wq0 = q0 + wave * 32;
-  const int qi = wq0 + c32;
-
-  int kv_len = p.Sk;
-  if (p.key_lengths_dev) {
-    int L = p.key_lengths_dev[b];
-    kv_len = L < 1 ? 1 : (L > p.Sk ? p.Sk : L);
-  } else if (p.use_host_lengths) {
-    kv_len = p.host_lengths[b];
-  }
   // With key splits (non-causal, no key lengths) this workgroup's keys start at kofs;
   // kv_len and kend count keys from there.
   const int kofs = p.kv_splits > 1 ? split * p.kv_chunk : 0;
-  if (p.kv_splits > 1) kv_len = max(0, min(kv_len, kofs + p.kv_chunk) - kofs);
-  int kend = kv_len;
-  if (p.causal) kend = min(kend, q0 + FLASH_V2_ROWS);
-  const int ntiles = (kend + F2_BN - 1) / F2_BN;
+  // Valid keys of batch entry bb, and the keys this workgroup uses of them.
+  auto entry_kv_len = [&](int bb) __attribute__((always_inline)) -> int {
+    int len = p.Sk;
+    if (p.key_lengths_dev) {
+      int L = p.key_lengths_dev[bb];
+      len = L < 1 ? 1 : (L > p.Sk ? p.Sk : L);
+    } else if (p.use_host_lengths) {
+      len = p.host_lengths[bb];
+    }
+    if (p.kv_splits > 1) len = max(0, min(len, kofs + p.kv_chunk) - kofs);
+    return len;
+  };
+  auto entry_kend = [&](int len) __attribute__((always_inline)) -> int {
+    return p.causal ? min(len, q0 + FLASH_V2_ROWS) : len;
+  };
+  auto entry_k = [&](int bb) __attribute__((always_inline)) -> const char* {
+    return reinterpret_cast<const char*>(p.k + (int64_t)bb * p.k_batch + (int64_t)kvh * p.k_head + (int64_t)kofs * p.k_tok);
+  };
+  auto entry_v = [&](int bb) __attribute__((always_inline)) -> const char* {
+    return reinterpret_cast<const char*>(p.v + (int64_t)bb * p.v_batch + (int64_t)kvh * p.v_head + (int64_t)kofs * p.v_tok);
+  };
 
-  const half_t* kbase = p.k + (int64_t)b * p.k_batch + (int64_t)kvh * p.k_head + (int64_t)kofs * p.k_tok;
-  const half_t* vbase = p.v + (int64_t)b * p.v_batch + (int64_t)kvh * p.v_head + (int64_t)kofs * p.v_tok;
+  constexpr int CPT = F2_BN * DCH / F2_NT;   // chunks per thread per tensor per tile
+  constexpr int RSTEP = F2_NT / DCH;
+  constexpr int NCP = 2 * CPT;               // copies per thread per tile: K chunks, then V chunks
+  static_assert(CPT * F2_NT == F2_BN * DCH && F2_NT % DCH == 0, "tile splits evenly over the threads");
+  // Carried from one batch entry to the next (PERSIST): the tile-staging registers (the
+  // next entry's tiles 0 and 1 in flight), its Q rows and the Q norm weight piece.
+  u32x4 stg2[2][NCP];
+  half8v qf[QS];
+  uint32_t wn = 0;
+
+  for (int entry = 0;; ++entry) {   // batch entries (one pass unless PERSIST)
+  // The lane index is re-derived per entry behind an empty asm so that per-lane values
+  // are computed in the entry that uses them instead of living across all entries.
+  int tid = threadIdx.x;
+  if constexpr (PERSIST) asm volatile("" : "+v"(tid));
+  const int lane = tid & 63;
+  const int c32 = lane & 31, hh = lane >> 5;
+  const int jj = lane & 15, gg = lane >> 4;
+  const int qi = wq0 + c32;
+  const int kv_len = entry_kv_len(b);
+  const int kend = entry_kend(kv_len);
+  const int ntiles = (kend + F2_BN - 1) / F2_BN;
+  const char* const kbase = entry_k(b);
+  const char* const vbase = entry_v(b);
+  uint64_t rp[QStage<D>::LOADS];   // RoPE table pieces (never with PERSIST)
 
   // Tile copies: thread t moves the 16-byte chunks t + F2_NT*r (r < CPT) of the K
   // tile and of the V tile (chunk -> row, column: 16-lane coalesced rows in
@@ -136,10 +180,6 @@ void flash_attention_v2_kernel(FlashParams p) {
   // past it, and every row of a tile past the last one, read as zeros without
   // touching memory.  64 key rows fit in 2^31 bytes (checked on the host), so the
   // per-lane offsets and sizes are 32-bit.
-  constexpr int CPT = F2_BN * DCH / F2_NT;   // chunks per thread per tensor per tile
-  constexpr int RSTEP = F2_NT / DCH;
-  constexpr int NCP = 2 * CPT;               // copies per thread per tile: K chunks, then V chunks
-  static_assert(CPT * F2_NT == F2_BN * DCH && F2_NT % DCH == 0, "tile splits evenly over the threads");
   const int crow = tid / DCH, cch = tid % DCH;
   const uint32_t ktok2 = (uint32_t)p.k_tok * 2u, vtok2 = (uint32_t)p.v_tok * 2u;
   uint32_t goff_k[CPT], goff_v[CPT];
@@ -165,7 +205,6 @@ void flash_attention_v2_kernel(FlashParams p) {
   // Copies go global -> VGPR -> LDS: load_tile fetches this thread's chunks of a tile
   // into staging buffer j % 2, store_seg writes copy r into a stage two tile
   // periods later (two buffers keep two tiles in flight).
-  u32x4 stg2[2][NCP];
   auto load_at = [&](const char* kt, int nk, const char* vt, int nv, auto bufc) __attribute__((always_inline)) {
     u32x4 (&stg)[NCP] = stg2[decltype(bufc)::value];
 #pragma unroll
@@ -174,16 +213,51 @@ void flash_attention_v2_kernel(FlashParams p) {
     for (int r = 0; r < CPT; ++r) stg[CPT + r] = load16_bounded(vt, nv, goff_v[r]);
   };
   auto load_tile = [&](int j, auto bufc) __attribute__((always_inline)) {
-    load_at(reinterpret_cast<const char*>(kbase) + j * kstep, clamp_bytes(kbytes - j * kstep),
-            reinterpret_cast<const char*>(vbase) + j * vstep, clamp_bytes(vbytes - j * vstep), bufc);
+    load_at(kbase + j * kstep, clamp_bytes(kbytes - j * kstep), vbase + j * vstep, clamp_bytes(vbytes - j * vstep), bufc);
   };
-  const char* k_next = reinterpret_cast<const char*>(kbase) + 4 * kstep;
-  const char* v_next = reinterpret_cast<const char*>(vbase) + 4 * vstep;
+  const char* k_next = kbase + 4 * kstep;
+  const char* v_next = vbase + 4 * vstep;
   int64_t k_rem = kbytes - 4 * kstep, v_rem = vbytes - 4 * vstep;
   auto load_next = [&](auto bufc) __attribute__((always_inline)) {
     load_at(k_next, clamp_bytes(k_rem), v_next, clamp_bytes(v_rem), bufc);
     k_next += kstep; v_next += vstep;
     k_rem -= kstep; v_rem -= vstep;
+  };
+  // PERSIST: this entry's load stream is its tiles 0 .. ntiles-1 (positions 0 .. ntiles-1,
+  // zero-size loads at ntiles and ntiles+1), then the next entry's Q rows in two parts of
+  // NCP loads at positions qa = ntiles+2 and qa+1: the last two loads of the stream, so
+  // nothing overwrites their staging buffers (position pos lands in buffer pos % 2) before
+  // the key loop ends.  Q row loads follow issue_q_loads (load t moves rows
+  // t * 64/QLPR + lane/QLPR, rows past the sequence repeat the last row) through one
+  // descriptor over the (batch, head) rows.
+  constexpr int QLPR = QStage<D>::QLPR;
+  static_assert(QS == 2 * NCP, "one Q part fills one staging buffer");
+  const uint32_t qtok2 = (uint32_t)p.q_tok * 2u;
+  const int qnbytes = (int)((uint32_t)(p.Sq - 1) * qtok2 + D * 2);
+  auto next_entry = [&]() __attribute__((always_inline)) { return PERSIST && entry + 1 < p.nbatch; };
+  const int bn = b + 1 == p.nbatch ? 0 : b + 1;   // next entry (PERSIST)
+  auto load_q_part = [&](int part, auto bufc) __attribute__((always_inline)) {
+    u32x4 (&stg)[NCP] = stg2[decltype(bufc)::value];
+    const char* qb = reinterpret_cast<const char*>(p.q + (int64_t)bn * p.q_batch + (int64_t)head * p.q_head);
+#pragma unroll
+    for (int r = 0; r < NCP; ++r) {
+      const int row = min(wq0 + (NCP * part + r) * (64 / QLPR) + lane / QLPR, p.Sq - 1);
+      stg[r] = load16_bounded(qb, qnbytes, (uint32_t)row * qtok2 + (uint32_t)(lane % QLPR) * 16u);
+    }
+  };
+  // Load of stream position pos into buffer pos % 2; FIRST: one of positions 0..3 (by
+  // tile index), else the next tile of the running pointers.
+  auto load_slot = [&](int pos, auto bufc, auto first) __attribute__((always_inline)) {
+    if constexpr (PERSIST) {
+      if (F2_Q_PREFETCH && next_entry() && pos >= ntiles + 2) {
+        load_q_part(pos - ntiles - 2, bufc);
+        return;
+      }
+    }
+    if constexpr (decltype(first)::value)
+      load_tile(pos, bufc);
+    else
+      load_next(bufc);
   };
   auto store_seg = [&](int r, auto st, auto bufc) __attribute__((always_inline)) {
     u32x4 (&stg)[NCP] = stg2[decltype(bufc)::value];
@@ -196,8 +270,6 @@ void flash_attention_v2_kernel(FlashParams p) {
 #pragma unroll
     for (int r = 0; r < NCP; ++r) store_seg(r, st, bufc);
   };
-
-  half8v qf[QS];   // filled in the prologue below, beside the first tile loads
 
   floatx16 acc[OB];
 #pragma unroll
@@ -309,8 +381,8 @@ void flash_attention_v2_kernel(FlashParams p) {
   auto x_phase = [&](int j, auto st) __attribute__((always_inline)) {
     using SW = std::integral_constant<int, (decltype(st)::value + 2) % F2_STAGES>;
     using BUF = std::integral_constant<int, decltype(st)::value % 2>;
-    store_tile(SW{}, BUF{});   // tile j+2
-    load_next(BUF{});          // tile j+4 (all zeros past the last tile)
+    store_tile(SW{}, BUF{});   // tile j+2 (never one of the next entry's Q parts)
+    load_slot(j + 4, BUF{}, std::false_type{});   // tile j+4 (all zeros past the last tile)
     const int k0 = j * F2_BN;
     if ((k0 + F2_BN > kv_len) || (p.causal && k0 + F2_BN - 1 > wq0)) {
 #pragma unroll
@@ -390,29 +462,32 @@ void flash_attention_v2_kernel(FlashParams p) {
   using B1 = std::integral_constant<int, 1>;
   // Prologue: the loads of the Q rows, of the Q norm weight, of the RoPE table rows and
   // of tiles 0 and 1 are all in flight together, so the workgroup pays one memory round
-  // trip before its first MFMA instead of three.
+  // trip before its first MFMA instead of three.  A later batch entry (PERSIST) finds its
+  // Q rows in qf and its tiles 0 and 1 in flight, loaded during the previous entry.
+  half_t* const rreg = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? K2 : wave == 3 ? K3
+                     : wave == 4 ? V0 : wave == 5 ? V1 : wave == 6 ? V2 : V3;
   {
     // The Q loads go first (they are on the critical path), then tiles 0 and 1.  The Q
     // rows, the Q norm weight and the RoPE table rows are staged through LDS
     // (finish_q_fragment): waves 0-3 use K stages 0-3, waves 4-7 V stages 0-3, all free
     // until the tile stores below, which wait behind one barrier for every wave's
-    // staged reads.
+    // staged reads (and, in a later entry, behind one for the previous entry's O rows).
     static_assert(QStage<D>::BYTES <= KTILE * 2 && QStage<D>::BYTES <= VTILE * 2, "Q staging fits a stage");
-    half_t* const rreg = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? K2 : wave == 3 ? K3
-                       : wave == 4 ? V0 : wave == 5 ? V1 : wave == 6 ? V2 : V3;
-    uint32_t wn = 0;
-    uint64_t rp[QStage<D>::LOADS];
-    issue_q_loads<D>(p, b, head, hh, wq0, lane, qf, wn, rp);
-    load_tile(0, B0{});
-    load_tile(1, B1{});
-    finish_q_fragment<D>(p, hh, lane, qf, wn, rp, (__attribute__((address_space(3))) char*)rreg, c2);
+    if (!PERSIST || entry == 0) {
+      issue_q_loads<D, !PERSIST>(p, b, head, hh, wq0, lane, qf, wn, rp);
+      load_tile(0, B0{});
+      load_tile(1, B1{});
+    } else {
+      barrier();
+    }
+    finish_q_fragment<D, !PERSIST>(p, hh, lane, qf, wn, rp, (__attribute__((address_space(3))) char*)rreg, c2);
     barrier();
   }
   for (int i = tid; i < VTILE / 8; i += F2_NT) reinterpret_cast<half8v*>(V3)[i] = half8v{};
   store_tile(S0{}, B0{});
   store_tile(S1{}, B1{});
-  load_tile(2, B0{});
-  load_tile(3, B1{});
+  load_slot(2, B0{}, std::true_type{});
+  load_slot(3, B1{}, std::true_type{});
   barrier();                      // tiles 0 and 1 resident
   if (group == 1) barrier();      // group 1 runs one phase behind
   // Tile j uses stage j % 4; the loop is unrolled by four so every stage is static.
@@ -434,6 +509,31 @@ void flash_attention_v2_kernel(FlashParams p) {
   }
   if (group == 0) barrier();      // same barrier count for both groups
   wait_vmcnt_imm<0>();            // loads of tiles past the end (no memory traffic)
+  const bool more = next_entry();
+  if constexpr (PERSIST) {
+    if (more) {
+      // The next entry's Q rows (stream positions ntiles+2 and ntiles+3) move to qf, and
+      // its tiles 0 and 1 load into the staging buffers they leave: that latency hides
+      // behind this entry's epilogue.
+      if constexpr (F2_Q_PREFETCH) {
+        const bool odd = (ntiles & 1) != 0;
+#pragma unroll
+        for (int r = 0; r < NCP; ++r) {
+          qf[r] = __builtin_bit_cast(half8v, odd ? stg2[1][r] : stg2[0][r]);
+          qf[NCP + r] = __builtin_bit_cast(half8v, odd ? stg2[0][r] : stg2[1][r]);
+        }
+      } else {
+        issue_q_loads<D, !PERSIST>(p, bn, head, hh, wq0, lane, qf, wn, rp);
+      }
+      const int nkend = entry_kend(entry_kv_len(bn));
+      const int64_t nkb = nkend > 0 ? (int64_t)(nkend - 1) * ktok2 + D * 2 : 0;
+      const int64_t nvb = nkend > 0 ? (int64_t)(nkend - 1) * vtok2 + D * 2 : 0;
+      const char* const nk = entry_k(bn);
+      const char* const nv = entry_v(bn);
+      load_at(nk, clamp_bytes(nkb), nv, clamp_bytes(nvb), B0{});
+      load_at(nk + kstep, clamp_bytes(nkb - kstep), nv + vstep, clamp_bytes(nvb - vstep), B1{});
+    }
+  }
 
   const float l_tot = xlane32_sum(lrow);
   // A key split stores its normalised rows O_s / l_s in fp16 (below, through the same
@@ -472,6 +572,9 @@ void flash_attention_v2_kernel(FlashParams p) {
     const u32x4 v = *reinterpret_cast<const u32x4*>(ost + r * KROW + ch * 8);
     if (wq0 + r < p.Sq) *reinterpret_cast<u32x4*>(obase + (int64_t)(wq0 + r) * otok + ch * 8) = v;
   }
+  if (!more) break;
+  b = bn;
+  }   // batch entries
 }
 
 // Merge of the key splits: O = sum_s w_s O_s / sum_s w_s l_s with w_s = 2^(m_s - max m).
@@ -536,19 +639,33 @@ void launch_flash_combine(const FlashParams& p, int D, int batch, hipStream_t st
   ANIMA_HIP(hipGetLastError());
 }
 
-void launch_flash_v2(const FlashParams& p, int D, dim3 grid, hipStream_t stream) {
-  // The kernel decodes blockIdx into (split, query tile, batch, head) with these counts:
-  // a grid of any other size would address rows past the tensors.
+void launch_flash_v2(const FlashParams& p, int D, dim3 grid, hipStream_t stream, bool persist) {
+  // The kernel decodes blockIdx into (split, query tile, batch, head) with these counts
+  // (persistent: (query tile, head), batch entries walked in the kernel): a grid of any
+  // other size would address rows past the tensors.
   if (p.nbatch < 1 || p.q_tiles < 1 || p.H < 1 ||
-      (int64_t)grid.x != (int64_t)p.q_tiles * p.H * p.nbatch * (p.kv_splits > 1 ? p.kv_splits : 1))
+      (int64_t)grid.x != (int64_t)p.q_tiles * p.H * (persist ? 1 : p.nbatch) * (p.kv_splits > 1 ? p.kv_splits : 1))
     fail(ANIMA_E_INVALID_ARGUMENT, "flash attention grid does not match its tiles, heads and batch");
-  if (D == 128)
-    hipLaunchKernelGGL(flash_attention_v2_kernel<128>, grid, dim3(F2_NT), 0, stream, p);
-  else if (D == 64)
-    hipLaunchKernelGGL(flash_attention_v2_kernel<64>, grid, dim3(F2_NT), 0, stream, p);
-  else
+  if (persist && (p.rope || p.kv_splits > 1 || !flash_v2_persist_fits(p, D)))
+    fail(ANIMA_E_INVALID_ARGUMENT, "persistent flash attention takes no Q RoPE, no key splits and Q rows within 2 GiB");
+  if (D == 128) {
+    if (persist)
+      hipLaunchKernelGGL((flash_attention_v2_kernel<128, true>), grid, dim3(F2_NT), 0, stream, p);
+    else
+      hipLaunchKernelGGL((flash_attention_v2_kernel<128, false>), grid, dim3(F2_NT), 0, stream, p);
+  } else if (D == 64) {
+    if (persist)
+      hipLaunchKernelGGL((flash_attention_v2_kernel<64, true>), grid, dim3(F2_NT), 0, stream, p);
+    else
+      hipLaunchKernelGGL((flash_attention_v2_kernel<64, false>), grid, dim3(F2_NT), 0, stream, p);
+  } else {
     fail(ANIMA_E_UNSUPPORTED, "flash attention requires head_dim 64 or 128");
+  }
   ANIMA_HIP(hipGetLastError());
+}
+
+bool flash_v2_persist_fits(const FlashParams& p, int D) {
+  return p.Sq >= 1 && (int64_t)(p.Sq - 1) * p.q_tok * 2 + D * 2 < ((int64_t)1 << 31);
 }
 
 }  // namespace anima

@@ -56,7 +56,8 @@ struct QStage {
   static_assert(32 * QPITCH <= WN && 64 % QLPR == 0, "Q rows fit before the norm weight");
 };
 
-template <int D>
+// ROPE = false compiles the RoPE table out (for kernels that never take one).
+template <int D, bool ROPE = true>
 __device__ __forceinline__ void issue_q_loads(const FlashParams& p, int b, int head, int hh, int wq0,
                                               int lane, half8v (&qf)[D / 16], uint32_t& wn,
                                               uint64_t (&rp)[QStage<D>::LOADS]) {
@@ -71,7 +72,7 @@ __device__ __forceinline__ void issue_q_loads(const FlashParams& p, int b, int h
     qf[t] = *reinterpret_cast<const half8v*>(qp + (int64_t)(row < p.Sq ? row : p.Sq - 1) * p.q_tok);
   }
   if (p.q_norm_w && lane < D / 2) wn = *reinterpret_cast<const uint32_t*>(p.q_norm_w + 2 * lane);
-  if (p.rope) {
+  if (ROPE && p.rope) {
     const char* tab = reinterpret_cast<const char*>(p.rope);
 #pragma unroll
     for (int t = 0; t < R::LOADS; ++t) {
@@ -82,7 +83,7 @@ __device__ __forceinline__ void issue_q_loads(const FlashParams& p, int b, int h
   }
 }
 
-template <int D>
+template <int D, bool ROPE = true>
 __device__ __forceinline__ void finish_q_fragment(const FlashParams& p, int hh, int lane, half8v (&qf)[D / 16],
                                                   uint32_t wn, const uint64_t (&rp)[QStage<D>::LOADS],
                                                   __attribute__((address_space(3))) char* region,
@@ -103,33 +104,42 @@ __device__ __forceinline__ void finish_q_fragment(const FlashParams& p, int hh, 
     for (int s = 0; s < QS; ++s) qf[s] = *(const lds_half8v*)(region + c32 * R::QPITCH + (16 * s + 8 * hh) * 2);
   }
   if (p.q_norm_w && lane < D / 2) *(lds_u32*)(region + R::WN + 4 * lane) = wn;
-  if (p.rope) {
+  if (ROPE && p.rope) {
 #pragma unroll
     for (int t = 0; t < R::LOADS; ++t)
       *(lds_u64*)(region + (t * (64 / R::E) + lane / R::E) * R::PITCH + (lane % R::E) * 8) = rp[t];
   }
-  if (p.q_norm_w || p.rope || qmul != 1.f) {
+  if (p.q_norm_w || (ROPE && p.rope) || qmul != 1.f) {
+    // x = q * w (v_fma_mix: the fp16 operands enter the fp32 FMA unconverted, and the
+    // product of two fp16 values is exact in fp32), or q itself without a norm; the
+    // norm factor and qmul join into one fp32 factor g applied once per element (to
+    // the rotation coefficients with RoPE).  Each result is rounded to fp32 and then to
+    // fp16 (f32_to_f16 keeps the compiler from fusing the last product and the
+    // conversion into one v_fma_mix*_f16 rounding, which it does or not depending on
+    // the surrounding kernel), so every kernel gets the same bits.
+    float g = qmul;
     float x[QS][8];
-#pragma unroll
-    for (int s = 0; s < QS; ++s)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x[s][i] = (float)qf[s][i];
     if (p.q_norm_w) {
       float ss = 0.f;
 #pragma unroll
       for (int s = 0; s < QS; ++s)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ss = fmaf(x[s][i], x[s][i], ss);
+        for (int i = 0; i < 8; ++i) ss = fmaf((float)qf[s][i], (float)qf[s][i], ss);
       ss = xlane32_sum(ss);
-      const float inv = rsqrtf(ss / (float)D + p.eps);
+      g *= rsqrtf(ss / (float)D + p.eps);
 #pragma unroll
       for (int s = 0; s < QS; ++s) {
         const half8v w = *(const lds_half8v*)(region + R::WN + (16 * s + 8 * hh) * 2);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] * inv * (float)w[i];
+        for (int i = 0; i < 8; ++i) x[s][i] = fmaf((float)qf[s][i], (float)w[i], 0.f);
       }
+    } else {
+#pragma unroll
+      for (int s = 0; s < QS; ++s)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[s][i] = (float)qf[s][i];
     }
-    if (p.rope) {
+    if (ROPE && p.rope) {
       const int c32 = lane & 31;
 #pragma unroll
       for (int s = 0; s < QS / 2; ++s)
@@ -139,17 +149,23 @@ __device__ __forceinline__ void finish_q_fragment(const FlashParams& p, int hh, 
           const floatx4 cs = *(const lds_floatx4*)(region + c32 * R::PITCH + (16 * s + 8 * hh + i) * 8);
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
-            const float c = cs[2 * u], ns = cs[2 * u + 1];
+            const float c = cs[2 * u] * g, ns = cs[2 * u + 1] * g;
             const float a = x[s][i + u], bb = x[s + QS / 2][i + u];
-            x[s][i + u] = c * a + ns * bb;
-            x[s + QS / 2][i + u] = -ns * a + c * bb;
+            qf[s][i + u] = f32_to_f16(c * a + ns * bb);
+            qf[s + QS / 2][i + u] = f32_to_f16(c * bb - ns * a);
           }
         }
+    } else if (p.q_norm_w) {
+#pragma unroll
+      for (int s = 0; s < QS; ++s)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qf[s][i] = f32_to_f16(x[s][i] * g);
+    } else {
+#pragma unroll
+      for (int s = 0; s < QS; ++s)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qf[s][i] = f32_to_f16(fmaf((float)qf[s][i], g, 0.f));
     }
-#pragma unroll
-    for (int s = 0; s < QS; ++s)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qf[s][i] = f32_to_f16(x[s][i] * qmul);
   }
 }
 

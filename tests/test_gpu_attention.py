@@ -221,6 +221,43 @@ def test_flash_key_splits(ctx, D, B, Sq, Sk):
     assert_attention_close(o, ref, label=f"splits D{D} B{B} Sq{Sq} Sk{Sk}")
 
 
+@pytest.mark.parametrize("B,H,Hkv,Sq,Sk,D,lengths,on_device", [
+    (3, 16, 16, 4000, 600, 128, [600, 1, 130], False),   # one-tile entry, partial query tile
+    (2, 32, 8, 2048, 64, 64, None, False),               # head_dim 64, grouped K/V heads, one tile
+    (2, 16, 4, 4096, 1000, 128, [1000, 65], True),       # device key lengths
+    (4, 64, 64, 1000, 128, 128, None, False),            # four entries over a partial query tile
+])
+def test_flash_persistent_batch_matches_per_entry_calls(ctx, B, H, Hkv, Sq, Sk, D, lengths, on_device):
+    """Batched non-causal calls whose query tiles x heads fill whole rounds of the chip (a
+    multiple of 256) run one workgroup per (query tile, head) over every batch entry, with the
+    next entry's Q rows and first tiles loaded during the current one.  Each entry must equal
+    the same entry computed alone (batch 1, one workgroup per tile) bit for bit, and the oracle
+    within the attention bar; the fused Q norm runs on every entry."""
+    g = torch.Generator().manual_seed(7 * B + H + Sq + Sk + D)
+    q = torch.randn(B, Sq, H, D, generator=g).half()
+    k = torch.randn(B, Sk, Hkv, D, generator=g).half()
+    v = torch.randn(B, Sk, Hkv, D, generator=g).half()
+    w = (0.8 + 0.4 * torch.rand(D, generator=g)).half()
+    pro = QKPrologue(dev(w), dev(w), 1e-6, None, 0, False, False)
+    kw = dict(layout=("tokenMajor", H * D), heads=H, Sq=Sq, Sk=Sk, D=D, key_value_heads=Hkv,
+              kv_token_stride=Hkv * D, prologue=pro)
+    lens = None if lengths is None else (dev(torch.tensor(lengths, dtype=torch.int32)) if on_device
+                                         else np.array(lengths, dtype=np.int32))
+    print(f"PERSIST B={B} H={H} Hkv={Hkv} Sq={Sq} Sk={Sk} D={D} lengths={lengths} dev={on_device}", flush=True)
+    o = _run(ctx, dev(q), dev(k), dev(v), out_shape=(B, Sq, H, D), batch=B, key_lengths=lens,
+             key_lengths_on_device=on_device, **kw)
+    for b in range(B):
+        lb = None if lengths is None else (dev(torch.tensor(lengths[b:b + 1], dtype=torch.int32)) if on_device
+                                           else np.array(lengths[b:b + 1], dtype=np.int32))
+        ob = _run(ctx, dev(q[b:b + 1]), dev(k[b:b + 1]), dev(v[b:b + 1]), out_shape=(1, Sq, H, D), batch=1,
+                  key_lengths=lb, key_lengths_on_device=on_device, **kw)
+        assert torch.equal(o[b:b + 1], ob), f"entry {b} differs from its batch-1 call"
+    qq = oatt.qk_prologue(q, w, 1e-6, None)
+    kk = oatt.qk_prologue(k, w, 1e-6, None)
+    ref = oatt.sdpa(qq, kk, v, key_lengths=lengths)
+    assert_attention_close(o, ref, label=f"persistent B{B} H{H} Sq{Sq} Sk{Sk} D{D}")
+
+
 @pytest.mark.parametrize("flash_rows", [128, 256])
 def test_flash_variants_masked_batch_gqa(ctx, flash_rows):
     """Both flash variants on batch + GQA + causal + right-padding key lengths + prologue."""
