@@ -151,16 +151,22 @@ void flash_attention_v2_kernel(FlashParams p) {
   constexpr int NCP = 2 * CPT;               // copies per thread per tile: K chunks, then V chunks
   static_assert(CPT * F2_NT == F2_BN * DCH && F2_NT % DCH == 0, "tile splits evenly over the threads");
   // Carried from one batch entry to the next (PERSIST): the tile-staging registers (the
-  // next entry's tiles 0 and 1 in flight), its Q rows and the Q norm weight piece.
+  // next entry's tiles 0 and 1 in flight), its Q rows and the Q norm weight piece (the
+  // last loaded after the key loop, so it is not live across it).
   u32x4 stg2[2][NCP];
   half8v qf[QS];
   uint32_t wn = 0;
 
   for (int entry = 0;; ++entry) {   // batch entries (one pass unless PERSIST)
-  // The lane index is re-derived per entry behind an empty asm so that per-lane values
-  // are computed in the entry that uses them instead of living across all entries.
+  // PERSIST: the lane index is re-derived per entry (v_mbcnt in an asm the compiler
+  // cannot hoist) so that per-lane values are computed in the entry that uses them
+  // instead of living across all entries.
   int tid = threadIdx.x;
-  if constexpr (PERSIST) asm volatile("" : "+v"(tid));
+  if constexpr (PERSIST) {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    tid = wave * 64 + l;
+  }
   const int lane = tid & 63;
   const int c32 = lane & 31, hh = lane >> 5;
   const int jj = lane & 15, gg = lane >> 4;
@@ -483,7 +489,14 @@ void flash_attention_v2_kernel(FlashParams p) {
     finish_q_fragment<D, !PERSIST>(p, hh, lane, qf, wn, rp, (__attribute__((address_space(3))) char*)rreg, c2);
     barrier();
   }
-  for (int i = tid; i < VTILE / 8; i += F2_NT) reinterpret_cast<half8v*>(V3)[i] = half8v{};
+  {
+    // The zero quad is made here (not hoisted out of the batch-entry loop, where the
+    // register allocator would keep it in scratch memory across the key loop).
+    u32x4 z;
+    asm volatile("v_mov_b32 %0, 0\n\tv_mov_b32 %1, 0\n\tv_mov_b32 %2, 0\n\tv_mov_b32 %3, 0"
+                 : "=v"(z[0]), "=v"(z[1]), "=v"(z[2]), "=v"(z[3]));
+    for (int i = tid; i < VTILE / 8; i += F2_NT) reinterpret_cast<u32x4*>(V3)[i] = z;
+  }
   store_tile(S0{}, B0{});
   store_tile(S1{}, B1{});
   load_slot(2, B0{}, std::true_type{});
@@ -522,6 +535,7 @@ void flash_attention_v2_kernel(FlashParams p) {
           qf[r] = __builtin_bit_cast(half8v, odd ? stg2[1][r] : stg2[0][r]);
           qf[NCP + r] = __builtin_bit_cast(half8v, odd ? stg2[0][r] : stg2[1][r]);
         }
+        if (p.q_norm_w && lane < D / 2) wn = *reinterpret_cast<const uint32_t*>(p.q_norm_w + 2 * lane);
       } else {
         issue_q_loads<D, !PERSIST>(p, bn, head, hh, wq0, lane, qf, wn, rp);
       }
