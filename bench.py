@@ -278,9 +278,9 @@ def main():
               "timed calls), then 3 x 256 MiB copies", file=sys.stderr)
         return
     if args.profile_step:
-        st_ms, first_ms, fwd_ms, finite = time_sampler_step(torch, A, ctx, stream, args)
+        st_ms, first_ms, fwd_ms, finite, streamed = time_sampler_step(torch, A, ctx, stream, args)
         print(f"# profile-step: sampler step 1024px {st_ms:.3f} ms (first {first_ms:.3f} ms, 28-block forward "
-              f"{fwd_ms:.3f} ms, velocity finite {finite})", file=sys.stderr)
+              f"{fwd_ms:.3f} ms, velocity finite {finite}); streamed forward {streamed}", file=sys.stderr)
         return
 
     # ---------------- headline: S=4096 self-attention with fused norm+RoPE ----------------
@@ -355,7 +355,9 @@ def main():
         qwen = time_qwen_layer(torch, A, ctx, stream, args)
         extra["qwen_layer_b4_s512"] = qwen
         print(f"# Qwen layer B4 S512: {qwen}", file=sys.stderr, flush=True)
-        st_ms, first_ms, fwd_ms, finite = time_sampler_step(torch, A, ctx, stream, args)
+        st_ms, first_ms, fwd_ms, finite, streamed = time_sampler_step(torch, A, ctx, stream, args)
+        extra["forward_28_blocks_streamed"] = streamed
+        print(f"# streamed 28-block forward: {streamed}", file=sys.stderr, flush=True)
         extra["sampler_step_1024px"] = {
             "ms": round(st_ms, 3), "first_step_ms": round(first_ms, 3), "forward_28_blocks_ms": round(fwd_ms, 3),
             "ms_per_block": round(fwd_ms / 28, 4), "generation_8_steps_ms": round(first_ms + 7 * st_ms, 2),
@@ -736,7 +738,65 @@ def time_sampler_step(torch, A, ctx, stream, args, blocks=28):
     finite = bool(torch.isfinite(vel).all())
     ms = time_region(torch, stream, step, args.block_steps, 1)
     fwd = time_region(torch, stream, forward_only, args.block_steps, 1)
-    return ms, first_ms, fwd, finite
+    streamed = time_streamed_forward(torch, A, ctx, stream, args, blk, block_list,
+                                     (residual, emb, adaln, ctxt, rope), cache, fwd)
+    return ms, first_ms, fwd, finite, streamed
+
+
+def time_streamed_forward(torch, A, ctx, stream, args, blk, block_list, bufs, cache, resident_ms):
+    """The same 28-block forward with every block's weights streamed from pinned host memory
+    through a WeightStreamer of 2 device slots (WeightStreamer.swift:94-213, DitForward.swift:
+    21-35): block i runs from one slot while the copy stream fills the other with block i+1.
+    Each block's tensors sit 256-byte aligned in one host range, and the block template holds
+    their offsets.  Returns ms per forward, bytes per block and the host-to-device rate the
+    forward implies."""
+    residual, emb, adaln, ctxt, rope = bufs
+    names, norm_names = A.DiTBlockExecutor.NAMES, A.DiTBlockExecutor.NORMS
+    templates, ranges, hosts = [], [], []
+    for weights, norms in block_list:
+        tensors = {}
+        for n in names:
+            for t in (weights[n].packed, weights[n].scale, weights[n].zero):
+                tensors[t.data_ptr()] = t
+        for n in norm_names:
+            tensors[norms[n].data_ptr()] = norms[n]
+        offs, off = {}, 0
+        for ptr, t in tensors.items():
+            off = (off + 255) // 256 * 256
+            offs[ptr] = off
+            off += t.numel() * t.element_size()
+        host = torch.empty(off, dtype=torch.uint8, pin_memory=True)
+        for ptr, t in tensors.items():
+            nb = t.numel() * t.element_size()
+            host[offs[ptr]:offs[ptr] + nb].copy_(t.reshape(-1).view(torch.uint8))
+        tmpl = blk.weights_struct(weights, norms)
+        for n in names:
+            q = getattr(tmpl, n)
+            for b in (q.packed, q.scale, q.zero):
+                b.ptr = offs[b.ptr]
+                b.length = 0
+        for n in norm_names:
+            b = getattr(tmpl, n)
+            b.ptr = offs[b.ptr]
+            b.length = 0
+        templates.append(tmpl)
+        ranges.append((host.data_ptr(), host.numel()))
+        hosts.append(host)
+    torch.cuda.synchronize()
+    per_block = max(r[1] for r in ranges)
+    st = A.WeightStreamer(ctx, capacity=per_block, slots=2)
+
+    def fwd_streamed(i):
+        blk.forward_streamed(st, templates, ranges, residual, emb, adaln, ctxt, rope, tokens=S, cache=cache)
+
+    ms = time_region(torch, stream, fwd_streamed, args.block_steps, 1)
+    total = sum(r[1] for r in ranges)
+    st.close()
+    del hosts
+    return {"ms": round(ms, 3), "resident_ms": round(resident_ms, 3), "slots": 2,
+            "bytes_per_block": int(per_block), "host_to_device_gbs": round(total / (ms * 1e-3) / 1e9, 1),
+            "includes": "28 W4 blocks, weights copied from pinned host ranges into 2 device slots on the "
+                        "streamer's copy stream, overlapped with the previous block's kernels"}
 
 
 def time_qwen_layer(torch, A, ctx, stream, args):
