@@ -221,24 +221,25 @@ def test_flash_key_splits(ctx, D, B, Sq, Sk):
     assert_attention_close(o, ref, label=f"splits D{D} B{B} Sq{Sq} Sk{Sk}")
 
 
-@pytest.mark.parametrize("B,H,Hkv,Sq,Sk,D,lengths,on_device", [
-    (3, 16, 16, 4000, 600, 128, [600, 1, 130], False),   # one-tile entry, partial query tile
-    (2, 32, 8, 2048, 64, 64, None, False),               # head_dim 64, grouped K/V heads, one tile
-    (2, 16, 4, 4096, 1000, 128, [1000, 65], True),       # device key lengths
-    (4, 64, 64, 1000, 128, 128, None, False),            # four entries over a partial query tile
+@pytest.mark.parametrize("B,H,Hkv,Sq,Sk,D,lengths,on_device,norm", [
+    (3, 16, 16, 4000, 600, 128, [600, 1, 130], False, True),   # one-tile entry, partial query tile
+    (2, 32, 8, 2048, 64, 64, None, False, True),               # head_dim 64, grouped K/V heads, one tile
+    (2, 16, 4, 4096, 1000, 128, [1000, 65], True, True),       # device key lengths
+    (4, 64, 64, 1000, 128, 128, None, False, True),            # four entries over a partial query tile
+    (5, 32, 32, 2048, 300, 128, [300, 2, 299, 64, 65], False, False),   # no Q/K norm, five entries
 ])
-def test_flash_persistent_batch_matches_per_entry_calls(ctx, B, H, Hkv, Sq, Sk, D, lengths, on_device):
+def test_flash_persistent_batch_matches_per_entry_calls(ctx, B, H, Hkv, Sq, Sk, D, lengths, on_device, norm):
     """Batched non-causal calls whose query tiles x heads fill whole rounds of the chip (a
     multiple of 256) run one workgroup per (query tile, head) over every batch entry, with the
     next entry's Q rows and first tiles loaded during the current one.  Each entry must equal
     the same entry computed alone (batch 1, one workgroup per tile) bit for bit, and the oracle
-    within the attention bar; the fused Q norm runs on every entry."""
+    within the attention bar; the fused Q norm (when given) runs on every entry."""
     g = torch.Generator().manual_seed(7 * B + H + Sq + Sk + D)
     q = torch.randn(B, Sq, H, D, generator=g).half()
     k = torch.randn(B, Sk, Hkv, D, generator=g).half()
     v = torch.randn(B, Sk, Hkv, D, generator=g).half()
     w = (0.8 + 0.4 * torch.rand(D, generator=g)).half()
-    pro = QKPrologue(dev(w), dev(w), 1e-6, None, 0, False, False)
+    pro = QKPrologue(dev(w), dev(w), 1e-6, None, 0, False, False) if norm else None
     kw = dict(layout=("tokenMajor", H * D), heads=H, Sq=Sq, Sk=Sk, D=D, key_value_heads=Hkv,
               kv_token_stride=Hkv * D, prologue=pro)
     lens = None if lengths is None else (dev(torch.tensor(lengths, dtype=torch.int32)) if on_device
@@ -252,10 +253,10 @@ def test_flash_persistent_batch_matches_per_entry_calls(ctx, B, H, Hkv, Sq, Sk, 
         ob = _run(ctx, dev(q[b:b + 1]), dev(k[b:b + 1]), dev(v[b:b + 1]), out_shape=(1, Sq, H, D), batch=1,
                   key_lengths=lb, key_lengths_on_device=on_device, **kw)
         assert torch.equal(o[b:b + 1], ob), f"entry {b} differs from its batch-1 call"
-    qq = oatt.qk_prologue(q, w, 1e-6, None)
-    kk = oatt.qk_prologue(k, w, 1e-6, None)
+    qq = oatt.qk_prologue(q, w, 1e-6, None) if norm else q
+    kk = oatt.qk_prologue(k, w, 1e-6, None) if norm else k
     ref = oatt.sdpa(qq, kk, v, key_lengths=lengths)
-    assert_attention_close(o, ref, label=f"persistent B{B} H{H} Sq{Sq} Sk{Sk} D{D}")
+    assert_attention_close(o, ref, label=f"persistent B{B} H{H} Sq{Sq} Sk{Sk} D{D} norm={norm}")
 
 
 @pytest.mark.parametrize("flash_rows", [128, 256])
