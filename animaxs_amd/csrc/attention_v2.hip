@@ -83,6 +83,8 @@ void flash_attention_v2_kernel(FlashParams p) {
   // another and does not make the reads wait for the copy.
   __shared__ __attribute__((aligned(1024))) half_t K0[KTILE], K1[KTILE], K2[KTILE], K3[KTILE];
   __shared__ __attribute__((aligned(1024))) half_t V0[VTILE], V1[VTILE], V2[VTILE], V3[VTILE];
+  // PERSIST: each wave's copy of the Q norm weight, written in the first entry.
+  __shared__ __attribute__((aligned(16))) half_t QW[PERSIST ? F2_NT / 64 * D : 8];
   static_assert(F2_STAGES == 4, "four stage objects");
   auto kstage = [&](auto st) __attribute__((always_inline)) -> half_t* {
     constexpr int S = decltype(st)::value % F2_STAGES;
@@ -129,7 +131,11 @@ void flash_attention_v2_kernel(FlashParams p) {
   auto entry_kv_len = [&](int bb) __attribute__((always_inline)) -> int {
     int len = p.Sk;
     if (p.key_lengths_dev) {
-      int L = p.key_lengths_dev[bb];
+      // A scalar load (constant address space: the kernel never writes the lengths).  A
+      // vector load here would have to wait for every vector memory operation in flight,
+      // in a later batch entry (PERSIST) the previous entry's O stores among them.
+      int L = *reinterpret_cast<const __attribute__((address_space(4))) int*>(
+          reinterpret_cast<uintptr_t>(p.key_lengths_dev + bb));
       len = L < 1 ? 1 : (L > p.Sk ? p.Sk : L);
     } else if (p.use_host_lengths) {
       len = p.host_lengths[bb];
@@ -152,11 +158,9 @@ void flash_attention_v2_kernel(FlashParams p) {
   constexpr int NCP = 2 * CPT;               // copies per thread per tile: K chunks, then V chunks
   static_assert(CPT * F2_NT == F2_BN * DCH && F2_NT % DCH == 0, "tile splits evenly over the threads");
   // Carried from one batch entry to the next (PERSIST): the tile-staging registers (the
-  // next entry's tiles 0 and 1 in flight), its Q rows and the Q norm weight piece (the
-  // last loaded after the key loop, so it is not live across it).
+  // next entry's tiles 0 and 1 in flight) and its Q fragment.
   u32x4 stg2[2][NCP];
   half8v qf[QS];
-  uint32_t wn = 0;
 
   for (int entry = 0;; ++entry) {   // batch entries (one pass unless PERSIST)
   // PERSIST: the lane index is re-derived per entry (v_mbcnt in an asm the compiler
@@ -178,6 +182,7 @@ void flash_attention_v2_kernel(FlashParams p) {
   const char* const kbase = entry_k(b);
   const char* const vbase = entry_v(b);
   uint64_t rp[QStage<D>::LOADS];   // RoPE table pieces (never with PERSIST)
+  uint32_t wn = 0;                 // Q norm weight piece
 
   // Tile copies: thread t moves the 16-byte chunks t + F2_NT*r (r < CPT) of the K
   // tile and of the V tile (chunk -> row, column: 16-lane coalesced rows in
@@ -234,23 +239,26 @@ void flash_attention_v2_kernel(FlashParams p) {
   // zero-size loads at ntiles and ntiles+1), then the next entry's Q rows in two parts of
   // NCP loads at positions qa = ntiles+2 and qa+1: the last two loads of the stream, so
   // nothing overwrites their staging buffers (position pos lands in buffer pos % 2) before
-  // the key loop ends.  Q row loads follow issue_q_loads (load t moves rows
-  // t * 64/QLPR + lane/QLPR, rows past the sequence repeat the last row) through one
-  // descriptor over the (batch, head) rows.
-  constexpr int QLPR = QStage<D>::QLPR;
+  // the key loop ends.  The Q rows load in the fragment layout (lane (c32, hh): row c32,
+  // columns 16s + 8hh .. +7; rows past the sequence repeat the last row) through one
+  // descriptor over the (batch, head) rows: part P holds s = NCP*P .. NCP*P + NCP-1.
+  // These loads touch 32 rows with 32 bytes each per instruction, half the vector memory
+  // rate of whole-row loads, but they run beside a key loop that leaves that path idle
+  // most of the time, and the fragment then needs no pass through LDS.
   static_assert(QS == 2 * NCP, "one Q part fills one staging buffer");
   const uint32_t qtok2 = (uint32_t)p.q_tok * 2u;
   const int qnbytes = (int)((uint32_t)(p.Sq - 1) * qtok2 + D * 2);
   auto next_entry = [&]() __attribute__((always_inline)) { return PERSIST && entry + 1 < p.nbatch; };
   const int bn = b + 1 == p.nbatch ? 0 : b + 1;   // next entry (PERSIST)
+  auto q_frag_load = [&](int bb, int s) __attribute__((always_inline)) -> u32x4 {
+    const char* qb = reinterpret_cast<const char*>(p.q + (int64_t)bb * p.q_batch + (int64_t)head * p.q_head);
+    const uint32_t row = (uint32_t)min(qi, p.Sq - 1);
+    return load16_bounded(qb, qnbytes, row * qtok2 + (uint32_t)(32 * s + 16 * hh));
+  };
   auto load_q_part = [&](int part, auto bufc) __attribute__((always_inline)) {
     u32x4 (&stg)[NCP] = stg2[decltype(bufc)::value];
-    const char* qb = reinterpret_cast<const char*>(p.q + (int64_t)bn * p.q_batch + (int64_t)head * p.q_head);
 #pragma unroll
-    for (int r = 0; r < NCP; ++r) {
-      const int row = min(wq0 + (NCP * part + r) * (64 / QLPR) + lane / QLPR, p.Sq - 1);
-      stg[r] = load16_bounded(qb, qnbytes, (uint32_t)row * qtok2 + (uint32_t)(lane % QLPR) * 16u);
-    }
+    for (int r = 0; r < NCP; ++r) stg[r] = q_frag_load(bn, NCP * part + r);
   };
   // Load of stream position pos into buffer pos % 2; FIRST: one of positions 0..3 (by
   // tile index), else the next tile of the running pointers.
@@ -471,24 +479,44 @@ void flash_attention_v2_kernel(FlashParams p) {
   // of tiles 0 and 1 are all in flight together, so the workgroup pays one memory round
   // trip before its first MFMA instead of three.  A later batch entry (PERSIST) finds its
   // Q rows in qf and its tiles 0 and 1 in flight, loaded during the previous entry.
-  half_t* const rreg = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? K2 : wave == 3 ? K3
-                     : wave == 4 ? V0 : wave == 5 ? V1 : wave == 6 ? V2 : V3;
-  {
+  if constexpr (!PERSIST) {
+    half_t* const rreg = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? K2 : wave == 3 ? K3
+                       : wave == 4 ? V0 : wave == 5 ? V1 : wave == 6 ? V2 : V3;
     // The Q loads go first (they are on the critical path), then tiles 0 and 1.  The Q
     // rows, the Q norm weight and the RoPE table rows are staged through LDS
     // (finish_q_fragment): waves 0-3 use K stages 0-3, waves 4-7 V stages 0-3, all free
     // until the tile stores below, which wait behind one barrier for every wave's
-    // staged reads (and, in a later entry, behind one for the previous entry's O rows).
+    // staged reads.
     static_assert(QStage<D>::BYTES <= KTILE * 2 && QStage<D>::BYTES <= VTILE * 2, "Q staging fits a stage");
-    if (!PERSIST || entry == 0) {
-      issue_q_loads<D, !PERSIST>(p, b, head, hh, wq0, lane, qf, wn, rp);
+    issue_q_loads<D, true>(p, b, head, hh, wq0, lane, qf, wn, rp);
+    load_tile(0, B0{});
+    load_tile(1, B1{});
+    finish_q_fragment<D, true>(p, hh, lane, qf, wn, rp, (__attribute__((address_space(3))) char*)rreg, c2);
+    barrier();
+  } else {
+    // The first entry loads its Q fragment, the norm weight (into the wave's LDS copy)
+    // and tiles 0 and 1; a later entry finds its fragment in qf and its tiles in flight.
+    // Only the norm runs here, on registers and the wave's own weight copy, so the one
+    // barrier left is the one that keeps the tile stores below behind every wave's reads
+    // of the previous entry's O rows (K stages).
+    auto* const wcopy = (__attribute__((address_space(3))) char*)(QW + wave * D);
+    if (entry == 0) {
+#pragma unroll
+      for (int s = 0; s < QS; ++s) qf[s] = __builtin_bit_cast(half8v, q_frag_load(b, s));
+      if (p.q_norm_w && lane < D / 2) wn = *reinterpret_cast<const uint32_t*>(p.q_norm_w + 2 * lane);
       load_tile(0, B0{});
       load_tile(1, B1{});
+      if (p.q_norm_w && lane < D / 2) *(__attribute__((address_space(3))) uint32_t*)(wcopy + 4 * lane) = wn;
+      finish_q_fragment<D, false, false>(p, hh, lane, qf, wn, rp, wcopy, c2);
+      // Nothing this path loaded is left pending where it meets the path of a later entry.
+      // There the previous entry's O stores were issued after tiles 0 and 1, and the
+      // compiler's wait counts take the worse of the two paths: with tile loads pending
+      // here, the tile stores below would also wait for every O store to complete.
+      wait_vmcnt_imm<0>();
     } else {
+      finish_q_fragment<D, false, false>(p, hh, lane, qf, wn, rp, wcopy, c2);
       barrier();
     }
-    finish_q_fragment<D, !PERSIST>(p, hh, lane, qf, wn, rp, (__attribute__((address_space(3))) char*)rreg, c2);
-    barrier();
   }
   {
     // The zero quad is made here (not hoisted out of the batch-entry loop, where the
@@ -536,9 +564,9 @@ void flash_attention_v2_kernel(FlashParams p) {
           qf[r] = __builtin_bit_cast(half8v, odd ? stg2[1][r] : stg2[0][r]);
           qf[NCP + r] = __builtin_bit_cast(half8v, odd ? stg2[0][r] : stg2[1][r]);
         }
-        if (p.q_norm_w && lane < D / 2) wn = *reinterpret_cast<const uint32_t*>(p.q_norm_w + 2 * lane);
       } else {
-        issue_q_loads<D, !PERSIST>(p, bn, head, hh, wq0, lane, qf, wn, rp);
+#pragma unroll
+        for (int s = 0; s < QS; ++s) qf[s] = __builtin_bit_cast(half8v, q_frag_load(bn, s));
       }
       const int nkend = entry_kend(entry_kv_len(bn));
       const int64_t nkb = nkend > 0 ? (int64_t)(nkend - 1) * ktok2 + D * 2 : 0;
@@ -554,7 +582,7 @@ void flash_attention_v2_kernel(FlashParams p) {
   // A key split stores its normalised rows O_s / l_s in fp16 (below, through the same
   // whole-row path as O) beside the fp32 (max, sum) pair of each row; the merge weighs
   // them by l_s.
-  if (p.kv_splits > 1 && qi < p.Sq && hh == 0) {
+  if (!PERSIST && p.kv_splits > 1 && qi < p.Sq && hh == 0) {
     const int64_t row = (((int64_t)split * p.nbatch + b) * p.H + head) * p.Sq + qi;
     *reinterpret_cast<float2*>(p.part_ml + row * 2) = make_float2(m_run, l_tot);
   }
@@ -577,15 +605,31 @@ void flash_attention_v2_kernel(FlashParams p) {
       *reinterpret_cast<half4v*>(ost + c32 * KROW + 32 * c + 8 * e4 + 4 * hh) = val;
     }
   constexpr int CPR = D / 8, RPI = 64 / CPR;   // 16-byte chunks per row, rows per store
-  half_t* const obase = p.kv_splits > 1
+  half_t* const obase = !PERSIST && p.kv_splits > 1
                             ? static_cast<half_t*>(p.part_o) + (((int64_t)split * p.nbatch + b) * p.H + head) * p.Sq * D
                             : p.o + (int64_t)b * p.o_batch + (int64_t)head * p.o_head;
-  const int64_t otok = p.kv_splits > 1 ? D : p.o_tok;
+  const int64_t otok = !PERSIST && p.kv_splits > 1 ? D : p.o_tok;
+  if constexpr (PERSIST) {
+    // Through one descriptor over the (batch, head) rows (within 2 GiB, checked on the
+    // host), which drops the rows past the sequence: with a branch per store instead, the
+    // compiler's wait counts in the next entry would take the path that skips every store
+    // and make the tile stores wait for these stores to complete.
+    const uint32_t otok2 = (uint32_t)p.o_tok * 2u;
+    const int onbytes = (int)((uint32_t)(p.Sq - 1) * otok2 + D * 2);
 #pragma unroll
-  for (int i = 0; i < 32 / RPI; ++i) {
-    const int r = i * RPI + lane / CPR, ch = lane % CPR;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(ost + r * KROW + ch * 8);
-    if (wq0 + r < p.Sq) *reinterpret_cast<u32x4*>(obase + (int64_t)(wq0 + r) * otok + ch * 8) = v;
+    for (int i = 0; i < 32 / RPI; ++i) {
+      const int r = i * RPI + lane / CPR, ch = lane % CPR;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(ost + r * KROW + ch * 8);
+      const uint32_t off = wq0 + r < p.Sq ? (uint32_t)(wq0 + r) * otok2 + (uint32_t)ch * 16u : 0x80000000u;
+      store16_bounded(obase, onbytes, off, v);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32 / RPI; ++i) {
+      const int r = i * RPI + lane / CPR, ch = lane % CPR;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(ost + r * KROW + ch * 8);
+      if (wq0 + r < p.Sq) *reinterpret_cast<u32x4*>(obase + (int64_t)(wq0 + r) * otok + ch * 8) = v;
+    }
   }
   if (!more) break;
   b = bn;
@@ -680,7 +724,8 @@ void launch_flash_v2(const FlashParams& p, int D, dim3 grid, hipStream_t stream,
 }
 
 bool flash_v2_persist_fits(const FlashParams& p, int D) {
-  return p.Sq >= 1 && (int64_t)(p.Sq - 1) * p.q_tok * 2 + D * 2 < ((int64_t)1 << 31);
+  return p.Sq >= 1 && (int64_t)(p.Sq - 1) * p.q_tok * 2 + D * 2 < ((int64_t)1 << 31) &&
+         (int64_t)(p.Sq - 1) * p.o_tok * 2 + D * 2 < ((int64_t)1 << 31);
 }
 
 }  // namespace anima

@@ -130,6 +130,16 @@ __device__ __forceinline__ u32x4 load16_bounded(const void* base, int n, uint32_
 #endif
 }
 
+// 16-byte store through a raw buffer descriptor of n bytes at base: stores at offsets
+// at or past n are dropped.  No branch guards it, so the compiler's count of vector
+// memory operations in flight does not fork at each store.
+__device__ __forceinline__ void store16_bounded(void* base, int n, uint32_t voff, u32x4 v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, n, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, 0, 0);
+#endif
+}
+
 // 2-byte variant of load16_bounded (zero-extended).
 __device__ __forceinline__ uint32_t load2_bounded(const void* base, int n, uint32_t voff, int soff = 0) {
 #if defined(__HIP_DEVICE_COMPILE__)

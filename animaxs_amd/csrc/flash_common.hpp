@@ -43,6 +43,10 @@ __device__ __forceinline__ float xlane32_sum(float x) {
 //    two at a time.
 // The wave's LDS region (QStage<D>::BYTES) is private to it; the caller must not reuse
 // it for other data before every wave of the workgroup is past finish_q_fragment.
+//
+// STAGED = false is for a caller that has loaded qf in the fragment layout itself (at a
+// time when the vector memory path is not the limit) and keeps the norm weight in LDS:
+// region is then the wave's copy of the weight (D halfs), and only the norm runs.
 template <int D>
 struct QStage {
   static constexpr int E = D / 2;                 // table blocks per row
@@ -83,7 +87,7 @@ __device__ __forceinline__ void issue_q_loads(const FlashParams& p, int b, int h
   }
 }
 
-template <int D, bool ROPE = true>
+template <int D, bool ROPE = true, bool STAGED = true>
 __device__ __forceinline__ void finish_q_fragment(const FlashParams& p, int hh, int lane, half8v (&qf)[D / 16],
                                                   uint32_t wn, const uint64_t (&rp)[QStage<D>::LOADS],
                                                   __attribute__((address_space(3))) char* region,
@@ -94,16 +98,18 @@ __device__ __forceinline__ void finish_q_fragment(const FlashParams& p, int hh, 
   typedef __attribute__((address_space(3))) uint32_t lds_u32;
   typedef __attribute__((address_space(3))) half8v lds_half8v;
   typedef __attribute__((address_space(3))) floatx4 lds_floatx4;
-  // Q rows to LDS and back as the fragment (lane (c32, hh): row c32, columns 16s + 8hh ..).
+  static_assert(STAGED || !ROPE, "the RoPE table is staged with the Q rows");
+  constexpr int WOFF = STAGED ? R::WN : 0;   // offset of the norm weight copy in region
+  if constexpr (STAGED) {
+    // Q rows to LDS and back as the fragment (lane (c32, hh): row c32, columns 16s + 8hh ..).
 #pragma unroll
-  for (int t = 0; t < QS; ++t)
-    *(lds_half8v*)(region + (t * (64 / R::QLPR) + lane / R::QLPR) * R::QPITCH + (lane % R::QLPR) * 16) = qf[t];
-  {
+    for (int t = 0; t < QS; ++t)
+      *(lds_half8v*)(region + (t * (64 / R::QLPR) + lane / R::QLPR) * R::QPITCH + (lane % R::QLPR) * 16) = qf[t];
     const int c32 = lane & 31;
 #pragma unroll
     for (int s = 0; s < QS; ++s) qf[s] = *(const lds_half8v*)(region + c32 * R::QPITCH + (16 * s + 8 * hh) * 2);
+    if (p.q_norm_w && lane < D / 2) *(lds_u32*)(region + R::WN + 4 * lane) = wn;
   }
-  if (p.q_norm_w && lane < D / 2) *(lds_u32*)(region + R::WN + 4 * lane) = wn;
   if (ROPE && p.rope) {
 #pragma unroll
     for (int t = 0; t < R::LOADS; ++t)
@@ -129,7 +135,7 @@ __device__ __forceinline__ void finish_q_fragment(const FlashParams& p, int hh, 
       g *= rsqrtf(ss / (float)D + p.eps);
 #pragma unroll
       for (int s = 0; s < QS; ++s) {
-        const half8v w = *(const lds_half8v*)(region + R::WN + (16 * s + 8 * hh) * 2);
+        const half8v w = *(const lds_half8v*)(region + WOFF + (16 * s + 8 * hh) * 2);
 #pragma unroll
         for (int i = 0; i < 8; ++i) x[s][i] = fmaf((float)qf[s][i], (float)w[i], 0.f);
       }
