@@ -98,7 +98,7 @@ __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kerne
   constexpr int WORDS = SmallMChunk<STORAGE>::WORDS;
   // Dynamic LDS: the S x R*MB partial-sum tiles of the final reduction, then the
   // workgroup's scale and zero rows ([16R][groups] halfs each).
-  extern __shared__ float red[];   // [S][R*MB][4][64], then scale, zero
+  extern __shared__ float red[];   // [S][R*MB][64][4], then scale, zero
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int S = blockDim.x >> 6;
@@ -230,7 +230,8 @@ __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kerne
 
   // Order per iteration: this step's X fragments (L2), then the next step's weight
   // prefetch (HBM), then the arithmetic.  Loads retire in issue order, so waiting for
-  // X and this step's weights never waits for the prefetch.
+  // X and this step's weights never waits for the prefetch.  (Issuing the next step's
+  // X with its weights, in a second X buffer, measured no faster.)
   auto compute_step = [&](int step, const Step& st, const half8v (&xs)[NCH][MB][4]) {
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
@@ -257,24 +258,46 @@ __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kerne
       bool fast = true;
 #pragma unroll
       for (int rb = 0; rb < R; ++rb) fast = fast && one_rounding_exact<QBITS>(sc[rb], zc[rb]);
-      half8v a[R][4];
-      if (__all(fast)) {
+      if constexpr (NST == 1) {
+        // One step: every fragment is dequantised before the first MFMA, so the VALU
+        // work overlaps the wait for X (issued after the weights).
+        half8v a[R][4];
+        if (__all(fast)) {
+#pragma unroll
+          for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[rb][t] = dequant_frag<STORAGE, true>(st.wv[c][rb], t, sc[rb], zc[rb]);
+        } else {
+#pragma unroll
+          for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[rb][t] = dequant_frag<STORAGE, false>(st.wv[c][rb], t, sc[rb], zc[rb]);
+        }
 #pragma unroll
         for (int rb = 0; rb < R; ++rb)
 #pragma unroll
-          for (int t = 0; t < 4; ++t) a[rb][t] = dequant_frag<STORAGE, true>(st.wv[c][rb], t, sc[rb], zc[rb]);
+          for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) acc[rb][mb] = mfma16(a[rb][t], xs[c][mb][t], acc[rb][mb]);
       } else {
+        // Several steps: each fragment is dequantised right before its MFMAs, which
+        // keeps the live A fragments to one (the two-row-block kernels for 49-64 input
+        // rows spilled otherwise).  The rounding form is one uniform branch around it.
+        auto run = [&](auto one_rounding) __attribute__((always_inline)) {
 #pragma unroll
-        for (int rb = 0; rb < R; ++rb)
+          for (int rb = 0; rb < R; ++rb)
 #pragma unroll
-          for (int t = 0; t < 4; ++t) a[rb][t] = dequant_frag<STORAGE, false>(st.wv[c][rb], t, sc[rb], zc[rb]);
+            for (int t = 0; t < 4; ++t) {
+              const half8v a = dequant_frag<STORAGE, decltype(one_rounding)::value>(st.wv[c][rb], t, sc[rb], zc[rb]);
+#pragma unroll
+              for (int mb = 0; mb < MB; ++mb) acc[rb][mb] = mfma16(a, xs[c][mb][t], acc[rb][mb]);
+            }
+        };
+        if (__all(fast))
+          run(std::true_type{});
+        else
+          run(std::false_type{});
       }
-#pragma unroll
-      for (int rb = 0; rb < R; ++rb)
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb) acc[rb][mb] = mfma16(a[rb][t], xs[c][mb][t], acc[rb][mb]);
     }
   };
 
@@ -314,21 +337,38 @@ __global__ __launch_bounds__(64 * smallm_max_waves<MB>()) void smallm_gemm_kerne
     compute_step(step, cur, xs);
   }
 
-  // Fixed-order reduction of the S K-slices through LDS.
+  // Fixed-order reduction of the S K-slices through LDS: each lane's 4 sums of a
+  // (row block, m block) pair are one 16-byte word, and the reading wave issues every
+  // slice's read before the first add (the loop runs to the largest S, reads past S
+  // predicated off), so the tail is one LDS round trip instead of S dependent ones.
+  floatx4* red4 = reinterpret_cast<floatx4*>(red);
 #pragma unroll
-  for (int pi = 0; pi < PAIRS; ++pi)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) red[((wave * PAIRS + pi) * 4 + i) * 64 + lane] = acc[pi / MB][pi % MB][i];
+  for (int pi = 0; pi < PAIRS; ++pi) red4[(wave * PAIRS + pi) * 64 + lane] = acc[pi / MB][pi % MB];
   __syncthreads();
   for (int pi = wave; pi < PAIRS; pi += S) {
     const int rb = pi / MB, mb = pi % MB;
-    float v[4];
+    // NS slots read at once (NS the smallest of 4, 8, 16 that covers S, one uniform
+    // branch); slots past S re-read slot S-1 and add +0 instead (no branch per slot).
+    // The sum starts at +0, so the extra +0 terms change no bit, not even a zero's sign.
+    auto reduce = [&](auto ns) __attribute__((always_inline)) -> floatx4 {
+      constexpr int NS = decltype(ns)::value;
+      floatx4 part[NS];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float s = 0.f;
-      for (int w = 0; w < S; ++w) s += red[((w * PAIRS + pi) * 4 + i) * 64 + lane];
-      v[i] = s;
-    }
+      for (int w = 0; w < NS; ++w) part[w] = red4[(min(w, S - 1) * PAIRS + pi) * 64 + lane];
+      floatx4 sum = floatx4{};
+#pragma unroll
+      for (int w = 0; w < NS; ++w) sum += w < S ? part[w] : floatx4{};
+      return sum;
+    };
+    constexpr int SMAX = smallm_max_waves<MB>();
+    floatx4 sum;
+    if (SMAX > 8 && S > 8)
+      sum = reduce(std::integral_constant<int, SMAX>{});
+    else if (S > 4)
+      sum = reduce(std::integral_constant<int, 8>{});
+    else
+      sum = reduce(std::integral_constant<int, 4>{});
+    const float v[4] = {sum[0], sum[1], sum[2], sum[3]};
     // C layout: lane (col = lane%16, rows 4*(lane/16) .. +3) -> y[m = col][n = row]
     const int m = mb * 16 + r;
     const int nb = n0 + rb * 16 + 4 * g;
