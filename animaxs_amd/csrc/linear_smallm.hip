@@ -506,13 +506,16 @@ void launch_smallm(const GemmParams& g, int storage, hipStream_t stream) {
 // Split-K form (W4/W8).  The kernel above gives each 16 weight rows all of X: with
 // 33..64 input rows every wave gathers M x K halfs of X from L2 for 16 x K/2 bytes of
 // weights, and N = 2048 leaves half the chip without a workgroup.  Here:
-//   * a workgroup of SK_WAVES waves owns SK_ROWS weight rows (16 per wave) and one K
-//     slice; the slice of X (all M rows, zero rows up to 16 * MB) is copied into LDS
-//     once with coalesced 16-byte loads, and every wave reads its B fragments there,
-//     so an X byte crosses the CU's memory path once per SK_ROWS weight rows;
-//   * a wave loads all its weight words of the slice at once (one 16-byte load per
-//     lane and chunk for W4, two for W8) and dequantises them chunk by chunk with the
-//     exact rounding of the kernel above (one_rounding_exact, wave-uniform);
+//   * a workgroup owns SK_ROWS weight rows (16 per row block) and one K slice; the
+//     slice of X (all M rows, zero rows up to 16 * MB) is copied into LDS once with
+//     coalesced 16-byte loads, and every wave reads its B fragments there, so an X
+//     byte crosses the CU's memory path once per SK_ROWS weight rows;
+//   * with four or more chunks per slice, two waves share each row block, one per half
+//     of the slice's chunks (two waves per SIMD, so one's dequantisation and LDS reads
+//     overlap the other's MFMAs), and add their sums through LDS at the end;
+//   * a wave loads all its weight words at once (one 16-byte load per lane and chunk
+//     for W4, two for W8) and dequantises them chunk by chunk with the exact rounding
+//     of the kernel above (one_rounding_exact, wave-uniform);
 //   * slices are chosen so the grid reaches 256 workgroups; with more than one, each
 //     writes fp32 partial rows [slice][M][N] and launch_splitk_reduce adds them in
 //     slice order (deterministic) and rounds once to fp16.
@@ -520,33 +523,41 @@ void launch_smallm(const GemmParams& g, int storage, hipStream_t stream) {
 // k = chunk + 32g + 8t .. +7 of step t), B = X^T with the same k, C lane (r, g) =
 // Y[m = 16mb + r][n = 16w + 4g .. +3].
 // ---------------------------------------------------------------------------
-constexpr int SK_WAVES = 4;
-constexpr int SK_ROWS = 16 * SK_WAVES;
+constexpr int SK_RWAVES = 4;                 // row blocks per workgroup
+constexpr int SK_ROWS = 16 * SK_RWAVES;
+template <int NCHK>
+constexpr int sk_khalves() { return NCHK >= 4 ? 2 : 1; }
 constexpr int SK_MAX_CHUNKS = 8;              // 128-wide K chunks per slice
 constexpr int64_t SK_MAX_LDS = 160 * 1024;    // X slice bytes per workgroup
 
 template <int STORAGE, int MB, int NCHK>
-__global__ __launch_bounds__(64 * SK_WAVES) void smallm_splitk_kernel(SmallMParams p, float* part, int rgroups) {
+__global__ __launch_bounds__(64 * SK_RWAVES * sk_khalves<NCHK>()) void smallm_splitk_kernel(SmallMParams p, float* part,
+                                                                                           int rgroups) {
   constexpr int WORDS = SmallMChunk<STORAGE>::WORDS;
   constexpr int QBITS = STORAGE == ANIMA_STORAGE_W4 ? 4 : 8;
+  constexpr int KH = sk_khalves<NCHK>();      // waves per row block
+  constexpr int NT = 64 * SK_RWAVES * KH;     // threads
+  constexpr int CPW = NCHK / KH;              // chunks per wave
   constexpr int KS = NCHK * SM_CHUNK;         // K of the slice
   constexpr int XROW = KS + 8;                // padded LDS row (halfs)
   constexpr int XCH = KS / 8;                 // 16-byte chunks per X row
+  static_assert(NCHK % KH == 0 && SK_RWAVES * MB * 64 * 16 <= 16 * MB * XROW * 2, "K halves and their LDS sums fit");
   __shared__ __attribute__((aligned(16))) half_t xs[16 * MB * XROW];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rw = wave % SK_RWAVES, kh = wave / SK_RWAVES;
   const int r = lane & 15, g = lane >> 4;
   const int rg = blockIdx.x % rgroups, slice = blockIdx.x / rgroups;
   const int k0 = slice * KS;
-  const int nb = rg * SK_ROWS + wave * 16;    // first weight row of this wave
+  const int nb = rg * SK_ROWS + rw * 16;      // first weight row of this wave
   // Rows past N re-read row N-1 (computed, never stored).
   const int n = min(nb + r, p.N - 1);
   const uint8_t* wrow = p.w + (int64_t)n * p.row_stride;
 
-  uint32_t wv[NCHK][WORDS];
-  half_t sc[NCHK], zc[NCHK];
+  uint32_t wv[CPW][WORDS];
+  half_t sc[CPW], zc[CPW];
 #pragma unroll
-  for (int c = 0; c < NCHK; ++c) {
-    const int kl = k0 + c * SM_CHUNK + 32 * g;
+  for (int c = 0; c < CPW; ++c) {
+    const int kl = k0 + (kh * CPW + c) * SM_CHUNK + 32 * g;
     const int64_t boff = STORAGE == ANIMA_STORAGE_W4 ? kl / 2 : kl;
     const u32x4* src = reinterpret_cast<const u32x4*>(wrow + boff);
 #pragma unroll
@@ -562,21 +573,21 @@ __global__ __launch_bounds__(64 * SK_WAVES) void smallm_splitk_kernel(SmallMPara
   }
   // The slice of X, 16 loads per thread in flight at a time.  Rows M .. 16 MB - 1 copy
   // row M - 1: they only feed output columns m >= M, which are never stored.
-  constexpr int PER = 16 * MB * XCH / (64 * SK_WAVES);
+  constexpr int PER = 16 * MB * XCH / NT;
   constexpr int BATCH = PER <= 16 ? PER : (PER % 16 == 0 ? 16 : (PER % 12 == 0 ? 12 : 8));
-  static_assert(PER * 64 * SK_WAVES == 16 * MB * XCH && PER % BATCH == 0, "X copy splits evenly");
+  static_assert(PER * NT == 16 * MB * XCH && PER % BATCH == 0, "X copy splits evenly");
 #pragma unroll
   for (int b0 = 0; b0 < PER; b0 += BATCH) {
     u32x4 v[BATCH];
 #pragma unroll
     for (int j = 0; j < BATCH; ++j) {
-      const int i = threadIdx.x + (b0 + j) * 64 * SK_WAVES;
+      const int i = threadIdx.x + (b0 + j) * NT;
       const int m = min(i / XCH, p.M - 1), ch = i % XCH;
       v[j] = *reinterpret_cast<const u32x4*>(p.x + (int64_t)m * p.K + k0 + ch * 8);
     }
 #pragma unroll
     for (int j = 0; j < BATCH; ++j) {
-      const int i = threadIdx.x + (b0 + j) * 64 * SK_WAVES;
+      const int i = threadIdx.x + (b0 + j) * NT;
       *reinterpret_cast<u32x4*>(xs + (i / XCH) * XROW + (i % XCH) * 8) = v[j];
     }
   }
@@ -586,7 +597,8 @@ __global__ __launch_bounds__(64 * SK_WAVES) void smallm_splitk_kernel(SmallMPara
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = floatx4{};
 #pragma unroll
-  for (int c = 0; c < NCHK; ++c) {
+  for (int c = 0; c < CPW; ++c) {
+    const int kc = (kh * CPW + c) * SM_CHUNK;   // chunk start within the slice
     const bool fast = __all(one_rounding_exact<QBITS>(sc[c], zc[c]));
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -594,10 +606,24 @@ __global__ __launch_bounds__(64 * SK_WAVES) void smallm_splitk_kernel(SmallMPara
                             : dequant_frag<STORAGE, false>(wv[c], t, sc[c], zc[c]);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        const half8v b = *reinterpret_cast<const half8v*>(xs + (mb * 16 + r) * XROW + c * SM_CHUNK + 32 * g + 8 * t);
+        const half8v b = *reinterpret_cast<const half8v*>(xs + (mb * 16 + r) * XROW + kc + 32 * g + 8 * t);
         acc[mb] = mfma16(a, b, acc[mb]);
       }
     }
+  }
+  if constexpr (KH == 2) {
+    // The second half's sums go to LDS over the X slice (once every wave is past its
+    // reads) and the first half adds them: first half + second half, a fixed order.
+    __syncthreads();
+    floatx4* red = reinterpret_cast<floatx4*>(xs);
+    if (kh == 1) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) red[(rw * MB + mb) * 64 + lane] = acc[mb];
+    }
+    __syncthreads();
+    if (kh == 1) return;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] += red[(rw * MB + mb) * 64 + lane];
   }
 
   const int nc = nb + 4 * g;                  // this lane's first output column
@@ -657,7 +683,7 @@ int smallm_splitk_slices(const GemmParams& p, int storage) {
 template <int STORAGE, int MB, int NCHK>
 static void launch_splitk_t(const SmallMParams& sp, float* part, int rgroups, int slices, hipStream_t stream) {
   hipLaunchKernelGGL((smallm_splitk_kernel<STORAGE, MB, NCHK>), dim3((unsigned)(rgroups * slices)),
-                     dim3(64 * SK_WAVES), 0, stream, sp, part, rgroups);
+                     dim3(64 * SK_RWAVES * sk_khalves<NCHK>()), 0, stream, sp, part, rgroups);
 }
 
 template <int STORAGE, int MB>
