@@ -576,8 +576,17 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i0 >= count) return;
   if (vec && i0 + 4 <= count) {
-    floatx4 acc = *reinterpret_cast<const floatx4*>(part + i0);
-    for (int s = 1; s < ksplit; ++s) acc += *reinterpret_cast<const floatx4*>(part + s * count + i0);
+    // Eight splits' loads go out together (indices past the last split re-read it and
+    // add -0, the identity of fp32 addition even for a -0 sum), then the adds run in
+    // split order: one memory round trip per eight splits instead of one per split.
+    floatx4 acc = floatx4{-0.f, -0.f, -0.f, -0.f};
+    for (int s0 = 0; s0 < ksplit; s0 += 8) {
+      floatx4 b[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) b[j] = *reinterpret_cast<const floatx4*>(part + min(s0 + j, ksplit - 1) * count + i0);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc += s0 + j < ksplit ? b[j] : floatx4{-0.f, -0.f, -0.f, -0.f};
+    }
     const half4v h = {(half_t)acc[0], (half_t)acc[1], (half_t)acc[2], (half_t)acc[3]};
     if (residual) {
       floatx4 r = *reinterpret_cast<const floatx4*>(residual + i0);
