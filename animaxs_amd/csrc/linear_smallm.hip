@@ -657,9 +657,13 @@ __global__ __launch_bounds__(64 * SK_RWAVES * sk_khalves<NCHK>()) void smallm_sp
 int smallm_splitk_slices(const GemmParams& p, int storage) {
   if (storage != ANIMA_STORAGE_W4 && storage != ANIMA_STORAGE_W8) return 0;
   if (p.epilogue != GEMM_STORE) return 0;
-  // With up to 32 input rows, or N wide enough for the weight-streaming kernel to give
-  // 256 workgroups of 32 rows, that kernel is faster (it needs no partial rows).
-  if (p.M <= 32 || p.N >= 32 * 256) return 0;
+  // With N wide enough for the weight-streaming kernel to give 256 workgroups of 32
+  // rows, that kernel is faster (it needs no partial rows); so it is with up to 32
+  // input rows while X is under 256 KB.  Past that, each of its workgroups reading all
+  // of X (about 0.044 us per KB at 16-row blocks) costs more than the partial rows:
+  // M=32 N=2048 K=4096 13.3 -> 8.5 us, M=16 K=8192 13.2 -> 10.9 us, M=8 K=16384
+  // 17.4 -> 14.9 us; M=16 K=4096 ties and M=32 N=4096 K=2048 is 5 % slower split.
+  if (p.N >= 32 * 256 || (p.M <= 32 && (int64_t)p.M * p.K < 131072)) return 0;
   if (p.M < 1 || p.M > SMALLM_MAX_ROWS || p.K % SM_CHUNK != 0 || !aligned16(p.x) || !aligned16(p.w) ||
       p.row_stride % 16 != 0)
     return 0;
