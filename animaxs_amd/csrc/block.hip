@@ -61,12 +61,30 @@ __global__ __launch_bounds__(256) void layernorm_modulate_wave_kernel(const floa
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const float* x = residual + (int64_t)row * n;
+  const float* scale = mod + mod_offset;
+  const float* shift = mod;
   floatx4 v[V];
-  float s = 0.f;
 #pragma unroll
   for (int e = 0; e < V; ++e) {
     const int c = 4 * (lane + 64 * e);
     v[e] = c < n ? *reinterpret_cast<const floatx4*>(x + c) : floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  // Up to 2048 columns the modulation rows go out right behind the row, so their round
+  // trip overlaps the row's instead of following the two reductions (wider rows load
+  // them at the end, within the registers that keep four waves per SIMD).
+  constexpr bool PRE = V <= 8;
+  floatx4 sc[PRE ? V : 1], sh[PRE ? V : 1];
+  if constexpr (PRE) {
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const int c = 4 * (lane + 64 * e);
+      sc[e] = c < n ? *reinterpret_cast<const floatx4*>(scale + c) : floatx4{0.f, 0.f, 0.f, 0.f};
+      sh[e] = c < n ? *reinterpret_cast<const floatx4*>(shift + c) : floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
     if (HB) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) v[e][u] = (float)(half_t)v[e][u];
@@ -87,21 +105,19 @@ __global__ __launch_bounds__(256) void layernorm_modulate_wave_kernel(const floa
     }
   }
   const float inv = rsqrtf(wave_sum(sq) / (float)n + eps);
-  const float* scale = mod + mod_offset;
-  const float* shift = mod;
   half_t* o = out + (int64_t)row * n;
 #pragma unroll
   for (int e = 0; e < V; ++e) {
     const int c = 4 * (lane + 64 * e);
     if (c < n) {
-      const floatx4 sc = *reinterpret_cast<const floatx4*>(scale + c);
-      const floatx4 sh = *reinterpret_cast<const floatx4*>(shift + c);
+      const floatx4 sce = PRE ? sc[PRE ? e : 0] : *reinterpret_cast<const floatx4*>(scale + c);
+      const floatx4 she = PRE ? sh[PRE ? e : 0] : *reinterpret_cast<const floatx4*>(shift + c);
       half4v h;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         float nv = (v[e][u] - mean) * inv;
         if (HB) nv = (float)f32_to_f16(nv);
-        h[u] = f32_to_f16(nv * (1.0f + sc[u]) + sh[u]);
+        h[u] = f32_to_f16(nv * (1.0f + sce[u]) + she[u]);
       }
       *reinterpret_cast<half4v*>(o + c) = h;
     }
