@@ -533,9 +533,20 @@ __global__ __launch_bounds__(PRO_D128_THREADS) void qk_prologue_d128_kernel(Prol
       c[j][i] = (float)xc[i];
     }
   }
+  // The norm weight and the table row go out with the rows (one memory round trip for
+  // the thread, not one for the rows and another for the table after the norm).
+  half8v wa{}, wc{};
   if (p.norm_w) {
-    const half8v wa = *reinterpret_cast<const half8v*>(p.norm_w + 8 * sub);
-    const half8v wc = *reinterpret_cast<const half8v*>(p.norm_w + 64 + 8 * sub);
+    wa = *reinterpret_cast<const half8v*>(p.norm_w + 8 * sub);
+    wc = *reinterpret_cast<const half8v*>(p.norm_w + 64 + 8 * sub);
+  }
+  floatx4 rrow[8];
+  if (p.rope) {
+    const floatx4* blk = reinterpret_cast<const floatx4*>(p.rope + (t * 64 + 8 * sub) * 4);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rrow[i] = blk[i];
+  }
+  if (p.norm_w) {
 #pragma unroll
     for (int j = 0; j < HPT; ++j) {
       float ss = 0.f;
@@ -553,10 +564,9 @@ __global__ __launch_bounds__(PRO_D128_THREADS) void qk_prologue_d128_kernel(Prol
     }
   }
   if (p.rope) {
-    const floatx4* blk = reinterpret_cast<const floatx4*>(p.rope + (t * 64 + 8 * sub) * 4);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const floatx4 r = blk[i];
+      const floatx4 r = rrow[i];
 #pragma unroll
       for (int j = 0; j < HPT; ++j) {
         const float ra = r[0] * a[j][i] + r[1] * c[j][i];
