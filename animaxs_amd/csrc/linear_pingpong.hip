@@ -45,6 +45,7 @@ namespace anima {
 constexpr int PG_BM = 128;                  // output rows (M) per workgroup
 constexpr int PG_BN = 256;                  // output columns (N) per workgroup: 4 waves x 64
 constexpr int PG_BK = 64;                   // K per block: one quantisation group
+constexpr int PG_GM = 4;                    // M blocks per tile group (tile order)
 constexpr int PG_NT = 512;                  // two groups of 4 waves
 constexpr int PG_XROW = PG_BK + 8;          // padded X row in LDS (halfs)
 constexpr int PG_XSTAGE = PG_BM * PG_XROW * 2;   // bytes per X stage (one per group)
@@ -100,7 +101,15 @@ void pingpong_gemm_kernel(GemmGroup gp) {
   const int ks = p.ksplit > 1 ? p.ksplit : 1;
   const int split = lb % ks;
   const int lt = lb / ks;
-  const int tn = lt % ntn, tm = lt / ntn;
+  // Tiles go in groups of PG_GM M blocks x all N tiles, M varying fastest: the 32
+  // consecutive tiles an XCD runs in one round are 4 M blocks x 8 N tiles, so each weight
+  // tile it loads serves four workgroups from its L2 (N varying fastest, a round of a wide
+  // GEMM took one M block x 32 N tiles and streamed the whole weight into every XCD).
+  const int ntm = (p.M + PG_BM - 1) / PG_BM;
+  const int gfirst = (lt / (PG_GM * ntn)) * PG_GM;
+  const int gm = ntm - gfirst < PG_GM ? ntm - gfirst : PG_GM;
+  const int gr = lt % (PG_GM * ntn);
+  const int tm = gfirst + gr % gm, tn = gr / gm;
   const int m0 = tm * PG_BM, n0 = tn * PG_BN;
   const int nk = p.K / PG_BK / ks;
   const int kbeg = split * nk;
