@@ -18,6 +18,8 @@ struct FlashParams {
   int64_t o_tok, o_head, o_batch;
   int Sq, Sk, H, group;
   int q_tiles;
+  int head_group;                  // 256-row kernel: heads one query tile takes on consecutive
+                                   // workgroups (set by launch_flash_v2)
   float scale_log2;                // scale * log2(e)
   float scale;                     // the softmax scale itself (MPS-rounding kernel)
   int causal;

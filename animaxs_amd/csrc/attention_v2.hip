@@ -111,12 +111,18 @@ void flash_attention_v2_kernel(FlashParams p) {
     split = lb % p.kv_splits;
     lb /= p.kv_splits;
   }
-  // Heads vary slowest: the XCD that owns a range of logical blocks gets whole heads
-  // (their K/V stay in its L2) over every batch entry, so batches of different key
-  // lengths spread evenly over the XCDs.
+  // Consecutive logical blocks share an XCD (and its L2).  They take p.head_group heads of
+  // one query tile, then the next query tile, and the remaining heads vary slowest.  With
+  // head_group 1 an XCD gets whole heads (their K/V stay in its L2) over every batch entry,
+  // so batches of different key lengths spread evenly over the XCDs; with 8 (single-image
+  // launches that fill the chip) an XCD's reads spread over 8 heads' pieces of each token
+  // row and it needs fewer of the RoPE table rows.
+  const int hgp = PERSIST ? 1 : p.head_group;   // the persistent form keeps whole heads per XCD
+  const int hl = lb % hgp;
+  lb /= hgp;
   const int qt = lb % p.q_tiles;
   lb /= p.q_tiles;
-  const int head = PERSIST ? lb : lb / p.nbatch;
+  const int head = (PERSIST ? lb : lb / p.nbatch) * hgp + hl;
   // PERSIST: the workgroups of head h start at entry h % nbatch and wrap around, so at any
   // time the heads are spread over the entries (of different key lengths) and their Q-row
   // loads and O-row stores do not all fall at the same moment.
@@ -698,11 +704,24 @@ void launch_flash_combine(const FlashParams& p, int D, int batch, hipStream_t st
   ANIMA_HIP(hipGetLastError());
 }
 
-void launch_flash_v2(const FlashParams& p, int D, dim3 grid, hipStream_t stream, bool persist) {
+// Heads of one query tile on consecutive workgroups (the kernel's block order): 8 for
+// single-image launches of at least 128 workgroups whose head count 8 divides, else 1.
+// Measured against 1 (A/B of library builds, medians of 3 rounds): S=4096 self-attention
+// with Q/K norm and RoPE 138.2 -> 137.1 us, S=1024 self-attention on two key splits 24.6
+// -> 23.7 us; 4 heads gave 137.0 and 24.9 us, 16 heads 138.0 and 23.7 us; the adapter
+// attention (32 workgroups) went from 19.35 to 19.6 us with 8, so small grids keep 1.
+static int flash_v2_head_group(const FlashParams& p, int64_t blocks, bool persist) {
+  if (persist || p.nbatch != 1 || p.H % 8 != 0 || blocks < 128) return 1;
+  return 8;
+}
+
+void launch_flash_v2(const FlashParams& p_in, int D, dim3 grid, hipStream_t stream, bool persist) {
+  FlashParams p = p_in;
+  p.head_group = flash_v2_head_group(p, grid.x, persist);
   // The kernel decodes blockIdx into (split, query tile, batch, head) with these counts
   // (persistent: (query tile, head), batch entries walked in the kernel): a grid of any
   // other size would address rows past the tensors.
-  if (p.nbatch < 1 || p.q_tiles < 1 || p.H < 1 ||
+  if (p.nbatch < 1 || p.q_tiles < 1 || p.H < 1 || p.H % p.head_group != 0 ||
       (int64_t)grid.x != (int64_t)p.q_tiles * p.H * (persist ? 1 : p.nbatch) * (p.kv_splits > 1 ? p.kv_splits : 1))
     fail(ANIMA_E_INVALID_ARGUMENT, "flash attention grid does not match its tiles, heads and batch");
   if (persist && (p.rope || p.kv_splits > 1 || !flash_v2_persist_fits(p, D)))
