@@ -221,6 +221,27 @@ def test_flash_key_splits(ctx, D, B, Sq, Sk):
     assert_attention_close(o, ref, label=f"splits D{D} B{B} Sq{Sq} Sk{Sk}")
 
 
+@pytest.mark.parametrize("H,Sq,Sk,lengths,D", [
+    (24, 2048, 2048, None, 128),   # 8 query tiles x 24 heads x 2 key splits = 384 workgroups
+    (8, 4096, 600, [517], 128),    # host key length (no splits): 16 query tiles x 8 heads = 128
+    (16, 2048, 1024, None, 64),    # head_dim 64: 8 query tiles x 16 heads x 2 key splits = 256
+])
+def test_flash_head_grouped_block_order(ctx, H, Sq, Sk, lengths, D):
+    """Single-image launches of at least 128 workgroups whose head count 8 divides decode 8 heads
+    of one query tile on consecutive workgroups (three groups of 8 at H=24, the only group at H=8),
+    with and without key splits: every (query tile, head) is still computed exactly once."""
+    g = torch.Generator().manual_seed(H * Sq + Sk + D)
+    q = torch.randn(1, Sq, H, D, generator=g).half()
+    k = torch.randn(1, Sk, H, D, generator=g).half()
+    v = torch.randn(1, Sk, H, D, generator=g).half()
+    lens = None if lengths is None else np.array(lengths, dtype=np.int32)
+    print(f"HEADGROUP H={H} Sq={Sq} Sk={Sk} D={D} lengths={lengths}", flush=True)
+    o = _run(ctx, dev(q), dev(k), dev(v), layout=("tokenMajor", H * D), heads=H, Sq=Sq, Sk=Sk, D=D,
+             out_shape=(1, Sq, H, D), key_lengths=lens)
+    ref = oatt.sdpa(q, k, v, key_lengths=lengths)
+    assert_attention_close(o, ref, label=f"head-grouped H{H} Sq{Sq} Sk{Sk} D{D}")
+
+
 @pytest.mark.parametrize("B,H,Hkv,Sq,Sk,D,lengths,on_device,norm", [
     (3, 16, 16, 4000, 600, 128, [600, 1, 130], False, True),   # one-tile entry, partial query tile
     (2, 32, 8, 2048, 64, 64, None, False, True),               # head_dim 64, grouped K/V heads, one tile
