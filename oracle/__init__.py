@@ -4,7 +4,7 @@ TEST INFRASTRUCTURE ONLY.  This package restates the reference algorithms on
 the CPU (numpy for byte/integer arithmetic, torch-CPU fp32 for floating point)
 so the HIP library can be checked against them.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
-import it, and only as the checker: the product library (``animaxs_amd``)
+import it, and only to compare against: the product library (``animaxs_amd``)
 never imports, links or calls anything here, and has no CPU fallback.
 
 Every function cites the reference file:line it follows (paths relative to the
