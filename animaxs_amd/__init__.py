@@ -10,8 +10,8 @@ from .animapk import AnimapkExecutionRange, AnimapkFile, AnimapkTensor, DiTBlock
 from .executors import (  # noqa: F401
     AttentionExecutor, BlockOps, Context, CrossKVCache, DiTBlockExecutor, DiTFinalLayerExecutor,
     DiTPreparationExecutor, DitRoPE, EulerSampler, LatentOps, LinearExecutor, QKPrologue, QuantDecoders,
-    QuantizedLinearWeightBuffers, QwenLayerExecutor, WeightStreamer, as_buffer, qwen_rope, read_probe,
-    read_probe_sink_bytes,
+    NumericalMonitor, ProbeFlag, ProbeStats, QuantizedLinearWeightBuffers, QwenLayerExecutor, WeightStreamer,
+    as_buffer, qwen_rope, read_probe, read_probe_sink_bytes,
 )
 
 __all__ = [
@@ -19,5 +19,6 @@ __all__ = [
     "DiTBlockExecutor", "WeightStreamer", "DiTPreparationExecutor", "DiTFinalLayerExecutor", "EulerSampler",
     "LatentOps", "AnimapkFile", "AnimapkTensor", "AnimapkExecutionRange", "DiTBlockLocator",
     "DitRoPE", "LinearExecutor", "QKPrologue", "QuantDecoders", "QuantizedLinearWeightBuffers",
-    "QwenLayerExecutor", "as_buffer", "qwen_rope", "read_probe", "read_probe_sink_bytes",
+    "QwenLayerExecutor", "as_buffer", "qwen_rope", "read_probe", "read_probe_sink_bytes", "NumericalMonitor",
+    "ProbeStats", "ProbeFlag",
 ]

@@ -183,6 +183,8 @@ SIGNATURES = {
     "anima_dequant_to_half_encode": (_S, [_P, C.POINTER(QWeight), Buffer, _I64, _I64]),
     "anima_read_probe_encode": (_S, [_P, Buffer, _I64, _I64, Buffer]),
     "anima_read_probe_sink_bytes": (_I64, [_I64]),
+    "anima_numerics_probe_reset_encode": (_S, [_P, Buffer, _I32]),
+    "anima_numerics_probe_encode": (_S, [_P, Buffer, _I64, _I64, _I32, Buffer, _I32]),
     "anima_dequant_w4": (_S, [_P, _P, _P, _I64, _I64, _P]),
     "anima_dequant_w4_matrix": (_S, [_P, _P, _P, _I64, _I64, _I64, _P]),
     "anima_dequant_w8": (_S, [_P, _P, _P, _I64, _I64, _P]),

@@ -9,6 +9,7 @@
 #include "context.hpp"
 #include "dit_io.hpp"
 #include "linear.hpp"
+#include "numerics_probe.hpp"
 
 namespace anima {
 
@@ -239,6 +240,43 @@ anima_status anima_read_probe_encode(anima_ctx* ctx, anima_buffer src, int64_t s
 }
 
 int64_t anima_read_probe_sink_bytes(int64_t bytes) { return bytes > 0 ? read_probe_sink_bytes(bytes) : 0; }
+
+// ---------------------------------------------------------------- numerical-health probes
+
+anima_status anima_numerics_probe_reset_encode(anima_ctx* ctx, anima_buffer stats, int32_t slots) {
+  return guarded([&] {
+    require(ctx, "context");
+    if (slots < 0) fail(ANIMA_E_INVALID_SHAPE, "numerics probe: slots must be >= 0");
+    check_elementwise(stats, (int64_t)slots * ANIMA_PROBE_SLOT_UINTS, 4, "numerics probe stats");
+    if (((uintptr_t)stats.ptr & 3u) != 0) fail(ANIMA_E_MISALIGNED, "numerics probe: stats must be 4-byte aligned");
+    if (slots == 0) return;
+    DeviceGuard g(ctx);
+    launch_numerics_probe_reset(static_cast<uint32_t*>(stats.ptr), slots, ctx->stream);
+  });
+}
+
+anima_status anima_numerics_probe_encode(anima_ctx* ctx, anima_buffer values, int64_t offset, int64_t count,
+                                         int32_t dtype, anima_buffer stats, int32_t slot) {
+  return guarded([&] {
+    require(ctx, "context");
+    if (dtype != ANIMA_PROBE_F16 && dtype != ANIMA_PROBE_F32)
+      fail(ANIMA_E_INVALID_ARGUMENT, "numerics probe: dtype must be ANIMA_PROBE_F16 or ANIMA_PROBE_F32");
+    if (count < 0 || offset < 0) fail(ANIMA_E_INVALID_SHAPE, "numerics probe: count and offset must be >= 0");
+    if (count >= (int64_t)ANIMA_PROBE_NO_INDEX)
+      fail(ANIMA_E_INVALID_SHAPE, "numerics probe: count must be below 0xFFFFFFFF");
+    if (slot < 0) fail(ANIMA_E_INVALID_ARGUMENT, "numerics probe: slot must be >= 0");
+    const int64_t elem = dtype == ANIMA_PROBE_F16 ? 2 : 4;
+    check_elementwise(values, checked_end(offset, count, "numerics probe"), elem, "numerics probe values");
+    check_elementwise(stats, ((int64_t)slot + 1) * ANIMA_PROBE_SLOT_UINTS, 4, "numerics probe stats");
+    if (((uintptr_t)stats.ptr & 3u) != 0) fail(ANIMA_E_MISALIGNED, "numerics probe: stats must be 4-byte aligned");
+    if (((uintptr_t)values.ptr & (uintptr_t)(elem - 1)) != 0)
+      fail(ANIMA_E_MISALIGNED, "numerics probe: values must be aligned to their element size");
+    if (count == 0) return;
+    DeviceGuard g(ctx);
+    launch_numerics_probe(static_cast<const char*>(values.ptr) + offset * elem, count, dtype == ANIMA_PROBE_F16,
+                          static_cast<uint32_t*>(stats.ptr) + (int64_t)slot * ANIMA_PROBE_SLOT_UINTS, ctx->stream);
+  });
+}
 
 // ---------------------------------------------------------------- DiT block support kernels
 

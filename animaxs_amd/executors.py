@@ -38,7 +38,7 @@ __all__ = [
     "AnimaError", "Context", "AttentionExecutor", "LinearExecutor", "QuantizedLinearWeightBuffers",
     "QKPrologue", "QuantDecoders", "DitRoPE", "qwen_rope", "DiTBlockExecutor", "BlockOps", "as_buffer",
     "CrossKVCache", "WeightStreamer", "QwenLayerExecutor", "LatentOps", "EulerSampler", "DiTPreparationExecutor",
-    "DiTFinalLayerExecutor",
+    "DiTFinalLayerExecutor", "NumericalMonitor", "ProbeStats", "ProbeFlag",
 ]
 
 
@@ -408,6 +408,111 @@ def read_probe(context: Context, src, nbytes: int, sink, src_offset: int = 0) ->
     """A plain streaming read of ``nbytes`` of ``src`` (the measurement probe
     anima_read_probe_encode): the floor for a weight-streaming kernel of that byte count."""
     call("anima_read_probe_encode", context.handle, as_buffer(src), int(src_offset), int(nbytes), as_buffer(sink))
+
+
+class ProbeFlag:
+    """Flag bits of a probe slot (NumericalMonitor.Flag, NumericalMonitor.swift:163-170).
+    The standalone passes set the first four; the last two belong to the reference's
+    in-kernel gate-add probe and are decoded for completeness."""
+    NAN = 1
+    POS_INF = 2
+    NEG_INF = 4
+    HALF_OVERFLOW = 8
+    RESULT_NAN = 16
+    RESULT_INF = 32
+
+
+PROBE_NO_INDEX = 0xFFFFFFFF
+
+
+@dataclass(frozen=True)
+class ProbeStats:
+    """One slot of the stats buffer (NumericalMonitor.Stats, NumericalMonitor.swift:136-161):
+    words [flags, max |v| as fp32 bits, first offending index, reserved]."""
+
+    flags: int = 0
+    max_abs: float = 0.0
+    first_index: int = PROBE_NO_INDEX
+
+    @classmethod
+    def from_words(cls, words) -> "ProbeStats":
+        w = np.asarray(words, dtype=np.int64).astype(np.uint32)
+        return cls(int(w[0]), float(w[1:2].view(np.float32)[0]), int(w[2]))
+
+    has_issue = property(lambda self: self.flags != 0)
+    has_nan = property(lambda self: bool(self.flags & ProbeFlag.NAN))
+    has_pos_inf = property(lambda self: bool(self.flags & ProbeFlag.POS_INF))
+    has_neg_inf = property(lambda self: bool(self.flags & ProbeFlag.NEG_INF))
+    has_half_overflow = property(lambda self: bool(self.flags & ProbeFlag.HALF_OVERFLOW))
+    result_nan = property(lambda self: bool(self.flags & ProbeFlag.RESULT_NAN))
+    result_inf = property(lambda self: bool(self.flags & ProbeFlag.RESULT_INF))
+
+    @property
+    def condition(self) -> str:
+        """The reference's short condition text, in its priority order."""
+        if self.has_nan:
+            return "NaN detected"
+        if self.has_pos_inf:
+            return "positive Inf detected"
+        if self.has_neg_inf:
+            return "negative Inf detected"
+        if self.result_nan:
+            return "residual became NaN"
+        if self.result_inf:
+            return "residual became non-finite"
+        if self.has_half_overflow:
+            return "value exceeded FP16 finite range"
+        return "non-finite value detected"
+
+
+class NumericalMonitor:
+    """The device side of NumericalMonitor (NumericalMonitor.swift:186-212, 320-358): a
+    stats buffer of one uint32 quad per probe slot, reset by ``begin_run`` and filled by
+    standalone passes over fp16 / fp32 buffers (anima_numerics_probe_encode), all on the
+    context's stream.  ``stats(slot)`` synchronises and decodes a slot.  Slot numbers are
+    the caller's (the reference numbers its probes in execution order, ``Probe`` below)."""
+
+    # Probe slots in the reference's execution order (NumericalMonitor.swift:21-53).
+    PROBES = ("crossContextToHalf", "patchesToHalf", "selfProjectionInput", "selfQToken", "selfKToken",
+              "selfVToken", "selfScores", "selfAttended", "selfBranch", "selfGateAdd", "selfResidual",
+              "crossProjectionInput", "crossQToken", "crossKToken", "crossVToken", "crossScores",
+              "crossAttended", "crossBranch", "crossGateAdd", "crossResidual", "mlpProjectionInput",
+              "mlpHiddenToHalf", "mlpBranch", "mlpGateAdd", "mlpResidual", "finalResidualToHalf",
+              "finalNormalizedToHalf", "finalProjectionInput", "finalProjected", "velocity", "denoised",
+              "eulerOutput")
+
+    def __init__(self, context: Context, slots: Optional[int] = None):
+        import torch
+        self.context = context
+        self.slots = len(self.PROBES) if slots is None else int(slots)
+        self.buffer = torch.zeros(self.slots * 4, dtype=torch.int32, device=f"cuda:{context.device}")
+        self.begin_run()
+
+    def slot(self, probe) -> int:
+        return self.PROBES.index(probe) if isinstance(probe, str) else int(probe)
+
+    def begin_run(self) -> None:
+        call("anima_numerics_probe_reset_encode", self.context.handle, as_buffer(self.buffer), self.slots)
+
+    def encode_probe(self, values, probe, count: Optional[int] = None, offset: int = 0) -> None:
+        """One pass over ``count`` values (fp16 or fp32 tensor; default: all after
+        ``offset``) into the probe's slot."""
+        import torch
+        if values.dtype == torch.float16:
+            dtype = 0
+        elif values.dtype == torch.float32:
+            dtype = 1
+        else:
+            raise TypeError("the probe reads fp16 or fp32 values")
+        n = values.numel() - int(offset) if count is None else int(count)
+        call("anima_numerics_probe_encode", self.context.handle, as_buffer(values), int(offset), n, dtype,
+             as_buffer(self.buffer), self.slot(probe))
+
+    def stats(self, probe) -> ProbeStats:
+        import torch
+        torch.cuda.synchronize(self.context.device)
+        s = self.slot(probe)
+        return ProbeStats.from_words(self.buffer[4 * s:4 * s + 4].cpu().numpy())
 
 
 def qwen_rope(tokens: int, head_dim: int = 128, theta: float = 1.0e6) -> np.ndarray:

@@ -706,6 +706,39 @@ anima_status anima_qwen_layer_destroy(anima_qwen_layer* layer);
 anima_status anima_qwen_layer_encode(anima_qwen_layer* layer, const anima_qwen_layer_weights* w,
                                      const anima_qwen_layer_args* args);
 
+/* ------------------------------------------------------------------------- */
+/* Numerical-health probes: NumericalMonitor (NumericalMonitor.swift:21-53,   */
+/* 136-170, 205-212, 320-358), the stats ABI of AnimaKernels.metal:1578-1600  */
+/* and the standalone passes probe_f16_stats / probe_f32_stats (:1921-2040).  */
+/* ------------------------------------------------------------------------- */
+/* stats holds one uint32 quad per slot: [0] flags (ANIMA_PROBE_FLAG_*), [1] max |v| over
+ * the finite values as fp32 bits (0 when there is none), [2] index of the first element
+ * that set a flag (ANIMA_PROBE_NO_INDEX when none did), [3] reserved.  A pass ORs its
+ * flags into [0] and takes the max of [1] and the min of [2] with relaxed atomics, so
+ * passes accumulate into a slot (also concurrently) until the slot is reset. */
+#define ANIMA_PROBE_SLOT_UINTS 4
+#define ANIMA_PROBE_FLAG_NAN 0x1u
+#define ANIMA_PROBE_FLAG_POS_INF 0x2u
+#define ANIMA_PROBE_FLAG_NEG_INF 0x4u
+#define ANIMA_PROBE_FLAG_HALF_OVERFLOW 0x8u   /* finite |v| > 65504 */
+#define ANIMA_PROBE_NO_INDEX 0xFFFFFFFFu
+
+typedef enum anima_probe_dtype {
+  ANIMA_PROBE_F16 = 0,  /* probe_f16_stats, NumericalMonitor.encodeProbe (:320-338) */
+  ANIMA_PROBE_F32 = 1   /* probe_f32_stats, NumericalMonitor.encodeProbeF32 (:340-358) */
+} anima_probe_dtype;
+
+/* beginRun (NumericalMonitor.swift:205-212): slots [0, slots) of stats (4-byte aligned,
+ * slots * 16 bytes) become 0, 0, ANIMA_PROBE_NO_INDEX, 0.  A kernel on the context's
+ * stream (no memset), so it may be recorded in a HIP graph. */
+anima_status anima_numerics_probe_reset_encode(anima_ctx* ctx, anima_buffer stats, int32_t slots);
+/* encodeProbe / encodeProbeF32 (NumericalMonitor.swift:320-358): one pass over `count`
+ * values of `dtype` starting `offset` elements into `values`, accumulated into slot
+ * `slot` of stats.  The first index counts from that start.  count 0 does nothing;
+ * count must be below ANIMA_PROBE_NO_INDEX (the index word). */
+anima_status anima_numerics_probe_encode(anima_ctx* ctx, anima_buffer values, int64_t offset, int64_t count,
+                                         int32_t dtype, anima_buffer stats, int32_t slot);
+
 #ifdef __cplusplus
 }
 #endif

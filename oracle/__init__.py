@@ -13,7 +13,7 @@ known answers, closed forms, brute force) is listed in ``PINNING`` below and
 exercised by ``tests/test_oracle_*.py``.
 """
 
-from . import quant, rope, norms, attention, inputs, blocks, dit_io  # noqa: F401
+from . import quant, rope, norms, attention, inputs, blocks, dit_io, probe  # noqa: F401
 
 # function -> the independent checks that pin it (see tests/test_oracle_*.py)
 PINNING = {
@@ -71,6 +71,12 @@ PINNING = {
         "distinct cross norm weights) that reject swapped shift/scale, another branch's gate, "
         "cross K/V from x, a missing Q or K RoPE, a Q or K normalised with the other's weight, "
         "a dropped cross Q or K norm, the self weights in the cross branch and RoPE on cross Q/K"),
+    "probe.probe_stats / accumulate": (
+        "known answers of AnimaXSTests/NumericalMonitorTests.swift:83-123 (float_to_half_probe "
+        "input: every flag, first index 2, max 70000) and :167-189 (fp16 NaN/+Inf first index 1; "
+        "fp32 -Inf and 80000 overflow, max 80000); closed forms (all finite: no flag, max of |v|; "
+        "65504 is not an overflow, its successor is; -0.0 counts as 0; an offender at index k "
+        "is first)"),
     "blocks.qwen_layer": (
         "composition following QwenEncoderMetal.swift:244-303 and "
         "scripts/qwen_comfy_oracle.py:268-300; zero-projection, causality, padding and "

@@ -57,7 +57,9 @@ def test_module_map_names_the_repository_header():
 def test_swift_wrappers_use_only_declared_symbols():
     header = _header_text()
     declared_fns = set(re.findall(r"\b(anima_[a-z0-9_]+)\s*\(", header))
+    # enum constants, and integer macros (Swift imports a literal #define as a constant)
     declared_consts = set(re.findall(r"\b(ANIMA_[A-Z0-9_]+)\s*=", header))
+    declared_consts |= set(re.findall(r"#define (ANIMA_[A-Z0-9_]+)\s+(?:0x[0-9A-Fa-f]+|[0-9]+)u?\s", header))
     declared_types = set(re.findall(r"typedef (?:struct|enum) (anima_[a-z0-9_]+)", header))
     swift = _swift_text()
     # calls and function references (an entry point passed as a closure) alike
