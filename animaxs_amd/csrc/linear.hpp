@@ -131,6 +131,10 @@ void launch_pingpong(const GemmParams& p, int storage, hipStream_t stream);
 int pingpong_ksplit(const GemmParams& p, int storage);
 // count (1..PG_GROUP) ping-pong GEMMs sharing K and storage in one launch.
 void launch_pingpong_group(const GemmParams* ps, int count, int storage, hipStream_t stream);
+// Whether a single launch of p runs the M-split form (256-row tiles, no K split between
+// the wave groups); its sums differ from the K-split form's in the last place, so a
+// grouped launch containing such a problem runs it on its own.
+bool pingpong_msplit(const GemmParams& p, int storage);
 
 // Weight-streaming GEMM for M <= SMALLM_MAX_ROWS (linear_smallm.hip); requires K a
 // multiple of 128 and 16-byte aligned X and weight rows.

@@ -57,6 +57,11 @@ constexpr int PG_WINOFF = 2 * PG_XSTAGE;    // windows: [group][buffer] after th
 static_assert(PG_WINOFF + 4 * PG_WINBUF <= PG_SMEM, "X stages and windows fit in the reduction area");
 constexpr int PG_OROW = PG_BN + 8;          // padded output-tile row in LDS (halfs)
 static_assert(PG_BM * PG_OROW * 2 <= PG_SMEM, "output tile fits in the reduction area");
+// M-split form (MSPLIT): 256-row tiles, the two groups on rows 0-127 and 128-255 over the
+// whole K range; its 256-row output tile needs more LDS than the reduction area.
+constexpr int PG_SMEM_M = 2 * PG_BM * PG_OROW * 2;
+static_assert(PG_SMEM_M >= PG_SMEM, "the M-split LDS area also holds the X stages and windows");
+constexpr int PG_GM_M = 4;                  // 256-row M blocks per tile group (M-split form)
 
 typedef __attribute__((address_space(3))) half8v lds_half8v;
 
@@ -70,7 +75,14 @@ typedef __attribute__((address_space(3))) half8v lds_half8v;
 // SWIN: the scale/zero rows are 16-byte aligned runs of 8 groups (groups % 8 == 0),
 // read 8 groups at a time per row into an LDS window instead of one 2-byte load per
 // row and block.
-template <int STORAGE, bool SWIN>
+// MSPLIT: the workgroup tile is 256 (M) x 256 (N) and the two wave groups split the rows
+// instead of the K range: group g computes rows 128g .. 128g+127 over every K block, so
+// there is no partial-sum exchange, and a launch has half the workgroups, each with the
+// first loads and output stage of one tile.  Every wave still owns 64 columns x 128 rows
+// and dequantises the same weights per MFMA as in the K-split form.  Only single plain
+// or fused-output launches without split K take it (pingpong_msplit); its sums run over
+// K in one order, so its bits differ from the K-split form's in the last place.
+template <int STORAGE, bool SWIN, bool MSPLIT>
 __global__ __launch_bounds__(PG_NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void pingpong_gemm_kernel(GemmGroup gp) {
   constexpr bool W4 = STORAGE == ANIMA_STORAGE_W4;
@@ -80,7 +92,9 @@ void pingpong_gemm_kernel(GemmGroup gp) {
   // X fragments read ahead of their MFMAs (W8's two weight blocks in flight leave
   // fewer registers).
   constexpr int PG_READ_AHEAD = W4 ? 3 : 2;
-  __shared__ __attribute__((aligned(1024))) char smem[PG_SMEM];
+  __shared__ __attribute__((aligned(1024))) char smem[MSPLIT ? PG_SMEM_M : PG_SMEM];
+  constexpr int BM = MSPLIT ? 2 * PG_BM : PG_BM;     // output rows per workgroup
+  constexpr int GM = MSPLIT ? PG_GM_M : PG_GM;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -105,25 +119,29 @@ void pingpong_gemm_kernel(GemmGroup gp) {
   // consecutive tiles an XCD runs in one round are 4 M blocks x 8 N tiles, so each weight
   // tile it loads serves four workgroups from its L2 (N varying fastest, a round of a wide
   // GEMM took one M block x 32 N tiles and streamed the whole weight into every XCD).
-  const int ntm = (p.M + PG_BM - 1) / PG_BM;
-  const int gfirst = (lt / (PG_GM * ntn)) * PG_GM;
-  const int gm = ntm - gfirst < PG_GM ? ntm - gfirst : PG_GM;
-  const int gr = lt % (PG_GM * ntn);
+  const int ntm = (p.M + BM - 1) / BM;
+  const int gfirst = (lt / (GM * ntn)) * GM;
+  const int gm = ntm - gfirst < GM ? ntm - gfirst : GM;
+  const int gr = lt % (GM * ntn);
   const int tm = gfirst + gr % gm, tn = gr / gm;
-  const int m0 = tm * PG_BM, n0 = tn * PG_BN;
+  const int m0 = tm * BM, n0 = tn * PG_BN;
   const int nk = p.K / PG_BK / ks;
   const int kbeg = split * nk;
   // Group 0 takes K blocks [0, half), group 1 [half, nk); with windows, half is a
   // multiple of the window so every window is aligned.
   int half = SWIN ? PG_WIN * ((nk + 2 * PG_WIN - 1) / (2 * PG_WIN)) : (nk + 1) / 2;
   half = half < nk ? half : nk;
-  const int kb0 = group == 0 ? 0 : half;
-  const int nown = group == 0 ? half : nk - half;
+  const int kb0 = MSPLIT || group == 0 ? 0 : half;
+  const int nown = MSPLIT ? nk : (group == 0 ? half : nk - half);
 
   // Tile-relative buffers (sizes fit in 31 bits; checked on the host).
   // With split K they start at the split's first K block; the sizes end where they did.
-  const half_t* xb = p.x + (int64_t)m0 * p.K + kbeg * PG_BK;
-  const int xbytes = (p.M - m0) * p.K * 2 - kbeg * PG_BK * 2;
+  // The group's X rows start at xr0 (M-split: its 128-row half of the tile, which can
+  // lie past M on the last tile row: then the descriptor is empty and reads zeros).
+  const int xr0 = m0 + (MSPLIT ? PG_BM * group : 0);
+  const half_t* xb = p.x + (int64_t)xr0 * p.K + kbeg * PG_BK;
+  const int xrem = (p.M - xr0) * p.K * 2 - kbeg * PG_BK * 2;
+  const int xbytes = xrem > 0 ? xrem : 0;
   const uint8_t* wb = p.w + (int64_t)n0 * p.row_stride + kbeg * 32 * WCH;
   const int wbytes = (int)((int64_t)(p.N - n0) * p.row_stride) - kbeg * 32 * WCH;
   const half_t* sb = p.scale + (int64_t)n0 * p.groups + kbeg;
@@ -391,7 +409,7 @@ void pingpong_gemm_kernel(GemmGroup gp) {
   wait_vmcnt_imm<0>();   // loads past the end
   // Same barrier count for both groups: group g passes 2 + g + 2*nown(g).
   {
-    const int bars0 = 2 + 2 * half, bars1 = 3 + 2 * (nk - half);
+    const int bars0 = 2 + 2 * (MSPLIT ? nk : half), bars1 = 3 + 2 * (MSPLIT ? nk : nk - half);
     const int mine = group == 0 ? bars0 : bars1;
     const int target = bars0 > bars1 ? bars0 : bars1;
     for (int i = mine; i < target; ++i) barrier();
@@ -467,11 +485,28 @@ void pingpong_gemm_kernel(GemmGroup gp) {
           *reinterpret_cast<half4v*>(tile + (32 * (MINE + j) + c32) * PG_OROW + 64 * wg + 32 * t + 8 * q + 4 * hh) =
               out[t][j][q];
   };
-  if (group == 0)
-    finish(std::integral_constant<int, 0>{});
-  else
-    finish(std::integral_constant<int, 2>{});
-  if (p.ksplit > 1) return;   // partial rows written; splitk_reduce_kernel finishes
+  if constexpr (MSPLIT) {
+    // Both groups are past their last K block (the barrier counts above match), so the
+    // X stages are free: each wave writes its rounded 64 x 128 sums straight into the
+    // group's half of the output tile.
+    half_t* tile = reinterpret_cast<half_t*>(smem);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<half4v*>(tile + (PG_BM * group + 32 * m + c32) * PG_OROW + 64 * wg + 32 * t + 8 * q +
+                                     4 * hh) =
+              half4v{(half_t)acc[t][m][4 * q], (half_t)acc[t][m][4 * q + 1], (half_t)acc[t][m][4 * q + 2],
+                     (half_t)acc[t][m][4 * q + 3]};
+  } else {
+    if (group == 0)
+      finish(std::integral_constant<int, 0>{});
+    else
+      finish(std::integral_constant<int, 2>{});
+    if (p.ksplit > 1) return;   // partial rows written; splitk_reduce_kernel finishes
+  }
   barrier();
 
   // Output stage: thread tid takes 16-byte chunk tid % 32 of tile rows tid / 32 + 16i.
@@ -481,7 +516,7 @@ void pingpong_gemm_kernel(GemmGroup gp) {
   auto store_tile = [&](auto epi_c) __attribute__((always_inline)) {
     constexpr int EPI = decltype(epi_c)::value;
 #pragma unroll 2
-    for (int i = 0; i < PG_BM / 16; ++i) {
+    for (int i = 0; i < BM / 16; ++i) {
       const int r = orow + 16 * i, m = m0 + r;
       half8v v = *reinterpret_cast<const half8v*>(tile + r * PG_OROW + 8 * ochunk);
       if (m >= p.M) continue;
@@ -631,11 +666,31 @@ int pingpong_ksplit(const GemmParams& p, int storage) {
   return best;
 }
 
+// A single launch of p takes the M-split form when its 256-row tiles still fill at least
+// two whole rounds of the chip (512 workgroups): it then pays half as many first loads
+// and output stages per output, and no partial-sum exchange.  Fewer tiles would leave
+// CUs idle that the 128-row form fills.  Split-K launches keep the K-split form.
+bool pingpong_msplit(const GemmParams& p, int storage) {
+  if (!pingpong_supported(p, storage) || pingpong_ksplit(p, storage) > 1) return false;
+  const int64_t wide = (int64_t)((p.M + 2 * PG_BM - 1) / (2 * PG_BM)) * ((p.N + PG_BN - 1) / PG_BN);
+  return wide >= 512;
+}
+
+template <int STORAGE, bool SWIN>
+static void launch_pingpong_t(const GemmGroup& g, int64_t tiles, bool msplit, hipStream_t stream) {
+  if (msplit)
+    hipLaunchKernelGGL((pingpong_gemm_kernel<STORAGE, SWIN, true>), dim3((unsigned)tiles), dim3(PG_NT), 0, stream, g);
+  else
+    hipLaunchKernelGGL((pingpong_gemm_kernel<STORAGE, SWIN, false>), dim3((unsigned)tiles), dim3(PG_NT), 0, stream, g);
+}
+
 void launch_pingpong_group(const GemmParams* ps, int count, int storage, hipStream_t stream) {
   if (count < 1 || count > PG_GROUP) fail(ANIMA_E_INVALID_ARGUMENT, "ping-pong GEMM group holds 1 to 3 problems");
   GemmGroup g{};
   bool swin = true;
   int64_t tiles = 0;
+  const bool msplit = count == 1 && pingpong_msplit(ps[0], storage);
+  const int bm = msplit ? 2 * PG_BM : PG_BM;
   for (int i = 0; i < count; ++i) {
     const GemmParams& p = ps[i];
     if (!pingpong_supported(p, storage)) fail(ANIMA_E_INVALID_SHAPE, "ping-pong GEMM: unsupported shape or alignment");
@@ -657,23 +712,22 @@ void launch_pingpong_group(const GemmParams* ps, int count, int storage, hipStre
     g.vec[i] = p.epilogue == GEMM_GATE_ADD       ? (aligned16(p.residual) && aligned16(p.gate) && p.N % 8 == 0 ? 1 : 0)
                : p.epilogue == GEMM_RESIDUAL_ADD ? (aligned16(p.residual) && p.N % 8 == 0 ? 1 : 0)
                                                  : (aligned16(p.y) && p.N % 8 == 0 ? 1 : 0);
-    tiles += (int64_t)((p.M + PG_BM - 1) / PG_BM) * ((p.N + PG_BN - 1) / PG_BN) * (p.ksplit > 1 ? p.ksplit : 1);
+    tiles += (int64_t)((p.M + bm - 1) / bm) * ((p.N + PG_BN - 1) / PG_BN) * (p.ksplit > 1 ? p.ksplit : 1);
     if (tiles > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "GEMM grid too large");
   }
   for (int i = count; i < PG_GROUP; ++i) g.first_tile[i] = (int)tiles;
   g.count = count;
   if (tiles <= 0) return;
-  const dim3 grid((unsigned)tiles), block(PG_NT);
   if (storage == ANIMA_STORAGE_W4) {
     if (swin)
-      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W4, true>), grid, block, 0, stream, g);
+      launch_pingpong_t<ANIMA_STORAGE_W4, true>(g, tiles, msplit, stream);
     else
-      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W4, false>), grid, block, 0, stream, g);
+      launch_pingpong_t<ANIMA_STORAGE_W4, false>(g, tiles, msplit, stream);
   } else {
     if (swin)
-      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W8, true>), grid, block, 0, stream, g);
+      launch_pingpong_t<ANIMA_STORAGE_W8, true>(g, tiles, msplit, stream);
     else
-      hipLaunchKernelGGL((pingpong_gemm_kernel<ANIMA_STORAGE_W8, false>), grid, block, 0, stream, g);
+      launch_pingpong_t<ANIMA_STORAGE_W8, false>(g, tiles, msplit, stream);
   }
   ANIMA_HIP(hipGetLastError());
   if (count == 1 && ps[0].ksplit > 1) {

@@ -118,10 +118,14 @@ def test_w4_gemm_block_shapes(ctx, backend, M, N, K):
 
 @pytest.mark.parametrize("storage", [0, 1])
 @pytest.mark.parametrize("M,N,K", [(65, 256, 64), (130, 520, 320), (257, 1000, 448), (1000, 2056, 1024),
-                                   (200, 300, 512), (129, 768, 1536), (383, 520, 4608)])
+                                   (200, 300, 512), (129, 768, 1536), (383, 520, 4608),
+                                   (4196, 8192, 512), (4300, 8256, 1024), (4196, 8192, 576)])
 def test_tiled_gemm_ragged_shapes_and_both_dequant_roundings(ctx, storage, M, N, K):
     """The tiled GEMM for M > 64 with K a multiple of 64: partial row and column tiles, a
-    single K block, odd block counts (the workgroup's two K halves get unequal shares), and
+    single K block, odd block counts (the workgroup's two K halves get unequal shares), the
+    M-split form of wide launches (256-row tiles: M=4196 leaves the second 128-row half of the
+    last tile row wholly past M, M=4300 partly; N=8256 a 64-column last tile; K=576 has no
+    scale windows), and
     per-group scale/zero pairs chosen per 64-row block so that whole waves take the
     one-rounding packed dequant (symmetric or zero offset) or the fp32 fallback (offset 2^-14
     of the scale: q*s + z no longer exact in fp32)."""
@@ -406,7 +410,7 @@ def test_gemm_dequant_bit_exact_via_one_hot(ctx, storage, M):
 
 @pytest.mark.parametrize("storage,M,N,K", [(0, 256, 2048, 2048), (1, 130, 520, 320), (0, 257, 1000, 448),
                                            (1, 129, 770, 128), (0, 32, 512, 512), (2, 96, 256, 256),
-                                           (0, 100, 300, 200)])
+                                           (0, 100, 300, 200), (0, 4096, 8192, 256)])
 def test_linear_epilogues_equal_two_step(ctx, storage, M, N, K):
     """anima_linear_encode_epilogue: the tiled GEMM's fused GELU / gate-add output stage (M > 64,
     W4/W8, K a multiple of 64; N % 4 != 0 takes its element-wise stores) and the two-kernel
@@ -485,11 +489,13 @@ def test_matvec_vectorised_every_storage(ctx, storage, N, K, pad):
 
 @pytest.mark.parametrize("storage,M,Ns,K", [(0, 4096 + 40, (2048, 1024, 1024), 1024), (1, 130, (520, 256), 320),
                                             (0, 512, (2048, 2048), 1024), (0, 257, (1000, 300, 1030), 448),
-                                            (0, 48, (512, 256), 512), (1, 200, (256, 256), 200)])
+                                            (0, 48, (512, 256), 512), (1, 200, (256, 256), 200),
+                                            (0, 4096, (8192, 2048), 256)])
 def test_linear_group_equals_separate_encodes(ctx, storage, M, Ns, K):
     """anima_linear_encode_group: one ping-pong launch over 2-3 weights of different N (tile ->
     problem mapping, ragged M and N) gives the bits of separate encodes; groups the tiled GEMM
-    does not take (small M, K not a multiple of 64) fall back to separate encodes."""
+    does not take (small M, K not a multiple of 64) and groups with a member that its own
+    encode runs in the M-split form (M=4096 N=8192) fall back to separate encodes."""
     ws = [_affine_weight(storage, N, K, seed=N + K + i) for i, N in enumerate(Ns)]
     qws, keeps = zip(*[device_weight(w) for w in ws])
     x = dev(torch.randn(M, K, generator=torch.Generator().manual_seed(M + K)).half())
