@@ -705,13 +705,15 @@ void launch_flash_combine(const FlashParams& p, int D, int batch, hipStream_t st
 }
 
 // Heads of one query tile on consecutive workgroups (the kernel's block order): 8 for
-// single-image launches of at least 128 workgroups whose head count 8 divides, else 1.
-// Measured against 1 (A/B of library builds, medians of 3 rounds): S=4096 self-attention
-// with Q/K norm and RoPE 138.2 -> 137.1 us, S=1024 self-attention on two key splits 24.6
-// -> 23.7 us; 4 heads gave 137.0 and 24.9 us, 16 heads 138.0 and 23.7 us; the adapter
-// attention (32 workgroups) went from 19.35 to 19.6 us with 8, so small grids keep 1.
+// single-image launches of at least 128 workgroups over at least 1024 keys whose head
+// count 8 divides, else 1.  Measured against 1 (A/B of library builds, medians of 3-5
+// rounds): S=4096 self-attention with Q/K norm and RoPE 138.2 -> 137.1 us, S=1024
+// self-attention on two key splits 24.6 -> 23.7 us; 4 heads gave 137.0 and 24.9 us, 16
+// heads 138.0 and 23.7 us.  With few keys a head's K/V is best shared in one XCD's L2 by
+// many workgroups: the adapter attention (32 workgroups) went from 19.35 to 19.6 us with
+// 8, and the DiT block's cross attention (4096 queries over 512 keys) from 26.08 to 26.34.
 static int flash_v2_head_group(const FlashParams& p, int64_t blocks, bool persist) {
-  if (persist || p.nbatch != 1 || p.H % 8 != 0 || blocks < 128) return 1;
+  if (persist || p.nbatch != 1 || p.H % 8 != 0 || blocks < 128 || p.Sk < 1024) return 1;
   return 8;
 }
 

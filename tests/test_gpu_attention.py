@@ -223,12 +223,12 @@ def test_flash_key_splits(ctx, D, B, Sq, Sk):
 
 @pytest.mark.parametrize("H,Sq,Sk,lengths,D", [
     (24, 2048, 2048, None, 128),   # 8 query tiles x 24 heads x 2 key splits = 384 workgroups
-    (8, 4096, 600, [517], 128),    # host key length (no splits): 16 query tiles x 8 heads = 128
+    (8, 4096, 1200, [1117], 128),  # host key length (no splits): 16 query tiles x 8 heads = 128
     (16, 2048, 1024, None, 64),    # head_dim 64: 8 query tiles x 16 heads x 2 key splits = 256
 ])
 def test_flash_head_grouped_block_order(ctx, H, Sq, Sk, lengths, D):
-    """Single-image launches of at least 128 workgroups whose head count 8 divides decode 8 heads
-    of one query tile on consecutive workgroups (three groups of 8 at H=24, the only group at H=8),
+    """Single-image launches of at least 128 workgroups over at least 1024 keys whose head count
+    8 divides decode 8 heads of one query tile on consecutive workgroups (three groups of 8 at H=24, the only group at H=8),
     with and without key splits: every (query tile, head) is still computed exactly once."""
     g = torch.Generator().manual_seed(H * Sq + Sk + D)
     q = torch.randn(1, Sq, H, D, generator=g).half()
