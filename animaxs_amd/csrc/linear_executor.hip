@@ -138,10 +138,11 @@ bool LinearExecutor::encode_group(anima_buffer input, const anima_qweight* const
   for (int i = 0; i < count; ++i) {
     const QWeightView w = validate_weight(*weights[i], "LinearExecutor");
     ps[i] = prepare(input, 0, w, outputs[i], 0, input_rows);
-    // A weight encode() would split over K or run in the M-split form runs on its own, so
-    // the bits match encode().
+    // A weight encode() would split over K runs on its own, and so does, in a group of two
+    // or more, one encode() would run in the M-split form (a single launch takes that form
+    // itself), so the bits match encode().
     together = together && !smallm_supported(ps[i], w.storage) && pingpong_supported(ps[i], w.storage) &&
-               pingpong_ksplit(ps[i], w.storage) == 1 && !pingpong_msplit(ps[i], w.storage) &&
+               pingpong_ksplit(ps[i], w.storage) == 1 && (count == 1 || !pingpong_msplit(ps[i], w.storage)) &&
                (i == 0 || (w.storage == storage && ps[i].K == ps[0].K));
     storage = w.storage;
   }

@@ -515,10 +515,12 @@ def test_linear_group_equals_separate_encodes(ctx, storage, M, Ns, K):
 
 @pytest.mark.parametrize("storage,M,N,K,hd", [(0, 300, 384, 512, 128), (1, 1000, 2048, 1024, 128),
                                               (0, 4096 + 40, 2048, 2048, 128), (0, 48, 384, 512, 128),
-                                              (0, 300, 384, 512, 64), (2, 100, 256, 256, 128)])
+                                              (0, 300, 384, 512, 64), (2, 100, 256, 256, 128),
+                                              (0, 4096 + 40, 8192, 256, 128)])
 def test_linear_head_rmsnorm_matches_encode_then_norm(ctx, storage, M, N, K, hd):
     """anima_linear_encode_head_rmsnorm: the tiled GEMM's per-head RMSNorm output stage (M > 64,
-    W4/W8, head_dim 128; ragged M, N = 384 leaves a 256-column tile half used) and the in-place
+    W4/W8, head_dim 128; ragged M, N = 384 leaves a 256-column tile half used; N = 8192 runs the
+    M-split form's 256-row tiles) and the in-place
     second pass (small M, head_dim 64, fp16 storage) against plain encode followed by the oracle's
     per-head RMSNorm (rmsnorm_heads_half, AnimaKernels.metal:660-689) of those fp16 outputs: within
     one fp16 ulp (the sum of squares is reduced in another order)."""
