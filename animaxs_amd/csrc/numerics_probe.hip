@@ -135,8 +135,9 @@ __global__ __launch_bounds__(NP_THREADS) void numerics_probe_kernel(const T* v, 
 // Slot reset (the monitor's beginRun, NumericalMonitor.swift:205-212): flags, max and
 // the reserved word 0, first index 0xFFFFFFFF.  A kernel rather than a memset, so that
 // a caller may record it in a HIP graph.
-__global__ __launch_bounds__(NP_THREADS) void numerics_probe_reset_kernel(uint32_t* stats, uint32_t words) {
-  const uint32_t i = blockIdx.x * NP_THREADS + threadIdx.x;
+// 64-bit word indices: slots up to 2^31 - 1 make up to 2^33 words.
+__global__ __launch_bounds__(NP_THREADS) void numerics_probe_reset_kernel(uint32_t* stats, uint64_t words) {
+  const uint64_t i = (uint64_t)blockIdx.x * NP_THREADS + threadIdx.x;
   if (i < words) stats[i] = (i & 3u) == 2u ? NP_NONE : 0u;
 }
 
@@ -160,7 +161,7 @@ void launch_numerics_probe_reset(uint32_t* stats, int64_t slots, hipStream_t str
   const int64_t words = slots * NUMERICS_PROBE_SLOT_UINTS;
   const int64_t blocks = (words + NP_THREADS - 1) / NP_THREADS;
   hipLaunchKernelGGL(numerics_probe_reset_kernel, dim3((unsigned)blocks), dim3(NP_THREADS), 0, stream, stats,
-                     (uint32_t)words);
+                     (uint64_t)words);
   ANIMA_HIP(hipGetLastError());
 }
 
