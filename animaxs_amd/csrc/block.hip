@@ -7,8 +7,10 @@
 // DiTBlockExecutor.encodeAttentionBranch / encodeMLP / encodeModulation
 // (AnimaXS/Runtime/Metal/DiTBlockExecutor.swift:1035-1319, :1403-1417) with every
 // shape a parameter (the reference hard-wires 1024 tokens).
+#include <algorithm>
 #include <cmath>
 #include <string>
+#include <vector>
 
 #include "attention.hpp"
 #include "block.hpp"
@@ -494,6 +496,14 @@ static MatvecParams matvec_params(const anima_qweight& weight, const float* x, f
   return p;
 }
 
+static void modulation_params(const anima_qweight& w1, const anima_qweight& w2, const anima_dit_block_args& a,
+                              float* hid, float* mod, MatvecParams* mv1, MatvecParams* mv2) {
+  *mv1 = matvec_params(w1, static_cast<const float*>(a.emb.ptr), hid);
+  mv1->silu_input = 1;
+  *mv2 = matvec_params(w2, hid, mod);
+  mv2->bias = static_cast<const float*>(a.adaln_lora.ptr);
+}
+
 static void require_buffer(const anima_buffer& b, int64_t bytes, const char* what) {
   if (!b.ptr) fail(ANIMA_E_INVALID_ARGUMENT, std::string(what) + " pointer is null");
   if (b.length < bytes) fail(ANIMA_E_OUT_OF_BOUNDS, std::string(what) + " buffer range is out of bounds");
@@ -541,6 +551,17 @@ void DitBlockExecutor::check(const anima_dit_block_weights& w, const anima_dit_b
 void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_block_args& a, CrossKVCache* cache,
                               int64_t block_index) {
   check(w, a, cache, block_index);
+  encode_block(w, a, cache, block_index, nullptr, 0);
+}
+
+// Modulation matvecs of one branch (DiTBlockExecutor.encodeModulation, :1403-1417):
+// SiLU(emb) -> W1 -> hid, then hid -> W2 (+ adaln_lora) -> mod.
+static void modulation_params(const anima_qweight& w1, const anima_qweight& w2, const anima_dit_block_args& a,
+                              float* hid, float* mod, MatvecParams* mv1, MatvecParams* mv2);
+
+void DitBlockExecutor::encode_block(const anima_dit_block_weights& w, const anima_dit_block_args& a,
+                                    CrossKVCache* cache, int64_t block_index, const float* premod,
+                                    int64_t mod_stride) {
   const int64_t S = a.tokens, dim = a.dim, H = a.heads, hd = a.head_dim, T = a.context_tokens,
                 hidden = a.mlp_hidden;
   const int64_t lora = w.mod_self_w1.rows;
@@ -573,21 +594,24 @@ void DitBlockExecutor::encode(const anima_dit_block_weights& w, const anima_dit_
 
   // Modulation (DiTBlockExecutor.encodeModulation, :1403-1417): SiLU(emb) -> W1 -> W2 -> + adaln_lora,
   // for the three branches at once: one launch for the W1 matvecs (SiLU applied to emb as it is
-  // read), one for the W2 matvecs (adaln_lora added to each output).
+  // read), one for the W2 matvecs (adaln_lora added to each output).  A forward computes every
+  // block's rows up front instead (they depend on emb and adaln_lora alone).
   const anima_qweight* w1s[3] = {&w.mod_self_w1, &w.mod_cross_w1, &w.mod_mlp_w1};
   const anima_qweight* w2s[3] = {&w.mod_self_w2, &w.mod_cross_w2, &w.mod_mlp_w2};
-  float* mods[3];
-  MatvecParams mv1[3], mv2[3];
-  for (int br = 0; br < 3; ++br) {
-    mods[br] = reinterpret_cast<float*>(ws + o_mod + br * mod_bytes);
-    float* hid = reinterpret_cast<float*>(ws + o_hid + br * hid_bytes);
-    mv1[br] = matvec_params(*w1s[br], static_cast<const float*>(a.emb.ptr), hid);
-    mv1[br].silu_input = 1;
-    mv2[br] = matvec_params(*w2s[br], hid, mods[br]);
-    mv2[br].bias = static_cast<const float*>(a.adaln_lora.ptr);
+  const float* mods[3];
+  if (premod) {
+    for (int br = 0; br < 3; ++br) mods[br] = premod + br * mod_stride;
+  } else {
+    MatvecParams mv1[3], mv2[3];
+    for (int br = 0; br < 3; ++br) {
+      float* mod = reinterpret_cast<float*>(ws + o_mod + br * mod_bytes);
+      float* hid = reinterpret_cast<float*>(ws + o_hid + br * hid_bytes);
+      modulation_params(*w1s[br], *w2s[br], a, hid, mod, &mv1[br], &mv2[br]);
+      mods[br] = mod;
+    }
+    launch_matvec_batch(mv1, 3, stream);
+    launch_matvec_batch(mv2, 3, stream);
   }
-  launch_matvec_batch(mv1, 3, stream);
-  launch_matvec_batch(mv2, 3, stream);
 
   anima_attention_args att{};
   att.heads = H; att.head_dim = hd; att.key_value_heads = H; att.layout = ANIMA_LAYOUT_TOKEN_MAJOR;
@@ -655,7 +679,33 @@ void DitBlockExecutor::forward(const anima_dit_block_weights* blocks, int64_t co
   if (cache && cache->blocks() < count) fail(ANIMA_E_INVALID_SHAPE, "cross K/V cache holds fewer blocks than the forward");
   // Every block validates before the first launch.
   for (int64_t i = 0; i < count; ++i) check(blocks[i], a, cache, i);
-  for (int64_t i = 0; i < count; ++i) encode(blocks[i], a, cache, i);
+  // The modulation rows depend on emb and adaln_lora alone, so every block's are computed
+  // first, MV_BATCH_WIDE matvecs per launch (the same kernel and bits as a block's own
+  // 3-matvec launches), in place of two small launches per block.
+  const int64_t dim = a.dim;
+  auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
+  int64_t hid_bytes = 0;
+  for (int64_t i = 0; i < count; ++i) hid_bytes = std::max<int64_t>(hid_bytes, al(blocks[i].mod_self_w1.rows * 4));
+  const int64_t mod_bytes = al(3 * dim * 4), per_block = 3 * (hid_bytes + mod_bytes);
+  DeviceGuard guard(ctx_);
+  hipStream_t stream = ctx_->stream;
+  char* mws = static_cast<char*>(mod_ws_.get(checked_product({count, per_block}, "DiT forward"), stream));
+  std::vector<MatvecParams> mv1((size_t)(3 * count)), mv2((size_t)(3 * count));
+  for (int64_t i = 0; i < count; ++i) {
+    const anima_dit_block_weights& w = blocks[i];
+    const anima_qweight* w1s[3] = {&w.mod_self_w1, &w.mod_cross_w1, &w.mod_mlp_w1};
+    const anima_qweight* w2s[3] = {&w.mod_self_w2, &w.mod_cross_w2, &w.mod_mlp_w2};
+    for (int br = 0; br < 3; ++br) {
+      float* hid = reinterpret_cast<float*>(mws + i * per_block + br * hid_bytes);
+      float* mod = reinterpret_cast<float*>(mws + i * per_block + 3 * hid_bytes + br * mod_bytes);
+      modulation_params(*w1s[br], *w2s[br], a, hid, mod, &mv1[3 * i + br], &mv2[3 * i + br]);
+    }
+  }
+  launch_matvec_many(mv1.data(), 3 * count, stream);
+  launch_matvec_many(mv2.data(), 3 * count, stream);
+  for (int64_t i = 0; i < count; ++i)
+    encode_block(blocks[i], a, cache, i, reinterpret_cast<const float*>(mws + i * per_block + 3 * hid_bytes),
+                 mod_bytes / 4);
 }
 
 // Rebase one template buffer (ptr holds a byte offset into the block's range) onto

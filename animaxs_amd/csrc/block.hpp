@@ -104,10 +104,16 @@ class DitBlockExecutor {
                         CrossKVCache* cache);
 
  private:
+  // encode() with the block's three modulation rows ([3][3 * dim] fp32, branch stride
+  // mod_stride floats) already computed when premod is not null.
+  void encode_block(const anima_dit_block_weights& w, const anima_dit_block_args& a, CrossKVCache* cache,
+                    int64_t block_index, const float* premod, int64_t mod_stride);
+
   anima_ctx* ctx_;
   AttentionExecutor attention_;
   LinearExecutor linear_;
   Workspace ws_;
+  Workspace mod_ws_;   // the forward's modulation rows of every block
 };
 
 class QwenLayerExecutor {

@@ -8,6 +8,7 @@
 // (AnimaXS/Shaders/AnimaKernels.metal:19-79, 804-1047).  Weight value
 // v = fl32(q*scale + zero) (q*scale is exact, so one rounding), fp16 weight
 // RNE16(v): bit-identical to the reference's dequant_*_to_half.
+#include <algorithm>
 #include <string>
 
 #include "linear.hpp"
@@ -357,16 +358,21 @@ __device__ __forceinline__ float mv_finish(const MatvecParams& p, int row, float
   return p.bias ? sum + p.bias[row] : sum;
 }
 
-template <int STORAGE, int LPR>
-__global__ __launch_bounds__(256) void matvec_vec_kernel(MatvecBatch b) {
+template <int STORAGE, int LPR, int CAP>
+__global__ __launch_bounds__(256) void matvec_vec_kernel(MatvecBatchN<CAP> b) {
   constexpr int E = MvChunk<STORAGE>::elems, RPW = 64 / LPR;
   int bi = 0;
 #pragma unroll
-  for (int j = 1; j < MV_BATCH; ++j)
+  for (int j = 1; j < CAP; ++j)
     if (j < b.count && (int)blockIdx.x >= b.first_block[j]) bi = j;
-  MatvecParams p = b.p[0];
-  if (bi == 1) p = b.p[1];
-  if (bi == 2) p = b.p[2];
+  MatvecParams p;
+  if constexpr (CAP == MV_BATCH) {
+    p = b.p[0];
+    if (bi == 1) p = b.p[1];
+    if (bi == 2) p = b.p[2];
+  } else {
+    p = b.p[bi];   // bi is uniform over the workgroup: scalar loads at a computed offset
+  }
   const int lane = threadIdx.x & 63, sub = lane & (LPR - 1);
   const int row = ((int)blockIdx.x - b.first_block[bi]) * (4 * RPW) + (threadIdx.x >> 6) * RPW + lane / LPR;
   float sum = 0.f;
@@ -500,14 +506,38 @@ static int matvec_lanes(const MatvecParams& p) {
   return lpr;
 }
 
-template <int STORAGE>
-static void launch_matvec_vec(const MatvecBatch& b, int lpr, unsigned blocks, hipStream_t stream) {
+template <int STORAGE, int CAP>
+static void launch_matvec_vec(const MatvecBatchN<CAP>& b, int lpr, unsigned blocks, hipStream_t stream) {
   switch (lpr) {
-    case 8: hipLaunchKernelGGL((matvec_vec_kernel<STORAGE, 8>), dim3(blocks), dim3(256), 0, stream, b); break;
-    case 16: hipLaunchKernelGGL((matvec_vec_kernel<STORAGE, 16>), dim3(blocks), dim3(256), 0, stream, b); break;
-    case 32: hipLaunchKernelGGL((matvec_vec_kernel<STORAGE, 32>), dim3(blocks), dim3(256), 0, stream, b); break;
-    default: hipLaunchKernelGGL((matvec_vec_kernel<STORAGE, 64>), dim3(blocks), dim3(256), 0, stream, b); break;
+    case 8: hipLaunchKernelGGL((matvec_vec_kernel<STORAGE, 8, CAP>), dim3(blocks), dim3(256), 0, stream, b); break;
+    case 16: hipLaunchKernelGGL((matvec_vec_kernel<STORAGE, 16, CAP>), dim3(blocks), dim3(256), 0, stream, b); break;
+    case 32: hipLaunchKernelGGL((matvec_vec_kernel<STORAGE, 32, CAP>), dim3(blocks), dim3(256), 0, stream, b); break;
+    default: hipLaunchKernelGGL((matvec_vec_kernel<STORAGE, 64, CAP>), dim3(blocks), dim3(256), 0, stream, b); break;
   }
+}
+
+// One launch of count (1..CAP) matvecs that share storage and lane split lpr.
+template <int CAP>
+static void launch_matvec_together(const MatvecParams* ps, int count, int lpr, hipStream_t stream) {
+  MatvecBatchN<CAP> b{};
+  const int rows_per_block = 4 * (64 / lpr);
+  int64_t blocks = 0;
+  for (int i = 0; i < count; ++i) {
+    b.p[i] = ps[i];
+    b.first_block[i] = (int)blocks;
+    blocks += ps[i].N > 0 ? (ps[i].N + rows_per_block - 1) / rows_per_block : 0;
+    if (blocks > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "matvec grid too large");
+  }
+  for (int i = count; i < CAP; ++i) b.first_block[i] = (int)blocks;
+  b.count = count;
+  if (blocks <= 0) return;
+  if (ps[0].storage == ANIMA_STORAGE_W4)
+    launch_matvec_vec<ANIMA_STORAGE_W4>(b, lpr, (unsigned)blocks, stream);
+  else if (ps[0].storage == ANIMA_STORAGE_W8)
+    launch_matvec_vec<ANIMA_STORAGE_W8>(b, lpr, (unsigned)blocks, stream);
+  else
+    launch_matvec_vec<ANIMA_STORAGE_FP16>(b, lpr, (unsigned)blocks, stream);
+  ANIMA_HIP(hipGetLastError());
 }
 
 void launch_matvec_batch(const MatvecParams* ps, int count, hipStream_t stream) {
@@ -528,25 +558,24 @@ void launch_matvec_batch(const MatvecParams* ps, int count, hipStream_t stream) 
     }
     return;
   }
-  MatvecBatch b{};
-  const int rows_per_block = 4 * (64 / lpr);
-  int64_t blocks = 0;
-  for (int i = 0; i < count; ++i) {
-    b.p[i] = ps[i];
-    b.first_block[i] = (int)blocks;
-    blocks += ps[i].N > 0 ? (ps[i].N + rows_per_block - 1) / rows_per_block : 0;
+  launch_matvec_together<MV_BATCH>(ps, count, lpr, stream);
+}
+
+void launch_matvec_many(const MatvecParams* ps, int64_t count, hipStream_t stream) {
+  if (count <= 0) return;
+  const int lpr = matvec_lanes(ps[0]);
+  bool together = lpr != 0;
+  for (int64_t i = 1; i < count; ++i)
+    together = together && ps[i].storage == ps[0].storage && matvec_lanes(ps[i]) == lpr;
+  for (int64_t i = 0; i < count;) {
+    const int cap = together ? MV_BATCH_WIDE : MV_BATCH;
+    const int n = (int)std::min<int64_t>(cap, count - i);
+    if (together)
+      launch_matvec_together<MV_BATCH_WIDE>(ps + i, n, lpr, stream);
+    else
+      launch_matvec_batch(ps + i, n, stream);
+    i += n;
   }
-  for (int i = count; i < MV_BATCH; ++i) b.first_block[i] = (int)blocks;
-  b.count = count;
-  if (blocks <= 0) return;
-  if (blocks > 0x7fffffff) fail(ANIMA_E_INVALID_SHAPE, "matvec grid too large");
-  if (ps[0].storage == ANIMA_STORAGE_W4)
-    launch_matvec_vec<ANIMA_STORAGE_W4>(b, lpr, (unsigned)blocks, stream);
-  else if (ps[0].storage == ANIMA_STORAGE_W8)
-    launch_matvec_vec<ANIMA_STORAGE_W8>(b, lpr, (unsigned)blocks, stream);
-  else
-    launch_matvec_vec<ANIMA_STORAGE_FP16>(b, lpr, (unsigned)blocks, stream);
-  ANIMA_HIP(hipGetLastError());
 }
 
 void launch_matvec(const MatvecParams& p, hipStream_t stream) {

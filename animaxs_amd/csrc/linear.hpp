@@ -68,14 +68,19 @@ struct MatvecParams {
   const float* bias;      // optional [N]: y = sum + bias (add_f32 fused)
 };
 
-// Up to MV_BATCH independent matvecs in one launch; blocks [first_block[i],
+// Up to CAP independent matvecs in one launch; blocks [first_block[i],
 // first_block[i+1]) compute matvec i.
-constexpr int MV_BATCH = 3;
-struct MatvecBatch {
-  MatvecParams p[MV_BATCH];
-  int first_block[MV_BATCH];
+template <int CAP>
+struct MatvecBatchN {
+  MatvecParams p[CAP];
+  int first_block[CAP];
   int count;
 };
+constexpr int MV_BATCH = 3;
+using MatvecBatch = MatvecBatchN<MV_BATCH>;
+// Wide batches (about 2 KB of kernel arguments): the modulation matvecs of up to 8 DiT
+// blocks, 3 branches each, in one launch.
+constexpr int MV_BATCH_WIDE = 24;
 
 struct DequantParams {
   const uint8_t* w;
@@ -152,6 +157,9 @@ void launch_splitk_reduce(const float* part, half_t* y, int64_t count, int kspli
 void launch_matvec(const MatvecParams& p, hipStream_t stream);
 // count (1..MV_BATCH) matvecs; one launch when they share storage and lane split.
 void launch_matvec_batch(const MatvecParams* ps, int count, hipStream_t stream);
+// Any count of matvecs: one launch per MV_BATCH_WIDE of them when all share storage and
+// lane split, else launch_matvec_batch per MV_BATCH.  Same bits per matvec either way.
+void launch_matvec_many(const MatvecParams* ps, int64_t count, hipStream_t stream);
 void launch_dequant(const DequantParams& p, hipStream_t stream);
 // Plain streaming read of `bytes` (a multiple of 16, 16-byte aligned); one 16-byte word per
 // workgroup goes to sink (read_probe_sink_bytes(bytes) bytes).

@@ -127,6 +127,26 @@ def test_forward_equals_blocks_and_second_step_hits_cache(ctx):
     assert torch.equal(step2.view(torch.int32), step1.view(torch.int32))
 
 
+def test_forward_of_nine_blocks_equals_blocks(ctx):
+    """The forward computes every block's modulation rows before the first block, up to 24
+    matvecs per launch: 9 blocks make 27 matvecs per stage, so one launch of 24 and one of 3.
+    The rows, and so the output, keep the bits of the blocks encoded one by one."""
+    S, n = 256, 9
+    ds = _blocks(S, n)
+    dev_blocks = [_device_block(d) for d in ds]
+    sh = _shared(ds[0])
+    blk = DiTBlockExecutor(ctx)
+    print(f"FORWARD equals blocks S={S} blocks={n}", flush=True)
+    seq = dev(ds[0]["x"].clone())
+    for w, nm, _ in dev_blocks:
+        blk.encode(w, nm, seq, tokens=S, **sh)
+    fwd = dev(ds[0]["x"].clone())
+    blk.forward([(w, nm) for w, nm, _ in dev_blocks], fwd, tokens=S, **sh)
+    torch.cuda.synchronize()
+    assert torch.isfinite(fwd).all()
+    assert torch.equal(fwd.view(torch.int32), seq.view(torch.int32))
+
+
 # --------------------------------------------------------------------------------------
 # Streamed weights: every block's tensors packed into one contiguous host range (the pack's
 # execution range), with a template whose pointers are offsets into that range.
